@@ -1,0 +1,204 @@
+/*
+ * w4a8_moe.h - C ABI of the MI355X (gfx950) W4A8 MoE expert path.
+ *
+ * This is the boundary the torch-op layer (w4a8_fp8_wmma/_ops.py) binds through
+ * ctypes; any other host (C++, cgo, JNI) can bind the same symbols. Every entry point
+ * takes raw device pointers, sizes and a hipStream_t (passed as void*), enqueues its
+ * kernels on that stream without synchronising, and returns a status code. Nothing
+ * here allocates device memory: scratch is a caller-owned workspace whose size the
+ * matching *_workspace_size() function returns.
+ *
+ * The reference (patcarter883/rdna4-vllm) exposes this path as torch ops
+ * (w4a8_fp8_wmma/bindings.cpp:388-424) over host launchers
+ * (w4a8_fp8_wmma/moe_kernel.hip:1327-1464); each entry point below names the
+ * reference interface it replaces.
+ *
+ * Tensor layouts (reference op layout, moe_kernel.hip:7-17):
+ *   x          (rows, K)          fp16 (or bf16 where stated), row-major
+ *   w_packed   (E, N, K/8)        int32, nibble j of word w is k = 8w + j (low first)
+ *   scales     (E, N, K/group)    fp16
+ *   w_zeros    (E, N/8, K/group)  int32, nibble n%8 of word n/8, or NULL (zp = 8)
+ *   sorted_token_ids (P,), expert_ids (P/block_m,), num_tokens_post_padded (1,) int32
+ *   topk_weights (M*top_k,) fp32, topk_ids (M, top_k) int32
+ */
+#ifndef W4A8_MOE_H_
+#define W4A8_MOE_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#if defined(__GNUC__) || defined(__clang__)
+#define W4A8_API __attribute__((visibility("default")))
+#else
+#define W4A8_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. A non-zero return leaves a message for w4a8_last_error(). */
+#define W4A8_OK 0
+#define W4A8_ERR_INVALID 1      /* argument violates the contract (TORCH_CHECK in the reference) */
+#define W4A8_ERR_HIP 2          /* a HIP runtime call or kernel launch failed */
+#define W4A8_ERR_WORKSPACE 3    /* workspace pointer NULL or smaller than required */
+
+/* Kernel ids carried over the ABI (w4a8_fp8_wmma/kernel_names.h:41-48). */
+#define W4A8_MOE_KERNEL_SCALAR 0   /* scalar golden grouped GEMM */
+#define W4A8_MOE_KERNEL_WMMA 6     /* tiled matrix-core grouped GEMM (fp8 MFMA on gfx950) */
+#define W4A8_MOE_KERNEL_GEMV 7     /* decode grouped GEMV (fp8 MFMA, token rows compacted) */
+
+/* x dtype selector for w4a8_moe_apply. */
+#define W4A8_DTYPE_F16 0
+#define W4A8_DTYPE_BF16 1
+
+/* Version of this ABI (bumped on any signature change). */
+W4A8_API int w4a8_abi_version(void);
+
+/* Thread-local message of the last failing call on this thread ("" if none). */
+W4A8_API const char* w4a8_last_error(void);
+
+/* ---------------------------------------------------------------------------------
+ * Per-token fp8 e4m3 activation quantisation.
+ * Replaces moe_compute_act_fp8_kernel (moe_kernel.hip:87-127) and the dense twin
+ * compute_act_fp8_and_scales_kernel (w4a8_fp8_wmma_kernel.hip:153-200).
+ * x_fp8 bytes are in natural k order when k8_interleave == 0, else in the
+ * kernels' k8-interleaved order (byte p of each 8-byte block holds k = {0,2,4,6,1,3,5,7}[p]).
+ */
+W4A8_API int w4a8_act_quant_fp8(const void* x_f16, int64_t rows, int64_t K, uint8_t* x_fp8,
+                       float* act_scales, int k8_interleave, void* stream);
+
+/* ---------------------------------------------------------------------------------
+ * int4 -> e4m3 dequant of op-layout weights: out (rows, K) bytes = e4m3(nibble - zp),
+ * natural k order. Exposes the exact decode the GEMM kernels run in registers
+ * (tile_config.h:42-71, moe_kernel.hip:63-83). rows = E*N; w_zeros NULL => zp = 8.
+ */
+W4A8_API int w4a8_dequant_fp8(const int32_t* w_packed, const int32_t* w_zeros, int64_t E, int64_t N,
+                     int64_t K, int64_t group_size, int weight_is_e2m1, uint8_t* out,
+                     void* stream);
+
+/* ---------------------------------------------------------------------------------
+ * Router: softmax over E logits -> top_k -> optional renormalise.
+ * Replaces vLLM fused_topk/topk_softmax, which the reference calls through vLLM
+ * (not in the reference tree; contract from the layer the reference patches).
+ * Selection is on logits, ties to the lower expert id; output order descending.
+ */
+W4A8_API int w4a8_topk_softmax(const float* logits, int64_t T, int64_t E, int64_t top_k,
+                      int renormalize, float* topk_weights, int32_t* topk_ids, void* stream);
+
+/* ---------------------------------------------------------------------------------
+ * moe_align_block_size (vLLM op called at moe_experts.py:587-589, contract mirrored
+ * by test_moe_experts.py:136-152). Groups slots t*top_k+j by expert ascending, slot
+ * ascending, pads each expert to a multiple of block_m with the sentinel numel.
+ * sorted_len must equal w4a8_moe_align_sorted_len(); entries past ntp hold the
+ * sentinel and expert_ids -1. expert_map (num_experts entries, -1 = not local) may be
+ * NULL. Deterministic (no atomics decide the order).
+ */
+W4A8_API int64_t w4a8_moe_align_sorted_len(int64_t numel, int64_t num_experts, int64_t block_m);
+W4A8_API size_t w4a8_moe_align_workspace_size(int64_t numel, int64_t num_experts);
+W4A8_API int w4a8_moe_align_block_size(const int32_t* topk_ids, int64_t numel, int64_t num_experts,
+                              int64_t block_m, const int32_t* expert_map,
+                              int32_t* sorted_token_ids, int64_t sorted_len,
+                              int32_t* expert_ids, int32_t* num_tokens_post_padded,
+                              void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------------
+ * Grouped GEMM, padded sorted layout: out (P, N) fp16.
+ * Replaces mmq_fp8_moe_gemm (bindings.cpp:178-228 -> moe_kernel.hip:1358-1392).
+ * Row r with slot s = sorted_token_ids[r] < T*top_k (and r < ntp) gathers x[s/top_k];
+ * other rows are not written.
+ */
+W4A8_API size_t w4a8_moe_gemm_workspace_size(int64_t x_rows, int64_t K);
+W4A8_API int w4a8_mmq_fp8_moe_gemm(const void* x_f16, int64_t T, int64_t K,
+                          const int32_t* w_packed, const void* scales_f16,
+                          const int32_t* w_zeros, int64_t E, int64_t N, int64_t group_size,
+                          const int32_t* sorted_token_ids, int64_t P,
+                          const int32_t* expert_ids, const int32_t* num_tokens_post_padded,
+                          int64_t top_k, int64_t block_m, int64_t kernel, int weight_is_e2m1,
+                          void* out_f16, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Fused gemm1 + silu_and_mul: w_packed is w13 (E, 2*inter, K/8); out (P, inter) fp16.
+ * Replaces mmq_fp8_moe_gemm1_silu (bindings.cpp:235-287 -> moe_kernel.hip:1327-1356).
+ * Same workspace as w4a8_mmq_fp8_moe_gemm. kernel must be WMMA. */
+W4A8_API int w4a8_mmq_fp8_moe_gemm1_silu(const void* x_f16, int64_t T, int64_t K,
+                                const int32_t* w_packed, const void* scales_f16,
+                                const int32_t* w_zeros, int64_t E, int64_t N,
+                                int64_t group_size, const int32_t* sorted_token_ids,
+                                int64_t P, const int32_t* expert_ids,
+                                const int32_t* num_tokens_post_padded, int64_t top_k,
+                                int64_t block_m, int64_t kernel, int weight_is_e2m1,
+                                void* out_f16, void* workspace, size_t workspace_bytes,
+                                void* stream);
+
+/* Fused gemm2 + top-k weight + atomic scatter into a pre-zeroed fp32 output (M, N).
+ * x is the (P, K) post-activation buffer, gathered by identity.
+ * Replaces mmq_fp8_moe_gemm_scatter (bindings.cpp:293-353 -> moe_kernel.hip:1398-1433).
+ * Workspace: w4a8_moe_gemm_workspace_size(P, K). */
+W4A8_API int w4a8_mmq_fp8_moe_gemm_scatter(const void* x_f16, int64_t P_rows, int64_t K,
+                                  const int32_t* w_packed, const void* scales_f16,
+                                  const int32_t* w_zeros, int64_t E, int64_t N,
+                                  int64_t group_size, const int32_t* sorted_token_ids,
+                                  int64_t P, const int32_t* expert_ids,
+                                  const int32_t* num_tokens_post_padded,
+                                  const float* topk_weights, float* output, int64_t M,
+                                  int64_t top_k, int64_t block_m, int64_t kernel,
+                                  int weight_is_e2m1, void* workspace,
+                                  size_t workspace_bytes, void* stream);
+
+/* Deterministic weighted gather-reduce: out (M, N) fp32 = sum_j w * out2[row(t, j)].
+ * Replaces mmq_fp8_moe_gather_reduce (bindings.cpp:357-380 -> moe_kernel.hip:1437-1464).
+ * Workspace: w4a8_gather_reduce_workspace_size(M*top_k). */
+W4A8_API size_t w4a8_gather_reduce_workspace_size(int64_t m_times_topk);
+W4A8_API int w4a8_mmq_fp8_moe_gather_reduce(const void* out2_f16, int64_t P, int64_t N,
+                                   const int32_t* sorted_token_ids,
+                                   const float* topk_weights, int64_t m_times_topk,
+                                   const int32_t* num_tokens_post_padded, int64_t top_k,
+                                   float* out, void* workspace, size_t workspace_bytes,
+                                   void* stream);
+
+/* vLLM silu_and_mul on (rows, 2*inter) fp16 -> (rows, inter) fp16, the unfused
+ * activation the reference decode path calls (moe_experts.py:627-630). */
+W4A8_API int w4a8_silu_and_mul(const void* in_f16, int64_t rows, int64_t inter, void* out_f16,
+                      void* stream);
+
+/* ---------------------------------------------------------------------------------
+ * Dense W4A8 GEMM: x (M, K) fp16, w (N, K/8), scales (N, K/g), zeros (N/8, K/g) or NULL
+ * -> out (M, N) fp16. Replaces mmq_fp8_gemm (bindings.cpp:98-146 ->
+ * launch_mmq_fp8_gemm_gfx1201, w4a8_fp8_wmma_kernel.hip:2507). kernel = a DenseKernel
+ * id (kernel_names.h:18-36); 0 runs the scalar golden, every other valid id the fp8
+ * MFMA path. Workspace: w4a8_moe_gemm_workspace_size(M, K). */
+W4A8_API int w4a8_mmq_fp8_gemm(const void* x_f16, int64_t M, int64_t K, const int32_t* w_packed,
+                      const void* scales_f16, const int32_t* w_zeros, int64_t N,
+                      int64_t group_size, int64_t kernel, int weight_is_e2m1, void* out_f16,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------------
+ * Whole gated MoE expert path: the _run_grouped_moe composition
+ * (moe_experts.py:493-665) behind the patched MoeWNA16Method.apply
+ * (moe_experts.py:1308-1332). x (T, H) in x_dtype -> out (T, H) in x_dtype.
+ * w13 (E, 2*inter, H/8), w2 (E, H, inter/8); scales/zeros as above (zeros may be
+ * NULL per weight). topk_ids (T, top_k) int32, topk_weights (T, top_k) fp32.
+ * expert_map may be NULL. Chooses the decode (T <= 96) or prefill schedule itself.
+ */
+W4A8_API size_t w4a8_moe_apply_workspace_size(int64_t T, int64_t H, int64_t inter, int64_t E,
+                                     int64_t top_k);
+W4A8_API int w4a8_moe_apply(const void* x, int x_dtype, int64_t T, int64_t H, int64_t inter,
+                   int64_t E, int64_t top_k, int64_t group_size,
+                   const int32_t* w13, const void* w13_scales_f16, const int32_t* w13_zeros,
+                   const int32_t* w2, const void* w2_scales_f16, const int32_t* w2_zeros,
+                   const float* topk_weights, const int32_t* topk_ids,
+                   const int32_t* expert_map, int weight_is_e2m1, void* out,
+                   void* workspace, size_t workspace_bytes, void* stream);
+
+/* Optional per-stage timing of w4a8_moe_apply on the calling thread: when count == 8,
+ * the next w4a8_moe_apply calls record events[0] before the first launch and events[i]
+ * after stage i (1 align, 2 act-quant x, 3 accumulator clear, 4 gemm1+SiLU, 5 act-quant
+ * h, 6 gemm2, 7 reduce/cast) on their stream. Events are hipEvent_t handles owned by the
+ * caller; count == 0 switches recording off. No reference counterpart (measurement aid). */
+W4A8_API int w4a8_moe_apply_set_stage_events(void* const* events, int count);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* W4A8_MOE_H_ */

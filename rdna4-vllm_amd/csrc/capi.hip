@@ -1,0 +1,466 @@
+// C ABI entry points (include/w4a8_moe.h): argument validation mirroring the reference's
+// TORCH_CHECKs (w4a8_fp8_wmma/bindings.cpp), workspace carving, kernel-id dispatch and the
+// whole-layer composition (moe_experts.py:493-665).
+#include <string>
+
+#include "w4a8_common.h"
+#include "w4a8_internal.h"
+
+namespace w4a8 {
+
+namespace {
+thread_local std::string g_error;
+
+hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+#define W4A8_REQUIRE(cond, msg)            \
+    do {                                   \
+        if (!(cond)) {                     \
+            ::w4a8::set_error(msg);        \
+            return W4A8_ERR_INVALID;       \
+        }                                  \
+    } while (0)
+
+bool moe_kernel_valid(int64_t k) { return k == 0 || k == 6 || k == 7; }
+bool dense_kernel_valid(int64_t v) { return v == 0 || v == 1 || v == 2 || (v >= 4 && v <= 14); }
+
+// Shapes shared by every grouped GEMM entry (bindings.cpp:191-221).
+int check_grouped(int64_t rows, int64_t K, int64_t E, int64_t N, int64_t gs, int64_t P,
+                  int64_t block_m, int64_t top_k, int64_t kernel, const void* x,
+                  const void* w, const void* scales, const int32_t* sti, const int32_t* eid,
+                  const int32_t* ntp) {
+    W4A8_REQUIRE(rows >= 0 && K > 0 && E > 0 && N > 0 && P >= 0, "invalid sizes");
+    W4A8_REQUIRE(K % kPackFactor == 0, "K must be a multiple of 8 (w_packed last dim is K/8)");
+    W4A8_REQUIRE(gs > 0 && K % gs == 0, "K not divisible by group_size");
+    W4A8_REQUIRE(gs % 16 == 0 && gs <= kMaxGroupSize,
+                 "group_size must be a multiple of 16 and <= 128");
+    W4A8_REQUIRE(block_m > 0 && P % block_m == 0, "P not divisible by block_m");
+    W4A8_REQUIRE(top_k > 0, "top_k must be positive");
+    W4A8_REQUIRE(moe_kernel_valid(kernel),
+                 "moe kernel id must be 0 (scalar) / 6 (wmma) / 7 (gemv)");
+    if (kernel == W4A8_MOE_KERNEL_WMMA)
+        W4A8_REQUIRE(block_m % 16 == 0 && block_m <= 128,
+                     "wmma block_m must be a multiple of 16 and <= 128");
+    if (kernel == W4A8_MOE_KERNEL_GEMV)
+        W4A8_REQUIRE(block_m % 8 == 0 && block_m <= 64 && K % 32 == 0 && gs % 32 == 0,
+                     "gemv needs block_m mult of 8 <= 64, K%32==0, group_size%32==0");
+    W4A8_REQUIRE(x != nullptr && w != nullptr && scales != nullptr, "null tensor pointer");
+    W4A8_REQUIRE(P == 0 || (sti != nullptr && eid != nullptr && ntp != nullptr),
+                 "null routing pointer");
+    return W4A8_OK;
+}
+
+int run_grouped(GroupedArgs& a, int64_t kernel, void* ws, size_t ws_bytes, hipStream_t s) {
+    Workspace w(ws, ws_bytes);
+    a.x_fp8 = w.take<uint8_t>((size_t)(a.x_rows * a.K));
+    a.act_scales = w.take<float>((size_t)a.x_rows);
+    if ((a.x_rows > 0 && ws == nullptr) || !w.ok()) {
+        set_error("workspace smaller than w4a8_moe_gemm_workspace_size()");
+        return W4A8_ERR_WORKSPACE;
+    }
+    // identity-gathered inputs (gemm2 / scatter) have one row per padded row: skip padding.
+    const bool filter = a.identity_gather && a.sorted_ids != nullptr;
+    if (int rc = launch_act_quant(a.x, a.x_bf16, a.x_rows, a.K, a.x_fp8, a.act_scales, true, s,
+                                  filter ? a.sorted_ids : nullptr, filter ? a.ntp : nullptr,
+                                  a.num_valid))
+        return rc;
+    const bool mfma = mfma_supported(a.K, a.group_size);
+    if (kernel == W4A8_MOE_KERNEL_WMMA && mfma) return launch_grouped_mfma(a, s);
+    if (kernel == W4A8_MOE_KERNEL_GEMV && mfma) return launch_grouped_gemv(a, s);
+    return launch_grouped_scalar(a, s);
+}
+
+}  // namespace
+
+void set_error(const std::string& msg) { g_error = msg; }
+void clear_error() { g_error.clear(); }
+
+int check_launch(const char* what) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        set_error(std::string(what) + ": " + hipGetErrorString(e));
+        return W4A8_ERR_HIP;
+    }
+    return W4A8_OK;
+}
+
+}  // namespace w4a8
+
+// ---------------------------------------------------------------------------------------
+// whole layer
+// ---------------------------------------------------------------------------------------
+namespace w4a8 {
+namespace {
+constexpr int64_t kGemvMaxM = 96;   // moe_experts.py:563 GEMV_MAX_M
+constexpr int64_t kDecodeBlockM = 16;
+constexpr int64_t kPrefillBlockM = 64;
+
+struct ApplyPlan {
+    bool decode;
+    int64_t block_m, P, nblk;
+};
+
+ApplyPlan plan_apply(int64_t T, int64_t E, int64_t top_k) {
+    ApplyPlan pl;
+    pl.decode = T <= kGemvMaxM;
+    pl.block_m = pl.decode ? kDecodeBlockM : kPrefillBlockM;
+    pl.P = w4a8_moe_align_sorted_len(T * top_k, E, pl.block_m);
+    pl.nblk = pl.P / pl.block_m;
+    return pl;
+}
+
+template <typename WS>
+void carve_apply(WS& w, const ApplyPlan& pl, int64_t T, int64_t H, int64_t inter, int64_t E,
+                 int64_t top_k, int32_t** sti, int32_t** eid, int32_t** ntp, void** align_ws,
+                 size_t* align_bytes, uint8_t** xq, float** s1, __half** h, uint8_t** hq,
+                 float** s2, float** acc) {
+    *sti = w.template take<int32_t>((size_t)pl.P);
+    *eid = w.template take<int32_t>((size_t)pl.nblk);
+    *ntp = w.template take<int32_t>(1);
+    *align_bytes = align_workspace_bytes(T * top_k, E);
+    *align_ws = w.template take<uint8_t>(*align_bytes);
+    *xq = w.template take<uint8_t>((size_t)(T * H));
+    *s1 = w.template take<float>((size_t)T);
+    *h = w.template take<__half>((size_t)(pl.P * inter));
+    *hq = w.template take<uint8_t>((size_t)(pl.P * inter));
+    *s2 = w.template take<float>((size_t)pl.P);
+    // decode: per-slot fp32 rows (T*k, H); prefill: fp32 (T, H) scatter accumulator
+    *acc = w.template take<float>((size_t)((pl.decode ? T * top_k : T) * H));
+}
+
+constexpr int kStageEvents = 8;
+thread_local hipEvent_t g_stage_events[kStageEvents];
+thread_local bool g_stage_on = false;
+
+inline void stage_mark(int i, hipStream_t s) {
+    if (g_stage_on) (void)hipEventRecord(g_stage_events[i], s);
+}
+
+struct SizeProbe {
+    WorkspaceSize s;
+    template <typename T>
+    T* take(size_t n) { s.take<T>(n); return nullptr; }
+};
+}  // namespace
+}  // namespace w4a8
+
+
+using namespace w4a8;
+
+extern "C" {
+
+int w4a8_abi_version(void) { return 1; }
+
+const char* w4a8_last_error(void) { return g_error.c_str(); }
+
+int w4a8_act_quant_fp8(const void* x_f16, int64_t rows, int64_t K, uint8_t* x_fp8,
+                       float* act_scales, int k8_interleave, void* stream) {
+    clear_error();
+    W4A8_REQUIRE(rows >= 0 && K > 0 && K % 8 == 0, "act_quant: K must be a positive multiple of 8");
+    W4A8_REQUIRE(rows == 0 || (x_f16 && x_fp8 && act_scales), "act_quant: null pointer");
+    return launch_act_quant(x_f16, false, rows, K, x_fp8, act_scales, k8_interleave != 0,
+                            as_stream(stream));
+}
+
+int w4a8_dequant_fp8(const int32_t* w_packed, const int32_t* w_zeros, int64_t E, int64_t N,
+                     int64_t K, int64_t group_size, int weight_is_e2m1, uint8_t* out,
+                     void* stream) {
+    clear_error();
+    W4A8_REQUIRE(E > 0 && N > 0 && K > 0 && K % 8 == 0, "dequant: invalid sizes");
+    W4A8_REQUIRE(group_size > 0 && K % group_size == 0 && group_size % 8 == 0,
+                 "dequant: group_size must divide K and be a multiple of 8");
+    W4A8_REQUIRE(w_zeros == nullptr || N % 8 == 0, "dequant: zero-points need N % 8 == 0");
+    W4A8_REQUIRE(!(weight_is_e2m1 && w_zeros), "mxfp4 (E2M1) weights are symmetric; w_zeros must be empty");
+    W4A8_REQUIRE(w_packed && out, "dequant: null pointer");
+    return launch_dequant(w_packed, w_zeros, E, N, K, group_size, weight_is_e2m1 != 0, out,
+                          as_stream(stream));
+}
+
+int w4a8_topk_softmax(const float* logits, int64_t T, int64_t E, int64_t top_k,
+                      int renormalize, float* topk_weights, int32_t* topk_ids, void* stream) {
+    clear_error();
+    W4A8_REQUIRE(T >= 0 && E > 0 && top_k > 0, "topk_softmax: invalid sizes");
+    W4A8_REQUIRE(T == 0 || (logits && topk_weights && topk_ids), "topk_softmax: null pointer");
+    return launch_topk_softmax(logits, T, E, top_k, renormalize != 0, topk_weights, topk_ids,
+                               as_stream(stream));
+}
+
+int64_t w4a8_moe_align_sorted_len(int64_t numel, int64_t num_experts, int64_t block_m) {
+    if (block_m <= 0) return -1;
+    const int64_t m = numel + num_experts * (block_m - 1);
+    return (m + block_m - 1) / block_m * block_m;
+}
+
+size_t w4a8_moe_align_workspace_size(int64_t numel, int64_t num_experts) {
+    return align_workspace_bytes(numel, num_experts);
+}
+
+int w4a8_moe_align_block_size(const int32_t* topk_ids, int64_t numel, int64_t num_experts,
+                              int64_t block_m, const int32_t* expert_map,
+                              int32_t* sorted_token_ids, int64_t sorted_len,
+                              int32_t* expert_ids, int32_t* num_tokens_post_padded,
+                              void* workspace, size_t workspace_bytes, void* stream) {
+    clear_error();
+    W4A8_REQUIRE(numel >= 0 && num_experts > 0 && block_m > 0, "moe_align: invalid sizes");
+    W4A8_REQUIRE(numel < (int64_t)1 << 30, "moe_align: too many slots");
+    W4A8_REQUIRE(sorted_len == w4a8_moe_align_sorted_len(numel, num_experts, block_m),
+                 "moe_align: sorted_len must equal round_up(numel + E*(block_m-1), block_m)");
+    W4A8_REQUIRE(sorted_token_ids && expert_ids && num_tokens_post_padded,
+                 "moe_align: null output pointer");
+    W4A8_REQUIRE(numel == 0 || topk_ids, "moe_align: null topk_ids");
+    return launch_align(topk_ids, numel, num_experts, block_m, expert_map, sorted_token_ids,
+                        sorted_len, expert_ids, num_tokens_post_padded, workspace,
+                        workspace_bytes, as_stream(stream));
+}
+
+size_t w4a8_moe_gemm_workspace_size(int64_t x_rows, int64_t K) {
+    WorkspaceSize s;
+    s.take<uint8_t>((size_t)(x_rows * K));
+    s.take<float>((size_t)x_rows);
+    return s.used;
+}
+
+int w4a8_mmq_fp8_moe_gemm(const void* x_f16, int64_t T, int64_t K, const int32_t* w_packed,
+                          const void* scales_f16, const int32_t* w_zeros, int64_t E, int64_t N,
+                          int64_t group_size, const int32_t* sorted_token_ids, int64_t P,
+                          const int32_t* expert_ids, const int32_t* ntp, int64_t top_k,
+                          int64_t block_m, int64_t kernel, int weight_is_e2m1, void* out_f16,
+                          void* workspace, size_t workspace_bytes, void* stream) {
+    clear_error();
+    if (int rc = check_grouped(T, K, E, N, group_size, P, block_m, top_k, kernel, x_f16,
+                               w_packed, scales_f16, sorted_token_ids, expert_ids, ntp))
+        return rc;
+    W4A8_REQUIRE(w_zeros == nullptr || N % 8 == 0, "w_zeros must be (E, N/8, K/group) int32");
+    W4A8_REQUIRE(!(weight_is_e2m1 && w_zeros), "mxfp4 (E2M1) weights are symmetric; w_zeros must be empty");
+    W4A8_REQUIRE(P == 0 || out_f16, "null output");
+    GroupedArgs a{};
+    a.x = x_f16; a.x_rows = T; a.K = K; a.w = w_packed;
+    a.scales = static_cast<const uint16_t*>(scales_f16); a.zeros = w_zeros;
+    a.E = E; a.N = N; a.group_size = group_size;
+    a.sorted_ids = sorted_token_ids; a.P = P; a.expert_ids = expert_ids; a.ntp = ntp;
+    a.top_k = top_k; a.identity_gather = false; a.num_valid = T * top_k; a.block_m = block_m;
+    a.e2m1 = weight_is_e2m1 != 0; a.epi = Epi::kHalf; a.out = out_f16; a.out_top_k = top_k;
+    return run_grouped(a, kernel, workspace, workspace_bytes, as_stream(stream));
+}
+
+int w4a8_mmq_fp8_moe_gemm1_silu(const void* x_f16, int64_t T, int64_t K, const int32_t* w_packed,
+                                const void* scales_f16, const int32_t* w_zeros, int64_t E,
+                                int64_t N, int64_t group_size, const int32_t* sorted_token_ids,
+                                int64_t P, const int32_t* expert_ids, const int32_t* ntp,
+                                int64_t top_k, int64_t block_m, int64_t kernel,
+                                int weight_is_e2m1, void* out_f16, void* workspace,
+                                size_t workspace_bytes, void* stream) {
+    clear_error();
+    W4A8_REQUIRE(kernel == W4A8_MOE_KERNEL_WMMA,
+                 "fused gemm1+silu needs the 'wmma' kernel");
+    if (int rc = check_grouped(T, K, E, N, group_size, P, block_m, top_k, kernel, x_f16,
+                               w_packed, scales_f16, sorted_token_ids, expert_ids, ntp))
+        return rc;
+    W4A8_REQUIRE(N % 2 == 0, "w13 N must be 2*inter (even)");
+    W4A8_REQUIRE(w_zeros == nullptr || N % 8 == 0, "w_zeros must be (E, (2*inter)/8, K/group) int32");
+    W4A8_REQUIRE(!(weight_is_e2m1 && w_zeros), "mxfp4 (E2M1) weights are symmetric; w_zeros must be empty");
+    W4A8_REQUIRE(P == 0 || out_f16, "null output");
+    GroupedArgs a{};
+    a.x = x_f16; a.x_rows = T; a.K = K; a.w = w_packed;
+    a.scales = static_cast<const uint16_t*>(scales_f16); a.zeros = w_zeros;
+    a.E = E; a.N = N; a.group_size = group_size;
+    a.sorted_ids = sorted_token_ids; a.P = P; a.expert_ids = expert_ids; a.ntp = ntp;
+    a.top_k = top_k; a.identity_gather = false; a.num_valid = T * top_k; a.block_m = block_m;
+    a.e2m1 = weight_is_e2m1 != 0; a.epi = Epi::kSiluHalf; a.out = out_f16; a.out_top_k = top_k;
+    return run_grouped(a, kernel, workspace, workspace_bytes, as_stream(stream));
+}
+
+int w4a8_mmq_fp8_moe_gemm_scatter(const void* x_f16, int64_t P_rows, int64_t K,
+                                  const int32_t* w_packed, const void* scales_f16,
+                                  const int32_t* w_zeros, int64_t E, int64_t N,
+                                  int64_t group_size, const int32_t* sorted_token_ids, int64_t P,
+                                  const int32_t* expert_ids, const int32_t* ntp,
+                                  const float* topk_weights, float* output, int64_t M,
+                                  int64_t top_k, int64_t block_m, int64_t kernel,
+                                  int weight_is_e2m1, void* workspace, size_t workspace_bytes,
+                                  void* stream) {
+    clear_error();
+    if (int rc = check_grouped(P_rows, K, E, N, group_size, P, block_m, top_k, kernel, x_f16,
+                               w_packed, scales_f16, sorted_token_ids, expert_ids, ntp))
+        return rc;
+    W4A8_REQUIRE(P_rows >= P, "x must have one row per padded row (P, K)");
+    W4A8_REQUIRE(M >= 0 && (M == 0 || (output && topk_weights)), "null output/topk_weights");
+    W4A8_REQUIRE(w_zeros == nullptr || N % 8 == 0, "w_zeros must be (E, N/8, K/group) int32");
+    W4A8_REQUIRE(!(weight_is_e2m1 && w_zeros), "mxfp4 (E2M1) weights are symmetric; w_zeros must be empty");
+    GroupedArgs a{};
+    a.x = x_f16; a.x_rows = P_rows; a.K = K; a.w = w_packed;
+    a.scales = static_cast<const uint16_t*>(scales_f16); a.zeros = w_zeros;
+    a.E = E; a.N = N; a.group_size = group_size;
+    a.sorted_ids = sorted_token_ids; a.P = P; a.expert_ids = expert_ids; a.ntp = ntp;
+    a.top_k = top_k; a.identity_gather = true; a.num_valid = M * top_k; a.block_m = block_m;
+    a.e2m1 = weight_is_e2m1 != 0; a.epi = Epi::kScatter; a.out = output;
+    a.topk_weights = topk_weights; a.out_top_k = top_k;
+    return run_grouped(a, kernel, workspace, workspace_bytes, as_stream(stream));
+}
+
+size_t w4a8_gather_reduce_workspace_size(int64_t m_times_topk) {
+    WorkspaceSize s;
+    s.take<int32_t>((size_t)m_times_topk);
+    return s.used;
+}
+
+int w4a8_mmq_fp8_moe_gather_reduce(const void* out2_f16, int64_t P, int64_t N,
+                                   const int32_t* sorted_token_ids, const float* topk_weights,
+                                   int64_t m_times_topk, const int32_t* ntp, int64_t top_k,
+                                   float* out, void* workspace, size_t workspace_bytes,
+                                   void* stream) {
+    clear_error();
+    W4A8_REQUIRE(P >= 0 && N >= 0 && top_k > 0 && m_times_topk >= 0, "gather_reduce: invalid sizes");
+    W4A8_REQUIRE(m_times_topk % top_k == 0, "topk_weights.numel() must be M*top_k");
+    W4A8_REQUIRE(P == 0 || (out2_f16 && sorted_token_ids && ntp), "gather_reduce: null pointer");
+    W4A8_REQUIRE(m_times_topk == 0 || (topk_weights && out), "gather_reduce: null pointer");
+    Workspace w(workspace, workspace_bytes);
+    int32_t* slot_to_row = w.take<int32_t>((size_t)m_times_topk);
+    if ((m_times_topk > 0 && workspace == nullptr) || !w.ok()) {
+        set_error("gather_reduce: workspace too small");
+        return W4A8_ERR_WORKSPACE;
+    }
+    return launch_gather_reduce(out2_f16, P, N, sorted_token_ids, topk_weights, m_times_topk,
+                                ntp, top_k, out, slot_to_row, as_stream(stream));
+}
+
+int w4a8_silu_and_mul(const void* in_f16, int64_t rows, int64_t inter, void* out_f16,
+                      void* stream) {
+    clear_error();
+    W4A8_REQUIRE(rows >= 0 && inter >= 0, "silu_and_mul: invalid sizes");
+    W4A8_REQUIRE(rows * inter == 0 || (in_f16 && out_f16), "silu_and_mul: null pointer");
+    return launch_silu_and_mul(in_f16, rows, inter, out_f16, as_stream(stream));
+}
+
+int w4a8_mmq_fp8_gemm(const void* x_f16, int64_t M, int64_t K, const int32_t* w_packed,
+                      const void* scales_f16, const int32_t* w_zeros, int64_t N,
+                      int64_t group_size, int64_t kernel, int weight_is_e2m1, void* out_f16,
+                      void* workspace, size_t workspace_bytes, void* stream) {
+    clear_error();
+    W4A8_REQUIRE(M >= 0 && K > 0 && N > 0 && K % 8 == 0, "dense: invalid sizes");
+    W4A8_REQUIRE(group_size > 0 && K % group_size == 0, "K not divisible by scales' K dim");
+    W4A8_REQUIRE(group_size % 16 == 0 && group_size <= kMaxGroupSize,
+                 "group_size must be a multiple of 16 and <= 128");
+    W4A8_REQUIRE(dense_kernel_valid(kernel), "dense kernel id invalid (DenseKernel 0..14, no 3)");
+    W4A8_REQUIRE(!(weight_is_e2m1 && w_zeros), "mxfp4 (E2M1) weights are symmetric; w_zeros must be empty");
+    W4A8_REQUIRE(w_zeros == nullptr || N % 8 == 0, "w_zeros shape mismatch");
+    W4A8_REQUIRE(M == 0 || (x_f16 && w_packed && scales_f16 && out_f16), "dense: null pointer");
+    GroupedArgs a{};
+    a.x = x_f16; a.x_rows = M; a.K = K; a.w = w_packed;
+    a.scales = static_cast<const uint16_t*>(scales_f16); a.zeros = w_zeros;
+    a.E = 1; a.N = N; a.group_size = group_size;
+    a.sorted_ids = nullptr; a.P = M; a.expert_ids = nullptr; a.ntp = nullptr;
+    a.top_k = 1; a.identity_gather = false; a.num_valid = M;
+    a.e2m1 = weight_is_e2m1 != 0; a.epi = Epi::kHalf; a.out = out_f16; a.out_top_k = 1;
+    // DenseKernel 0 = reference_scalar, 11 = decode_gemv, everything else = matrix cores.
+    int64_t mk = W4A8_MOE_KERNEL_WMMA;
+    a.block_m = 64;
+    if (kernel == 0) { mk = W4A8_MOE_KERNEL_SCALAR; a.block_m = 1; }
+    if (kernel == 11) { mk = W4A8_MOE_KERNEL_GEMV; a.block_m = 16; }
+    return run_grouped(a, mk, workspace, workspace_bytes, as_stream(stream));
+}
+
+int w4a8_moe_apply_set_stage_events(void* const* events, int count) {
+    clear_error();
+    if (count == 0) { g_stage_on = false; return W4A8_OK; }
+    W4A8_REQUIRE(count == kStageEvents && events != nullptr, "stage events: need exactly 8 events");
+    for (int i = 0; i < kStageEvents; ++i) {
+        W4A8_REQUIRE(events[i] != nullptr, "stage events: null event");
+        g_stage_events[i] = reinterpret_cast<hipEvent_t>(events[i]);
+    }
+    g_stage_on = true;
+    return W4A8_OK;
+}
+
+size_t w4a8_moe_apply_workspace_size(int64_t T, int64_t H, int64_t inter, int64_t E,
+                                     int64_t top_k) {
+    const ApplyPlan pl = plan_apply(T, E, top_k);
+    SizeProbe sp;
+    int32_t *a, *b, *c; void* d; size_t db; uint8_t* e; float* f; __half* g; uint8_t* h;
+    float *i, *j;
+    carve_apply(sp, pl, T, H, inter, E, top_k, &a, &b, &c, &d, &db, &e, &f, &g, &h, &i, &j);
+    return sp.s.used;
+}
+
+int w4a8_moe_apply(const void* x, int x_dtype, int64_t T, int64_t H, int64_t inter, int64_t E,
+                   int64_t top_k, int64_t group_size, const int32_t* w13,
+                   const void* w13_scales_f16, const int32_t* w13_zeros, const int32_t* w2,
+                   const void* w2_scales_f16, const int32_t* w2_zeros,
+                   const float* topk_weights, const int32_t* topk_ids,
+                   const int32_t* expert_map, int weight_is_e2m1, void* out, void* workspace,
+                   size_t workspace_bytes, void* stream) {
+    clear_error();
+    W4A8_REQUIRE(x_dtype == W4A8_DTYPE_F16 || x_dtype == W4A8_DTYPE_BF16, "x dtype must be fp16 or bf16");
+    W4A8_REQUIRE(T >= 0 && H > 0 && inter > 0 && E > 0 && top_k > 0, "moe_apply: invalid sizes");
+    W4A8_REQUIRE(group_size > 0 && H % group_size == 0 && inter % group_size == 0 &&
+                 group_size % 16 == 0 && group_size <= kMaxGroupSize,
+                 "moe_apply: group_size must divide hidden and intermediate, mult of 16, <= 128");
+    W4A8_REQUIRE(H % 8 == 0 && inter % 8 == 0, "moe_apply: sizes must be multiples of 8");
+    W4A8_REQUIRE(!(weight_is_e2m1 && (w13_zeros || w2_zeros)),
+                 "mxfp4 (E2M1) weights are symmetric; w_zeros must be empty");
+    if (T == 0) return W4A8_OK;
+    W4A8_REQUIRE(x && w13 && w13_scales_f16 && w2 && w2_scales_f16 && topk_weights && topk_ids && out,
+                 "moe_apply: null pointer");
+    hipStream_t s = as_stream(stream);
+    const ApplyPlan pl = plan_apply(T, E, top_k);
+    Workspace w(workspace, workspace_bytes);
+    int32_t *sti, *eid, *ntp; void* aws; size_t abytes; uint8_t* xq; float* s1; __half* h;
+    uint8_t* hq; float* s2; float* acc;
+    carve_apply(w, pl, T, H, inter, E, top_k, &sti, &eid, &ntp, &aws, &abytes, &xq, &s1, &h, &hq,
+                &s2, &acc);
+    if (workspace == nullptr || !w.ok()) {
+        set_error("moe_apply: workspace smaller than w4a8_moe_apply_workspace_size()");
+        return W4A8_ERR_WORKSPACE;
+    }
+    const bool bf16 = x_dtype == W4A8_DTYPE_BF16;
+    const bool e2m1 = weight_is_e2m1 != 0;
+    const int64_t numel = T * top_k;
+    stage_mark(0, s);
+    if (int rc = launch_align(topk_ids, numel, E, pl.block_m, expert_map, sti, pl.P, eid, ntp,
+                              aws, abytes, s))
+        return rc;
+    stage_mark(1, s);
+    if (int rc = launch_act_quant(x, bf16, T, H, xq, s1, true, s)) return rc;
+    stage_mark(2, s);
+    if (!pl.decode)
+        if (int rc = launch_zero_f32(acc, T * H, s)) return rc;
+    stage_mark(3, s);
+
+    const bool mfma = mfma_supported(H, group_size) && mfma_supported(inter, group_size);
+    // gemm1 + SiLU*mul -> h (P, inter)
+    GroupedArgs g1{};
+    g1.x_rows = T; g1.K = H; g1.w = w13; g1.scales = static_cast<const uint16_t*>(w13_scales_f16);
+    g1.zeros = w13_zeros; g1.E = E; g1.N = 2 * inter; g1.group_size = group_size;
+    g1.sorted_ids = sti; g1.P = pl.P; g1.expert_ids = eid; g1.ntp = ntp; g1.top_k = top_k;
+    g1.identity_gather = false; g1.num_valid = numel; g1.block_m = pl.block_m; g1.e2m1 = e2m1;
+    g1.epi = Epi::kSiluHalf; g1.out = h; g1.out_top_k = top_k; g1.x_fp8 = xq; g1.act_scales = s1;
+    int rc;
+    if (!mfma) rc = launch_grouped_scalar(g1, s);
+    else rc = pl.decode ? launch_grouped_gemv(g1, s) : launch_grouped_mfma(g1, s);
+    if (rc) return rc;
+    stage_mark(4, s);
+    // act-quant of h over real rows only
+    if ((rc = launch_act_quant(h, false, pl.P, inter, hq, s2, true, s, sti, ntp, numel))) return rc;
+    stage_mark(5, s);
+    // gemm2 (identity gather) -> per-slot rows (decode) or scatter (prefill)
+    GroupedArgs g2{};
+    g2.x_rows = pl.P; g2.K = inter; g2.w = w2; g2.scales = static_cast<const uint16_t*>(w2_scales_f16);
+    g2.zeros = w2_zeros; g2.E = E; g2.N = H; g2.group_size = group_size;
+    g2.sorted_ids = sti; g2.P = pl.P; g2.expert_ids = eid; g2.ntp = ntp; g2.top_k = top_k;
+    g2.identity_gather = true; g2.num_valid = numel; g2.block_m = pl.block_m; g2.e2m1 = e2m1;
+    g2.epi = pl.decode ? Epi::kSlotF32 : Epi::kScatter; g2.out = acc;
+    g2.topk_weights = topk_weights; g2.out_top_k = top_k; g2.x_fp8 = hq; g2.act_scales = s2;
+    if (!mfma) rc = launch_grouped_scalar(g2, s);
+    else rc = pl.decode ? launch_grouped_gemv(g2, s) : launch_grouped_mfma(g2, s);
+    if (rc) return rc;
+    stage_mark(6, s);
+    if (pl.decode)   // slots whose expert is not local / out of range contribute nothing
+        rc = launch_slot_reduce(acc, topk_weights, topk_ids, expert_map, E, T, H, top_k, out,
+                                bf16, s);
+    else
+        rc = launch_cast_f32(acc, T * H, out, bf16, s);
+    stage_mark(7, s);
+    return rc;
+}
+
+}  // extern "C"

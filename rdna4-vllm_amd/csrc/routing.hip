@@ -1,0 +1,314 @@
+// Router top-k softmax and deterministic moe_align_block_size (gfx950).
+//
+// Align contract (test_moe_experts.py:136-152; vLLM call at moe_experts.py:587-589):
+// slots t*top_k+j are grouped by expert ascending and, within an expert, by slot
+// ascending; each expert's run is padded to a multiple of block_m with the sentinel
+// numel; expert_ids[b] names the expert of block b; ntp = total padded rows. Entries past
+// ntp keep the sentinel and expert id -1.
+//
+// Schedule: slots are cut into chunks of kChunk. Per chunk, a work-group builds a
+// per-expert histogram and the stable in-chunk rank of every slot (bucket the slots with
+// LDS atomics, then rank each slot by counting smaller slot ids in its bucket, so the
+// result never depends on atomic order). A single work-group scans the chunk histograms
+// into expert offsets. Small inputs (one chunk) run all three phases in one launch.
+#include "w4a8_common.h"
+#include "w4a8_internal.h"
+
+namespace w4a8 {
+namespace {
+
+constexpr int kChunk = 1024;       // slots per chunk (one per thread)
+constexpr int kAlignThreads = 1024;
+constexpr int kMaxExperts = 1024;  // experts handled by the align kernels
+
+struct ChunkScratch {
+    int hist[kMaxExperts];
+    int boff[kMaxExperts];    // bucket start (exclusive scan of hist)
+    int fill[kMaxExperts];
+    int16_t bucket[kChunk];   // in-chunk slot indices grouped by expert
+    int warp_tot[kAlignThreads / 64];
+};
+
+__device__ __forceinline__ int map_expert(const int32_t* __restrict__ ids, int64_t i,
+                                          const int32_t* __restrict__ emap, int E) {
+    int e = ids[i];
+    if (emap != nullptr) e = (e >= 0 && e < E) ? emap[e] : -1;
+    return (e >= 0 && e < E) ? e : -1;
+}
+
+// Block-wide exclusive scan of one int per thread (1024 threads, wave64).
+__device__ int block_exclusive_scan(int v, int* warp_tot, int& total) {
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    int x = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(x, o, 64);
+        if (lane >= o) x += y;
+    }
+    if (lane == 63) warp_tot[wid] = x;
+    __syncthreads();
+    if (wid == 0) {
+        int t = (lane < kAlignThreads / 64) ? warp_tot[lane] : 0;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int y = __shfl_up(t, o, 64);
+            if (lane >= o) t += y;
+        }
+        if (lane < kAlignThreads / 64) warp_tot[lane] = t;
+    }
+    __syncthreads();
+    const int before = (wid > 0) ? warp_tot[wid - 1] : 0;
+    total = warp_tot[kAlignThreads / 64 - 1];
+    __syncthreads();
+    return before + x - v;
+}
+
+// Phase A for one chunk: histogram, buckets and the stable rank of this thread's slot.
+// Returns the expert (or -1) of slot `base + threadIdx.x`, writes its rank.
+__device__ int chunk_rank(const int32_t* __restrict__ ids, int64_t numel, int64_t base,
+                          const int32_t* __restrict__ emap, int E, ChunkScratch& s,
+                          int& rank) {
+    const int tid = threadIdx.x;
+    for (int e = tid; e < E; e += kAlignThreads) { s.hist[e] = 0; s.fill[e] = 0; }
+    __syncthreads();
+    const int64_t i = base + tid;
+    const int e = (i < numel) ? map_expert(ids, i, emap, E) : -1;
+    if (e >= 0) atomicAdd(&s.hist[e], 1);
+    __syncthreads();
+    // bucket offsets: scan hist over experts (E <= 1024 -> one element per thread)
+    int total;
+    const int h = (tid < E) ? s.hist[tid] : 0;
+    const int off = block_exclusive_scan(h, s.warp_tot, total);
+    if (tid < E) s.boff[tid] = off;
+    __syncthreads();
+    if (e >= 0) {
+        const int p = atomicAdd(&s.fill[e], 1);
+        s.bucket[s.boff[e] + p] = (int16_t)tid;
+    }
+    __syncthreads();
+    rank = 0;
+    if (e >= 0) {
+        const int b0 = s.boff[e], n = s.hist[e];
+        for (int q = 0; q < n; ++q) rank += (s.bucket[b0 + q] < tid) ? 1 : 0;
+    }
+    return e;
+}
+
+// Writes expert_ids, the padding sentinels and ntp from per-expert totals `cnt` and
+// padded offsets `eoff` (both in LDS). One thread per expert.
+__device__ void write_layout(const int* cnt, const int* eoff, int E, int64_t block_m,
+                             int64_t numel, int total_padded, int32_t* __restrict__ sorted_ids,
+                             int64_t sorted_len, int32_t* __restrict__ expert_ids,
+                             int32_t* __restrict__ ntp) {
+    const int tid = threadIdx.x;
+    for (int e = tid; e < E; e += kAlignThreads) {
+        const int c = cnt[e];
+        if (c == 0) continue;
+        const int o = eoff[e];
+        const int padded = (int)((c + block_m - 1) / block_m * block_m);
+        for (int r = o + c; r < o + padded; ++r) sorted_ids[r] = (int32_t)numel;
+        for (int b = (int)(o / block_m); b < (int)((o + padded) / block_m); ++b)
+            expert_ids[b] = e;
+    }
+    for (int64_t r = total_padded + tid; r < sorted_len; r += kAlignThreads)
+        sorted_ids[r] = (int32_t)numel;
+    for (int64_t b = total_padded / block_m + tid; b < sorted_len / block_m; b += kAlignThreads)
+        expert_ids[b] = -1;
+    if (tid == 0) ntp[0] = total_padded;
+}
+
+// Single launch for numel <= kChunk.
+__global__ void __launch_bounds__(kAlignThreads) align_small_kernel(
+    const int32_t* __restrict__ ids, int64_t numel, int E, int64_t block_m,
+    const int32_t* __restrict__ emap, int32_t* __restrict__ sorted_ids, int64_t sorted_len,
+    int32_t* __restrict__ expert_ids, int32_t* __restrict__ ntp) {
+    __shared__ ChunkScratch s;
+    __shared__ int eoff[kMaxExperts];
+    int rank;
+    const int e = chunk_rank(ids, numel, 0, emap, E, s, rank);
+    const int tid = threadIdx.x;
+    int total;
+    const int padded = (tid < E) ? (int)((s.hist[tid] + block_m - 1) / block_m * block_m) : 0;
+    const int off = block_exclusive_scan(padded, s.warp_tot, total);
+    if (tid < E) eoff[tid] = off;
+    __syncthreads();
+    if (e >= 0) sorted_ids[eoff[e] + rank] = tid;
+    write_layout(s.hist, eoff, E, block_m, numel, total, sorted_ids, sorted_len, expert_ids,
+                 ntp);
+}
+
+// Multi-chunk phase 1: per-chunk histograms -> counts[chunk][E].
+__global__ void __launch_bounds__(kAlignThreads) align_count_kernel(
+    const int32_t* __restrict__ ids, int64_t numel, int E, const int32_t* __restrict__ emap,
+    int32_t* __restrict__ counts) {
+    __shared__ int hist[kMaxExperts];
+    const int tid = threadIdx.x;
+    for (int e = tid; e < E; e += kAlignThreads) hist[e] = 0;
+    __syncthreads();
+    const int64_t i = (int64_t)blockIdx.x * kChunk + tid;
+    const int e = (i < numel) ? map_expert(ids, i, emap, E) : -1;
+    if (e >= 0) atomicAdd(&hist[e], 1);
+    __syncthreads();
+    for (int x = tid; x < E; x += kAlignThreads) counts[(int64_t)blockIdx.x * E + x] = hist[x];
+}
+
+// Multi-chunk phase 2 (one work-group): counts -> per-chunk expert bases (in place),
+// padded expert offsets, layout.
+__global__ void __launch_bounds__(kAlignThreads) align_scan_kernel(
+    int32_t* __restrict__ counts, int nchunks, int E, int64_t block_m, int64_t numel,
+    int32_t* __restrict__ eoff_out, int32_t* __restrict__ sorted_ids, int64_t sorted_len,
+    int32_t* __restrict__ expert_ids, int32_t* __restrict__ ntp) {
+    __shared__ int cnt[kMaxExperts];
+    __shared__ int eoff[kMaxExperts];
+    __shared__ int warp_tot[kAlignThreads / 64];
+    const int tid = threadIdx.x;
+    if (tid < E) {
+        int run = 0;
+        for (int c = 0; c < nchunks; ++c) {
+            const int v = counts[(int64_t)c * E + tid];
+            counts[(int64_t)c * E + tid] = run;
+            run += v;
+        }
+        cnt[tid] = run;
+    }
+    __syncthreads();
+    int total;
+    const int padded = (tid < E) ? (int)((cnt[tid] + block_m - 1) / block_m * block_m) : 0;
+    const int off = block_exclusive_scan(padded, warp_tot, total);
+    if (tid < E) { eoff[tid] = off; eoff_out[tid] = off; }
+    __syncthreads();
+    write_layout(cnt, eoff, E, block_m, numel, total, sorted_ids, sorted_len, expert_ids, ntp);
+}
+
+// Multi-chunk phase 3: stable placement.
+__global__ void __launch_bounds__(kAlignThreads) align_place_kernel(
+    const int32_t* __restrict__ ids, int64_t numel, int E, const int32_t* __restrict__ emap,
+    const int32_t* __restrict__ chunk_base, const int32_t* __restrict__ eoff,
+    int32_t* __restrict__ sorted_ids) {
+    __shared__ ChunkScratch s;
+    int rank;
+    const int64_t base = (int64_t)blockIdx.x * kChunk;
+    const int e = chunk_rank(ids, numel, base, emap, E, s, rank);
+    if (e >= 0)
+        sorted_ids[eoff[e] + chunk_base[(int64_t)blockIdx.x * E + e] + rank] =
+            (int32_t)(base + threadIdx.x);
+}
+
+// ---- router: one wave per token ----
+constexpr int kRouterMaxPerLane = 16;   // E <= 1024
+
+__global__ void __launch_bounds__(256) topk_softmax_kernel(
+    const float* __restrict__ logits, int64_t T, int E, int top_k, bool renorm,
+    float* __restrict__ tw, int32_t* __restrict__ tids) {
+    const int lane = threadIdx.x & 63;
+    const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= T) return;
+    const float* l = logits + t * E;
+    float v[kRouterMaxPerLane];
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < kRouterMaxPerLane; ++i) {
+        const int e = lane + 64 * i;
+        v[i] = (e < E) ? l[e] : -INFINITY;
+        m = fmaxf(m, v[i]);
+    }
+    m = wave_max(m);
+    float ssum = 0.f;
+#pragma unroll
+    for (int i = 0; i < kRouterMaxPerLane; ++i) {
+        const int e = lane + 64 * i;
+        if (e < E) ssum += expf(v[i] - m);
+    }
+    ssum = wave_sum(ssum);
+    uint32_t taken = 0;   // bit i: v[i] already selected
+    float wsel = 0.f;     // this lane's output weight (lane j < top_k holds pick j)
+    int isel = 0;
+    float sum_sel = 0.f;
+    for (int j = 0; j < top_k; ++j) {
+        // best (value desc, expert asc) among this lane's untaken entries
+        float bv = -INFINITY;
+        int be = 0x7FFFFFFF;
+#pragma unroll
+        for (int i = 0; i < kRouterMaxPerLane; ++i) {
+            const int e = lane + 64 * i;
+            if (e < E && !(taken & (1u << i)) && (v[i] > bv || (v[i] == bv && e < be))) {
+                bv = v[i];
+                be = e;
+            }
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const float ov = __shfl_xor(bv, o, 64);
+            const int oe = __shfl_xor(be, o, 64);
+            if (ov > bv || (ov == bv && oe < be)) { bv = ov; be = oe; }
+        }
+        if ((be & 63) == lane) taken |= 1u << (be >> 6);
+        const float p = expf(bv - m) / ssum;
+        sum_sel += p;
+        if (lane == j) { wsel = p; isel = be; }
+    }
+    if (lane < top_k) {
+        tw[t * top_k + lane] = renorm ? wsel / sum_sel : wsel;
+        tids[t * top_k + lane] = isel;
+    }
+}
+
+}  // namespace
+
+size_t align_workspace_bytes(int64_t numel, int64_t num_experts) {
+    if (numel <= kChunk) return 0;
+    const int64_t nchunks = (numel + kChunk - 1) / kChunk;
+    WorkspaceSize s;
+    s.take<int32_t>((size_t)(nchunks * num_experts));
+    s.take<int32_t>((size_t)num_experts);
+    return s.used;
+}
+
+int launch_align(const int32_t* ids, int64_t numel, int64_t E, int64_t block_m,
+                 const int32_t* emap, int32_t* sorted_ids, int64_t sorted_len,
+                 int32_t* expert_ids, int32_t* ntp, void* ws, size_t ws_bytes,
+                 hipStream_t stream) {
+    if (E > kMaxExperts) {
+        set_error("moe_align: num_experts must be <= 1024");
+        return W4A8_ERR_INVALID;
+    }
+    if (numel <= kChunk) {
+        align_small_kernel<<<1, kAlignThreads, 0, stream>>>(ids, numel, (int)E, block_m, emap,
+                                                           sorted_ids, sorted_len, expert_ids,
+                                                           ntp);
+        return check_launch("align_small_kernel");
+    }
+    const int64_t nchunks = (numel + kChunk - 1) / kChunk;
+    Workspace w(ws, ws_bytes);
+    int32_t* counts = w.take<int32_t>((size_t)(nchunks * E));
+    int32_t* eoff = w.take<int32_t>((size_t)E);
+    if (ws == nullptr || !w.ok()) {
+        set_error("moe_align: workspace too small");
+        return W4A8_ERR_WORKSPACE;
+    }
+    align_count_kernel<<<(unsigned)nchunks, kAlignThreads, 0, stream>>>(ids, numel, (int)E, emap,
+                                                                        counts);
+    if (int rc = check_launch("align_count_kernel")) return rc;
+    align_scan_kernel<<<1, kAlignThreads, 0, stream>>>(counts, (int)nchunks, (int)E, block_m,
+                                                       numel, eoff, sorted_ids, sorted_len,
+                                                       expert_ids, ntp);
+    if (int rc = check_launch("align_scan_kernel")) return rc;
+    align_place_kernel<<<(unsigned)nchunks, kAlignThreads, 0, stream>>>(ids, numel, (int)E, emap,
+                                                                        counts, eoff,
+                                                                        sorted_ids);
+    return check_launch("align_place_kernel");
+}
+
+int launch_topk_softmax(const float* logits, int64_t T, int64_t E, int64_t top_k, bool renorm,
+                        float* w, int32_t* ids, hipStream_t stream) {
+    if (E > 64 * kRouterMaxPerLane || top_k > 64 || top_k > E) {
+        set_error("topk_softmax: need E <= 1024 and top_k <= min(64, E)");
+        return W4A8_ERR_INVALID;
+    }
+    if (T == 0) return W4A8_OK;
+    topk_softmax_kernel<<<(unsigned)((T + 3) / 4), 256, 0, stream>>>(logits, T, (int)E,
+                                                                    (int)top_k, renorm, w, ids);
+    return check_launch("topk_softmax_kernel");
+}
+
+}  // namespace w4a8

@@ -1,0 +1,136 @@
+// Shared device helpers for the gfx950 W4A8 MoE kernels.
+//
+// Numeric contract (patcarter883/rdna4-vllm, w4a8_fp8_wmma/):
+//   * activations: per-row s = max(absmax/448, 1e-8), q = e4m3_RNE(x * (1/s))
+//     (moe_kernel.hip:87-127);
+//   * weights: the e4m3 byte of (nibble - zp), exact because |nibble - zp| <= 15
+//     (tile_config.h:42-45); zp = 8 when no zero-points; E2M1 codebook when
+//     weight_is_e2m1 (tile_config.h:59-71);
+//   * per 128-wide K group: fp32 partial sum, then run += partial * scale[n, g]
+//     (moe_gemm_tiled.h:144-151).
+//
+// fp8 byte order of activation scratch ("k8 interleave"): within every 8-byte block
+// the byte at position p holds k = 8*block + kPerm8[p], kPerm8 = {0,2,4,6,1,3,5,7}.
+// That is the order the nibble decoder below produces for weights (low nibbles of a
+// dword, then high nibbles), so A and B fragments pair the same k in every MFMA
+// without re-interleaving the decoded weights.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <hip/hip_bf16.h>
+#include <cstdint>
+
+namespace w4a8 {
+
+constexpr int kPackFactor = 8;      // int4 nibbles per int32 word
+constexpr float kE4m3Max = 448.0f;
+constexpr float kActScaleFloor = 1e-8f;
+constexpr int kMaxGroupSize = 128;
+constexpr int kNumDecodeTables = 17;  // zp = 0..15, then the E2M1 codebook
+constexpr int kE2m1Table = 16;
+
+using v8i = int __attribute__((ext_vector_type(8)));
+using v4i = int __attribute__((ext_vector_type(4)));
+using v4f = float __attribute__((ext_vector_type(4)));
+using v16f = float __attribute__((ext_vector_type(16)));
+
+// Nibble -> e4m3 byte tables, 4 dwords each (entry i in byte i%4 of dword i/4).
+// Table z < 16 holds e4m3(n - z) for n = 0..15; table 16 holds e4m3 of the OCP E2M1
+// codebook {0,.5,1,1.5,2,3,4,6,-0,-.5,...,-6}. Every entry is exact in e4m3.
+static __constant__ uint32_t g_decode_tables[kNumDecodeTables][4] = {
+    {0x44403800u, 0x4E4C4A48u, 0x53525150u, 0x57565554u},  // zp=0
+    {0x403800B8u, 0x4C4A4844u, 0x5251504Eu, 0x56555453u},  // zp=1
+    {0x3800B8C0u, 0x4A484440u, 0x51504E4Cu, 0x55545352u},  // zp=2
+    {0x00B8C0C4u, 0x48444038u, 0x504E4C4Au, 0x54535251u},  // zp=3
+    {0xB8C0C4C8u, 0x44403800u, 0x4E4C4A48u, 0x53525150u},  // zp=4
+    {0xC0C4C8CAu, 0x403800B8u, 0x4C4A4844u, 0x5251504Eu},  // zp=5
+    {0xC4C8CACCu, 0x3800B8C0u, 0x4A484440u, 0x51504E4Cu},  // zp=6
+    {0xC8CACCCEu, 0x00B8C0C4u, 0x48444038u, 0x504E4C4Au},  // zp=7
+    {0xCACCCED0u, 0xB8C0C4C8u, 0x44403800u, 0x4E4C4A48u},  // zp=8
+    {0xCCCED0D1u, 0xC0C4C8CAu, 0x403800B8u, 0x4C4A4844u},  // zp=9
+    {0xCED0D1D2u, 0xC4C8CACCu, 0x3800B8C0u, 0x4A484440u},  // zp=10
+    {0xD0D1D2D3u, 0xC8CACCCEu, 0x00B8C0C4u, 0x48444038u},  // zp=11
+    {0xD1D2D3D4u, 0xCACCCED0u, 0xB8C0C4C8u, 0x44403800u},  // zp=12
+    {0xD2D3D4D5u, 0xCCCED0D1u, 0xC0C4C8CAu, 0x403800B8u},  // zp=13
+    {0xD3D4D5D6u, 0xCED0D1D2u, 0xC4C8CACCu, 0x3800B8C0u},  // zp=14
+    {0xD4D5D6D7u, 0xD0D1D2D3u, 0xC8CACCCEu, 0x00B8C0C4u},  // zp=15
+    {0x3C383000u, 0x4C484440u, 0xBCB8B080u, 0xCCC8C4C0u},  // E2M1
+};
+
+__device__ __forceinline__ uint32_t cvt_f32_e4m3(float v) {
+    return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(v, v, 0, false)) & 0xFFu;
+}
+// Four floats -> four e4m3 bytes (a in byte 0 ... d in byte 3).
+__device__ __forceinline__ uint32_t pack4_e4m3(float a, float b, float c, float d) {
+    const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+    return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(c, d, lo, true));
+}
+__device__ __forceinline__ float e4m3_to_f32(uint32_t byte) {
+    return __builtin_amdgcn_cvt_f32_fp8(static_cast<int>(byte), 0);
+}
+
+// 16-entry byte lookup of each byte of x (values 0..15) in table t.
+// v_perm_b32 selects from 8 bytes; entries 8..15 come from a second select, and the
+// third select turns (x + 5) >= 13 into an all-ones byte mask for x >= 8.
+__device__ __forceinline__ uint32_t lut16(uint32_t x, uint4 t) {
+    const uint32_t a = __builtin_amdgcn_perm(t.y, t.x, x);
+    const uint32_t b = __builtin_amdgcn_perm(t.w, t.z, x ^ 0x08080808u);
+    const uint32_t m = __builtin_amdgcn_perm(0u, 0u, x + 0x05050505u);
+    return (a & ~m) | (b & m);
+}
+
+// One int32 of 8 nibbles (k = 0..7) -> 8 e4m3 bytes in k8-interleave order:
+// lo = {k0,k2,k4,k6}, hi = {k1,k3,k5,k7}.
+__device__ __forceinline__ void decode8(uint32_t w, uint4 t, uint32_t& lo, uint32_t& hi) {
+    lo = lut16(w & 0x0F0F0F0Fu, t);
+    hi = lut16((w >> 4) & 0x0F0F0F0Fu, t);
+}
+
+__device__ __forceinline__ uint4 load_table(int idx) {
+    return make_uint4(g_decode_tables[idx][0], g_decode_tables[idx][1],
+                      g_decode_tables[idx][2], g_decode_tables[idx][3]);
+}
+
+// Decode-table index for output row n, group g of one expert's packed zero-points
+// (E, N/8, G) (moe_kernel.hip:172-176: (z[n/8][g] >> 4*(n%8)) & 0xF).
+__device__ __forceinline__ int table_index(const int* __restrict__ zeros_e, int n, int g,
+                                           int num_groups, bool e2m1) {
+    if (e2m1) return kE2m1Table;
+    if (zeros_e == nullptr) return 8;
+    return (zeros_e[(n >> 3) * num_groups + g] >> ((n & 7) * 4)) & 0xF;
+}
+
+// Position of k inside the k8-interleaved activation row.
+__device__ __host__ __forceinline__ int k8_pos(int k) {
+    const int r = k & 7;
+    return (k & ~7) | ((r >> 1) | ((r & 1) << 2));
+}
+
+// Wave64 reductions.
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// Activation scale from an fp32 absmax (moe_kernel.hip:117-118).
+__device__ __forceinline__ float act_scale_from_absmax(float amax) {
+    float s = amax / kE4m3Max;
+    if (s < kActScaleFloor) s = kActScaleFloor;
+    return s;
+}
+
+// vLLM silu_and_mul on fp16 gate/up stores (moe_kernel.hip:555-561).
+__device__ __forceinline__ __half silu_mul_h(__half gate_h, __half up_h) {
+    const float g = __half2float(gate_h);
+    const __half silu_h = __float2half(g / (1.0f + expf(-g)));
+    return __hmul(silu_h, up_h);
+}
+
+}  // namespace w4a8

@@ -1,0 +1,112 @@
+// Host-side internals shared by the C-ABI translation units (not part of the ABI).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <cstdint>
+#include <cstddef>
+#include <string>
+
+#include "../../include/w4a8_moe.h"
+
+namespace w4a8 {
+
+// Thread-local error slot behind w4a8_last_error().
+void set_error(const std::string& msg);
+void clear_error();
+
+// Returns W4A8_ERR_HIP (with message) if the last launch failed, else W4A8_OK.
+int check_launch(const char* what);
+
+inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// Bump allocator over a caller workspace (256-byte aligned carve-outs).
+struct Workspace {
+    char* base;
+    size_t size;
+    size_t used = 0;
+    Workspace(void* p, size_t n) : base(static_cast<char*>(p)), size(n) {}
+    template <typename T>
+    T* take(size_t count) {
+        used = align_up(used, 256);
+        T* p = reinterpret_cast<T*>(base + used);
+        used += count * sizeof(T);
+        return p;
+    }
+    bool ok() const { return used <= size; }
+};
+
+// Bytes a Workspace needs for a sequence of carve-outs.
+struct WorkspaceSize {
+    size_t used = 0;
+    template <typename T>
+    void take(size_t count) { used = align_up(used, 256) + count * sizeof(T); }
+};
+
+// ---- launchers implemented in the .hip files (all enqueue on `stream`) ----
+int launch_act_quant(const void* x, bool x_bf16, int64_t rows, int64_t K, uint8_t* x_fp8,
+                     float* scales, bool k8_interleave, hipStream_t stream,
+                     const int32_t* sorted_ids = nullptr, const int32_t* ntp = nullptr,
+                     int64_t num_valid = 0);
+int launch_dequant(const int32_t* w, const int32_t* z, int64_t E, int64_t N, int64_t K,
+                   int64_t gs, bool e2m1, uint8_t* out, hipStream_t stream);
+int launch_silu_and_mul(const void* in, int64_t rows, int64_t inter, void* out,
+                        hipStream_t stream);
+int launch_topk_softmax(const float* logits, int64_t T, int64_t E, int64_t top_k,
+                        bool renorm, float* w, int32_t* ids, hipStream_t stream);
+size_t align_workspace_bytes(int64_t numel, int64_t num_experts);
+int launch_align(const int32_t* topk_ids, int64_t numel, int64_t E, int64_t block_m,
+                 const int32_t* expert_map, int32_t* sorted_ids, int64_t sorted_len,
+                 int32_t* expert_ids, int32_t* ntp, void* ws, size_t ws_bytes,
+                 hipStream_t stream);
+int launch_gather_reduce(const void* out2, int64_t P, int64_t N, const int32_t* sorted_ids,
+                         const float* tw, int64_t m_tk, const int32_t* ntp, int64_t top_k,
+                         float* out, int32_t* slot_to_row, hipStream_t stream);
+// out[t, n] = cast(sum_{j asc} w[t*k+j] * y[(t*k+j), n]) with y fp32 (rows = T*k);
+// slots whose (mapped) expert is outside [0, E) are skipped.
+int launch_slot_reduce(const float* y, const float* tw, const int32_t* topk_ids,
+                       const int32_t* expert_map, int64_t E, int64_t T, int64_t N,
+                       int64_t top_k, void* out, bool out_bf16, hipStream_t stream);
+int launch_cast_f32(const float* in, int64_t n, void* out, bool out_bf16, hipStream_t stream);
+int launch_zero_f32(float* p, int64_t n, hipStream_t stream);
+
+// Grouped GEMM epilogue modes.
+enum class Epi : int {
+    kHalf = 0,      // out[row_pad, n] = fp16(run * asc)            (P, N)
+    kSiluHalf = 1,  // out[row_pad, n] = silu_mul(gate, up)          (P, N/2)
+    kScatter = 2,   // atomicAdd(out[slot / top_k, n], w[slot] * run * asc)
+    kSlotF32 = 3,   // out[slot, n] = run * asc (fp32, rows = M*top_k)
+};
+
+struct GroupedArgs {
+    const void* x;          // activation rows: fp16 (or bf16 when x_bf16)
+    bool x_bf16;
+    int64_t x_rows;         // rows of x
+    int64_t K;
+    const int32_t* w;       // (E, N, K/8)
+    const uint16_t* scales; // (E, N, G) fp16 bits
+    const int32_t* zeros;   // (E, N/8, G) or null
+    int64_t E, N, group_size;
+    const int32_t* sorted_ids;
+    int64_t P;
+    const int32_t* expert_ids;
+    const int32_t* ntp;
+    int64_t top_k;          // gather row = slot / top_k (ignored when identity)
+    bool identity_gather;   // gather row = padded row index
+    int64_t num_valid;      // slots >= num_valid are padding
+    int64_t block_m;
+    bool e2m1;
+    Epi epi;
+    void* out;              // see Epi
+    const float* topk_weights;  // kScatter
+    int64_t out_top_k;      // kScatter: token = slot / out_top_k
+    // scratch for the prequantised path
+    uint8_t* x_fp8;         // (x_rows, K) k8-interleaved, or null
+    float* act_scales;      // (x_rows,)
+};
+
+int launch_grouped_scalar(const GroupedArgs& a, hipStream_t stream);
+int launch_grouped_mfma(const GroupedArgs& a, hipStream_t stream);   // prefill tiles
+int launch_grouped_gemv(const GroupedArgs& a, hipStream_t stream);   // decode GEMV
+bool mfma_supported(int64_t K, int64_t group_size);
+
+}  // namespace w4a8

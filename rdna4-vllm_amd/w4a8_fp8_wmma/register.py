@@ -1,0 +1,29 @@
+"""vLLM general-plugin entry point (w4a8_fp8_wmma/w4a8_fp8_wmma/register.py:42-175).
+
+``register()`` installs the MoeWNA16 MoE hook. The dense-linear and other MoE hooks of
+the reference are outside this package's scope (the W4A8 MoE expert path only).
+Removed env knobs raise at boot, like the reference (register.py:29-39).
+"""
+from __future__ import annotations
+
+import os
+
+_REMOVED_ENV = ("VLLM_ROCM_W4A8_FP8_WMMA_VERSION", "VLLM_ROCM_W4A8_FP8_WMMA_MOE_VERSION")
+
+
+def _check_removed_w4a8_env() -> None:
+    for name in _REMOVED_ENV:
+        if name in os.environ:
+            raise RuntimeError(f"{name} is removed; use the descriptive kernel-name env vars")
+
+
+def register() -> None:
+    if os.environ.get("VLLM_ROCM_USE_W4A8_FP8_WMMA", "1") != "1":
+        print("[w4a8_fp8_wmma] disabled via VLLM_ROCM_USE_W4A8_FP8_WMMA")
+        return
+    _check_removed_w4a8_env()
+    from .moe_experts import register_moe_wna16
+    try:
+        register_moe_wna16()
+    except ImportError as e:
+        print(f"[w4a8_fp8_wmma] MoE hook not installed: {e}")

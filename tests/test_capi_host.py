@@ -1,0 +1,240 @@
+"""C-ABI library exports, argument validation and host-side API logic (CPU only).
+
+No kernel is launched here: every C call below fails validation before touching HIP.
+"""
+import ctypes
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+import w4a8_fp8_wmma as W
+from w4a8_fp8_wmma import _lib, moe_experts
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "w4a8_moe.h")
+
+
+def header_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"W4A8_API\s+[\w\s\*]+?\b(w4a8_\w+)\s*\(", text)))
+
+
+def test_library_exports_exactly_the_header():
+    syms = header_symbols()
+    assert len(syms) >= 18
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)],
+                         capture_output=True, text=True, check=True).stdout
+    exported = sorted(l.split()[-1] for l in out.splitlines() if " T " in l and "w4a8_" in l)
+    assert exported == syms
+    assert sorted(_lib.SIGNATURES) == syms
+    cdll = ctypes.CDLL(str(_lib.LIB_PATH))
+    for s in syms:
+        assert getattr(cdll, s) is not None
+
+
+def test_abi_version_and_sizes():
+    L = _lib.lib
+    assert L.w4a8_abi_version() == 1
+    assert L.w4a8_moe_align_sorted_len(256, 256, 16) == O.align_alloc_len(256, 256, 16)
+    assert L.w4a8_moe_align_sorted_len(32768, 256, 64) == 48896      # SURVEY C4 P_alloc
+    assert L.w4a8_moe_align_sorted_len(8, 256, 8) == 1800            # C2 with block_m 8
+    assert L.w4a8_moe_align_workspace_size(256, 256) == 0            # one-chunk path
+    assert L.w4a8_moe_align_workspace_size(32768, 256) > 0
+    assert L.w4a8_moe_gemm_workspace_size(32, 2048) >= 32 * 2048 + 32 * 4
+    assert L.w4a8_moe_apply_workspace_size(32, 2048, 512, 256, 8) > 0
+
+
+def _err():
+    return _lib.lib.w4a8_last_error().decode()
+
+
+def test_validation_errors_are_reported_without_gpu():
+    L = _lib.lib
+    # K not a multiple of 8
+    rc = L.w4a8_mmq_fp8_moe_gemm(1, 4, 12, 1, 1, None, 2, 16, 16, 1, 16, 1, 1, 1, 16, 6, 0,
+                                 1, 1, 1 << 20, None)
+    assert rc == 1 and "multiple of 8" in _err()
+    # bad kernel id
+    rc = L.w4a8_mmq_fp8_moe_gemm(1, 4, 256, 1, 1, None, 2, 16, 128, 1, 16, 1, 1, 1, 16, 5, 0,
+                                 1, 1, 1 << 20, None)
+    assert rc == 1 and "kernel id" in _err()
+    # gemv block_m cap
+    rc = L.w4a8_mmq_fp8_moe_gemm(1, 4, 256, 1, 1, None, 2, 16, 128, 1, 128, 1, 1, 1, 128, 7, 0,
+                                 1, 1, 1 << 20, None)
+    assert rc == 1 and "gemv" in _err()
+    # fused silu needs wmma
+    rc = L.w4a8_mmq_fp8_moe_gemm1_silu(1, 4, 256, 1, 1, None, 2, 32, 128, 1, 16, 1, 1, 1, 16,
+                                       7, 0, 1, 1, 1 << 20, None)
+    assert rc == 1 and "wmma" in _err()
+    # e2m1 with zero-points
+    rc = L.w4a8_dequant_fp8(1, 1, 1, 8, 128, 128, 1, 1, None)
+    assert rc == 1 and "symmetric" in _err()
+    # align: wrong sorted_len
+    rc = L.w4a8_moe_align_block_size(1, 16, 8, 4, None, 1, 17, 1, 1, None, 0, None)
+    assert rc == 1 and "sorted_len" in _err()
+    # dense: retired v3 id
+    rc = L.w4a8_mmq_fp8_gemm(1, 16, 256, 1, 1, None, 64, 128, 3, 0, 1, 1, 1 << 20, None)
+    assert rc == 1 and "dense kernel" in _err()
+    # group size > 128
+    rc = L.w4a8_mmq_fp8_gemm(1, 16, 512, 1, 1, None, 64, 256, 0, 0, 1, 1, 1 << 20, None)
+    assert rc == 1 and "group_size" in _err()
+    # moe_apply bad dtype
+    rc = L.w4a8_moe_apply(1, 7, 4, 256, 128, 8, 2, 128, 1, 1, None, 1, 1, None, 1, 1, None, 0,
+                          1, 1, 1 << 20, None)
+    assert rc == 1 and "dtype" in _err()
+    with pytest.raises(RuntimeError, match="multiple of 8"):
+        _lib.check(L.w4a8_act_quant_fp8(1, 4, 12, 1, 1, 0, None), "act_quant")
+
+
+def test_kernel_name_maps():
+    assert W._resolve_moe_kernel("scalar") == 0
+    assert W._resolve_moe_kernel("wmma") == 6
+    assert W._resolve_moe_kernel("gemv") == 7
+    assert W._resolve_dense_kernel("decode_gemv") == 11
+    with pytest.raises(ValueError):
+        W._resolve_moe_kernel("v5")
+    with pytest.raises(TypeError):
+        W._resolve_moe_kernel(6)
+    with pytest.raises(ValueError):
+        W._resolve_dense_kernel("nope")
+    with pytest.raises(TypeError):
+        W._resolve_dense_kernel(5)
+
+
+def test_op_schemas_match_reference():
+    s = torch.ops.w4a8_fp8_wmma.mmq_fp8_moe_gemm_scatter.default._schema
+    assert "Tensor(a!) output" in str(s)
+    for name in ("mmq_fp8_gemm", "mmq_fp8_moe_gemm", "mmq_fp8_moe_gemm1_silu",
+                 "mmq_fp8_moe_gemm_scatter", "mmq_fp8_moe_gather_reduce"):
+        op = getattr(torch.ops.w4a8_fp8_wmma, name).default
+        assert torch.Tag.pt2_compliant_tag in op.tags
+
+
+def test_fake_impls_shapes():
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    with FakeTensorMode():
+        x = torch.empty(8, 256, dtype=torch.float16)
+        w = torch.empty(4, 64, 32, dtype=torch.int32)
+        s = torch.empty(4, 64, 2, dtype=torch.float16)
+        z = torch.empty(0, dtype=torch.int32)
+        sti = torch.empty(128, dtype=torch.int32)
+        eid = torch.empty(8, dtype=torch.int32)
+        ntp = torch.empty(1, dtype=torch.int32)
+        o = torch.ops.w4a8_fp8_wmma.mmq_fp8_moe_gemm(x, w, s, z, sti, eid, ntp, 2, 16, 6)
+        assert o.shape == (128, 64) and o.dtype == torch.float16
+        o = torch.ops.w4a8_fp8_wmma.mmq_fp8_moe_gemm1_silu(x, w, s, z, sti, eid, ntp, 2, 16, 6)
+        assert o.shape == (128, 32)
+        tw = torch.empty(16, dtype=torch.float32)
+        g = torch.ops.w4a8_fp8_wmma.mmq_fp8_moe_gather_reduce(o, sti, tw, ntp, 2)
+        assert g.shape == (8, 32) and g.dtype == torch.float32
+        d = torch.ops.w4a8_fp8_wmma.mmq_fp8_gemm(x, w[0], s[0], z, 0)
+        assert d.shape == (8, 64)
+        out = torch.ops.vllm.w4a8_moe_apply(x, w, w, s, s, None, None, tw.view(8, 2),
+                                             sti[:16].view(8, 2), "silu", 4, None, False, "wmma")
+        assert out.shape == x.shape
+
+
+def test_ops_reject_cpu_tensors():
+    x = torch.zeros(4, 256, dtype=torch.float16)
+    w = torch.zeros(2, 16, 32, dtype=torch.int32)
+    s = torch.zeros(2, 16, 2, dtype=torch.float16)
+    sti = torch.zeros(16, dtype=torch.int32)
+    with pytest.raises((RuntimeError, NotImplementedError)):
+        W.mmq_fp8_moe_gemm(x, w, s, sti, sti[:1], sti[:1], 2, 16)
+
+
+def test_torch_converters_match_oracle():
+    r = np.random.default_rng(30)
+    E, K, N, g = 3, 256, 64, 32
+    q = r.integers(0, 16, (E, K, N))
+    zz = r.integers(0, 16, (E, K // g, N))
+    s = r.uniform(0.005, 0.02, (E, K // g, N)).astype(np.float16)
+    qw, qz = O.awq_pack(q), O.awq_pack(zz)
+    w, sc, z = moe_experts._awq_moe_to_op_layout(torch.from_numpy(qw), torch.from_numpy(s),
+                                                 torch.from_numpy(qz), g)
+    wo, so, zo = O.awq_to_op_layout(qw, s, qz)
+    assert np.array_equal(w.numpy(), wo) and np.array_equal(z.numpy(), zo)
+    assert np.array_equal(sc.numpy(), so)
+    # MoeWNA16 zero-copy view
+    u8w = np.stack([O.convert_awq_tensor(qw[e], "qweight") for e in range(E)])
+    u8z = np.stack([O.convert_awq_tensor(qz[e], "qzeros") for e in range(E)])
+    tw_, ts_, tz_ = moe_experts._wna16_moe_to_op_layout(
+        torch.from_numpy(u8w), torch.from_numpy(np.swapaxes(s, 1, 2).copy()), torch.from_numpy(u8z))
+    assert np.array_equal(tw_.numpy(), wo) and np.array_equal(tz_.numpy(), zo)
+    # compressed-tensors (GPTQ-packed along K, symmetric)
+    ct = np.zeros((E, K // 8, N), np.int64)
+    for j in range(8):
+        ct |= (q[:, j::8, :] & 0xF) << (4 * j)
+    cw, cs = moe_experts._ct_moe_to_op_layout(torch.from_numpy(ct.astype(np.uint32).view(np.int32)),
+                                              torch.from_numpy(s))
+    assert np.array_equal(O.unpack_nibbles(cw.numpy()), np.swapaxes(q, 1, 2))
+
+
+def test_run_grouped_moe_rejects_non_silu():
+    x = torch.zeros(2, 256, dtype=torch.bfloat16)
+    with pytest.raises(NotImplementedError):
+        moe_experts._run_grouped_moe(x, None, None, None, None, None, None, None,
+                                     torch.zeros(2, 2, dtype=torch.int32), "gelu", 4, None,
+                                     False, "wmma")
+
+
+def test_env_hard_break_and_kernel_env(monkeypatch):
+    monkeypatch.setenv("VLLM_ROCM_W4A8_FP8_WMMA_MOE_VERSION", "6")
+    with pytest.raises(RuntimeError, match="removed"):
+        moe_experts._moe_kernel()
+    monkeypatch.delenv("VLLM_ROCM_W4A8_FP8_WMMA_MOE_VERSION")
+    monkeypatch.setenv("VLLM_ROCM_W4A8_FP8_WMMA_MOE_KERNEL", "bogus")
+    with pytest.raises(RuntimeError, match="invalid"):
+        moe_experts._moe_kernel()
+    monkeypatch.setenv("VLLM_ROCM_W4A8_FP8_WMMA_MOE_KERNEL", "gemv")
+    assert moe_experts._moe_kernel() == "gemv"
+
+
+def test_wna16_hook_with_stand_in_class(monkeypatch):
+    """Drive the patched process/apply with a stand-in MoeWNA16Method (no vLLM)."""
+    calls = {}
+
+    class QC:
+        weight_bits = 4
+        has_zp = True
+
+    class Method:
+        def __init__(self):
+            self.quant_config = QC()
+
+        def process_weights_after_loading(self, layer):
+            calls["process"] = True
+
+        def apply(self, layer, x, topk_weights, topk_ids, shared_experts, shared_experts_input):
+            calls["orig_apply"] = True
+            return "stock"
+
+    moe_experts.install_moe_wna16_hooks(Method)
+    E, N, K, g = 2, 16, 256, 128
+
+    class Layer:
+        group_size = g
+        w13_qweight = torch.nn.Parameter(torch.zeros(E, N, K // 2, dtype=torch.uint8), False)
+        w2_qweight = torch.nn.Parameter(torch.zeros(E, K, N // 4, dtype=torch.uint8), False)
+        w13_scales = torch.nn.Parameter(torch.ones(E, N, K // g), False)
+        w2_scales = torch.nn.Parameter(torch.ones(E, K, 1), False)
+        w13_qzeros = torch.nn.Parameter(torch.zeros(E, N // 2, K // g, dtype=torch.uint8), False)
+        w2_qzeros = torch.nn.Parameter(torch.zeros(E, K // 2, 1, dtype=torch.uint8), False)
+
+    m, layer = Method(), Layer()
+    m.process_weights_after_loading(layer)
+    assert calls["process"] and m._w4a8_wna16
+    assert layer._w4a8_w13.shape == (E, N, K // 8) and layer._w4a8_w13.dtype == torch.int32
+    assert layer._w4a8_w13z.shape == (E, N // 8, K // g)
+    assert layer._w4a8_w13s.dtype == torch.float16
+    # unsupported group size keeps the stock apply
+    layer2 = Layer()
+    layer2.group_size = 256
+    m2 = Method()
+    m2.process_weights_after_loading(layer2)
+    assert m2.apply(layer2, None, None, None) == "stock"

@@ -1,0 +1,246 @@
+"""GPU parity of the individual gfx950 kernels against the CPU oracle, through the C ABI.
+
+Bars: bit-exact for act-quant bytes/scales, dequant bytes, align indices and router ids;
+max|out - ref| / max|ref| <= 1e-2 for fp32-accumulated GEMM outputs.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+import w4a8_fp8_wmma as W
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+REL_TOL = 1e-2
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _need_gpu():
+    assert torch.cuda.is_available(), "GPU tests need a visible MI355X"
+
+
+def maxrel(got, ref):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    return float(np.abs(got - ref).max() / max(np.abs(ref).max(), 1e-30))
+
+
+def rng(seed):
+    return np.random.default_rng(seed)
+
+
+# --------------------------------------------------------------------------- #
+# act-quant / dequant / silu
+# --------------------------------------------------------------------------- #
+@pytest.mark.parametrize("k8", [False, True])
+@pytest.mark.parametrize("K", [128, 512, 2048, 4096])
+def test_act_quant_bit_exact(k8, K):
+    r = rng(K)
+    x = (r.standard_normal((67, K)) * np.exp2(r.integers(-8, 8, (67, 1)))).astype(np.float16)
+    x[0] = 0
+    x[1] = np.float16(6e-8)
+    x[2, ::7] = np.float16(-65504)
+    q, s = W.act_quant_fp8(torch.from_numpy(x).to(DEV), k8_interleave=k8)
+    qo, so = O.act_quant(x)
+    if k8:   # byte p of each 8-block holds k = {0,2,4,6,1,3,5,7}[p]
+        perm = np.array([0, 2, 4, 6, 1, 3, 5, 7])
+        qo = qo.reshape(67, K // 8, 8)[:, :, perm].reshape(67, K)
+    assert np.array_equal(s.cpu().numpy(), so)
+    assert np.array_equal(q.cpu().numpy(), qo)
+
+
+@pytest.mark.parametrize("asym", [True, False])
+def test_dequant_bit_exact_all_zero_points(asym):
+    r = rng(5)
+    E, N, K, g = 3, 64, 1024, 128
+    w = r.integers(-2**31, 2**31, (E, N, K // 8), dtype=np.int64).astype(np.int32)
+    z = r.integers(-2**31, 2**31, (E, N // 8, K // g), dtype=np.int64).astype(np.int32) if asym else None
+    got = W.dequant_fp8(torch.from_numpy(w).to(DEV), g,
+                        None if z is None else torch.from_numpy(z).to(DEV))
+    ref = O.dequant_codes(w, z, g)
+    assert np.array_equal(got.cpu().numpy(), ref)
+    # every (nibble, zp) pair occurs
+    nib = O.unpack_nibbles(w)
+    if asym:
+        zp = np.repeat(O.unpack_zeros(z, N), g, -1)
+        assert np.unique(nib.astype(np.int64) * 16 + zp).size == 256
+
+
+def test_dequant_e2m1_bit_exact():
+    r = rng(6)
+    w = r.integers(-2**31, 2**31, (2, 16, 32), dtype=np.int64).astype(np.int32)
+    got = W.dequant_fp8(torch.from_numpy(w).to(DEV), 32, None, weight_is_e2m1=True)
+    assert np.array_equal(got.cpu().numpy(), O.dequant_codes(w, None, 32, e2m1=True))
+
+
+def test_silu_and_mul_close():
+    r = rng(7)
+    x = (r.standard_normal((33, 2 * 256)) * 3).astype(np.float16)
+    out = torch.empty((33, 256), dtype=torch.float16, device=DEV)
+    W.silu_and_mul(out, torch.from_numpy(x).to(DEV))
+    ref = O.silu_and_mul(x[:, :256], x[:, 256:])
+    diff = np.abs(out.cpu().numpy().astype(np.float32) - ref.astype(np.float32))
+    # expf may differ from numpy exp by an ulp -> at most one fp16 ulp of difference
+    assert np.all(diff <= np.abs(ref.astype(np.float32)) * 2.0 ** -10 * 2.01 + 2.0 ** -24 * 4)
+
+
+# --------------------------------------------------------------------------- #
+# router and align
+# --------------------------------------------------------------------------- #
+@pytest.mark.parametrize("T,E,k", [(1, 256, 8), (32, 256, 8), (1000, 128, 8), (7, 64, 1)])
+def test_topk_softmax(T, E, k):
+    r = rng(T + E)
+    lg = r.standard_normal((T, E)).astype(np.float32)
+    lg[0, :] = 0.25   # ties resolve to the lowest ids
+    w, ids = W.fused_topk(None, torch.from_numpy(lg).to(DEV), k, True)
+    wo, io = O.topk_softmax(lg, k)
+    assert np.array_equal(ids.cpu().numpy(), io)
+    np.testing.assert_allclose(w.cpu().numpy(), wo, rtol=2e-5, atol=1e-7)
+
+
+@pytest.mark.parametrize("T,k,E,bm", [(1, 8, 256, 16), (32, 8, 256, 16), (32, 8, 256, 8),
+                                      (128, 8, 256, 64), (4096, 8, 256, 64), (2048, 8, 128, 64),
+                                      (200, 4, 1024, 32), (1, 1, 1, 1)])
+def test_align_bit_exact(T, k, E, bm):
+    r = rng(T * 7 + E)
+    ids = np.stack([r.permutation(E)[:k] for _ in range(T)]).astype(np.int32)
+    sti, eid, ntp = W.moe_align_block_size(torch.from_numpy(ids).to(DEV), bm, E)
+    so, eo, no = O.moe_align(ids, bm, E)
+    assert int(ntp.item()) == int(no[0])
+    assert np.array_equal(sti.cpu().numpy(), so)
+    assert np.array_equal(eid.cpu().numpy(), eo)
+
+
+def test_align_zipf_skew_and_expert_map():
+    r = rng(8)
+    T, k, E, bm = 4096, 8, 256, 64
+    p = 1.0 / np.arange(1, E + 1) ** 1.1
+    lg = np.log(p / p.sum())[r.permutation(E)] + r.gumbel(size=(T, E))
+    ids = np.argsort(-lg, axis=1)[:, :k].astype(np.int32)
+    emap = np.where(np.arange(E) % 3 == 0, np.arange(E) // 3, -1).astype(np.int32)
+    for em in (None, emap):
+        tm = None if em is None else torch.from_numpy(em).to(DEV)
+        sti, eid, ntp = W.moe_align_block_size(torch.from_numpy(ids).to(DEV), bm, E, tm)
+        so, eo, no = O.moe_align(ids, bm, E, expert_map=em)
+        assert int(ntp.item()) == int(no[0])
+        assert np.array_equal(sti.cpu().numpy(), so) and np.array_equal(eid.cpu().numpy(), eo)
+
+
+# --------------------------------------------------------------------------- #
+# grouped GEMMs
+# --------------------------------------------------------------------------- #
+def make_case(seed, T, E, N, K, k, g, asym=True):
+    r = rng(seed)
+    nib = r.integers(0, 16, (E, N, K))
+    zp = r.integers(0, 16, (E, N, K // g))
+    w = O.pack_nibbles(nib)
+    z = O.pack_zeros(zp) if asym else None
+    sc = r.uniform(0.005, 0.02, (E, N, K // g)).astype(np.float16)
+    x = r.standard_normal((T, K)).astype(np.float16)
+    ids = np.stack([r.permutation(E)[:k] for _ in range(T)]).astype(np.int32)
+    tw = r.random((T, k)).astype(np.float32)
+    return x, w, z, sc, ids, tw
+
+
+def to_dev(*arrs):
+    return [None if a is None else torch.from_numpy(np.ascontiguousarray(a)).to(DEV) for a in arrs]
+
+
+GEMM_CASES = [
+    # (T, E, N, K, top_k, block_m, g)   reference sweep shapes (test_moe_correctness.py:149-156)
+    (64, 8, 128, 256, 2, 16, 128),
+    (32, 4, 256, 512, 2, 32, 128),
+    (128, 8, 512, 1024, 2, 64, 128),
+    (1, 8, 512, 1024, 2, 16, 128),
+    (16, 16, 256, 256, 4, 16, 32),
+    (64, 8, 128, 256, 2, 16, 32),
+    (40, 8, 256, 2048, 8, 128, 128),
+]
+
+
+@pytest.mark.parametrize("kernel", ["scalar", "wmma", "gemv"])
+@pytest.mark.parametrize("asym", [True, False])
+@pytest.mark.parametrize("case", GEMM_CASES)
+def test_moe_gemm_vs_oracle(kernel, asym, case):
+    T, E, N, K, k, bm, g = case
+    if kernel == "gemv" and bm > 64:
+        pytest.skip("gemv block_m <= 64 (reference contract)")
+    x, w, z, sc, ids, _ = make_case(hash(case) % 1000, T, E, N, K, k, g, asym)
+    sti, eid, ntp = O.moe_align(ids, bm, E)
+    xd, wd, zd, scd, stid, eidd, ntpd = to_dev(x, w, z, sc, sti, eid, ntp)
+    out = W.mmq_fp8_moe_gemm(xd, wd, scd, stid, eidd, ntpd, k, bm, kernel=kernel, w_zeros=zd)
+    ref, valid = O.grouped_gemm_padded(x, w, sc, z, sti, eid, ntp, k, bm)
+    got = out.cpu().numpy()[valid]
+    assert maxrel(got, ref[valid]) <= REL_TOL
+
+
+@pytest.mark.parametrize("case", [(64, 8, 256, 256, 2, 16, 128), (128, 8, 512, 512, 2, 64, 128),
+                                  (256, 4, 1024, 2048, 2, 128, 128), (16, 16, 256, 256, 4, 16, 32)])
+def test_gemm1_silu_fused_bit_exact_to_unfused(case):
+    """Fused gemm1+SiLU == gemm1 fp16 store + silu_and_mul, bit for bit
+    (test_moe_experts.py:283-315)."""
+    T, E, N, K, k, bm, g = case
+    x, w, z, sc, ids, _ = make_case(sum(case), T, E, N, K, k, g)
+    sti, eid, ntp = O.moe_align(ids, bm, E)
+    xd, wd, zd, scd, stid, eidd, ntpd = to_dev(x, w, z, sc, sti, eid, ntp)
+    out1 = W.mmq_fp8_moe_gemm(xd, wd, scd, stid, eidd, ntpd, k, bm, kernel="wmma", w_zeros=zd)
+    unf = torch.empty((out1.shape[0], N // 2), dtype=torch.float16, device=DEV)
+    W.silu_and_mul(unf, out1)
+    fused = W.mmq_fp8_moe_gemm1_silu(xd, wd, scd, stid, eidd, ntpd, k, bm, kernel="wmma",
+                                      w_zeros=zd)
+    valid = torch.from_numpy(
+        (np.arange(sti.size) < ntp[0]) & (sti < T * k)).to(DEV)
+    assert torch.equal(fused[valid], unf[valid])
+    # and close to the oracle
+    ref, vmask = O.grouped_gemm_padded(x, w, sc, z, sti, eid, ntp, k, bm)
+    h = O.silu_and_mul(ref[:, :N // 2], ref[:, N // 2:])
+    assert maxrel(fused.cpu().numpy()[vmask], h[vmask]) <= REL_TOL
+
+
+@pytest.mark.parametrize("kernel", ["scalar", "wmma", "gemv"])
+def test_scatter_vs_oracle(kernel):
+    T, E, N, K, k, bm, g = 24, 8, 256, 512, 4, 16, 128
+    x, w, z, sc, ids, tw = make_case(41, T, E, N, K, k, g)
+    sti, eid, ntp = O.moe_align(ids, bm, E)
+    P = sti.size
+    h = rng(42).standard_normal((P, K)).astype(np.float16)
+    out = torch.zeros((T, N), dtype=torch.float32, device=DEV)
+    hd, wd, zd, scd, stid, eidd, ntpd, twd = to_dev(h, w, z, sc, sti, eid, ntp, tw.reshape(-1))
+    W.mmq_fp8_moe_gemm_scatter(hd, wd, scd, stid, eidd, ntpd, twd, out, k, bm, kernel=kernel,
+                               w_zeros=zd)
+    ref = O.gemm_scatter(h, w, sc, z, sti, eid, ntp, tw.reshape(-1), np.zeros((T, N), np.float32),
+                         k, bm)
+    assert maxrel(out.cpu().numpy(), ref) <= REL_TOL
+
+
+def test_gather_reduce_bit_exact():
+    r = rng(50)
+    T, k, E, bm, N = 33, 8, 64, 16, 384
+    ids = np.stack([r.permutation(E)[:k] for _ in range(T)]).astype(np.int32)
+    sti, eid, ntp = O.moe_align(ids, bm, E)
+    out2 = r.standard_normal((sti.size, N)).astype(np.float16)
+    tw = r.random(T * k).astype(np.float32)
+    o2d, stid, twd, ntpd = to_dev(out2, sti, tw, ntp)
+    got = W.mmq_fp8_moe_gather_reduce(o2d, stid, twd, ntpd, k)
+    ref = O.gather_reduce(out2, sti, tw, ntp, k)
+    assert np.array_equal(got.cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("kernel", ["reference_scalar", "prefill_wmma", "decode_gemv",
+                                    "prefill_wmma_ashuffle"])
+def test_dense_config1(kernel):
+    """Config 1: dense M=16, N=1024, K=2048 AWQ g128 with zero-points."""
+    r = rng(1001)
+    M, N, K, g = 16, 1024, 2048, 128
+    x = torch.randn(M, K, generator=torch.Generator().manual_seed(1001)).to(torch.bfloat16)
+    x16 = x.to(torch.float16).numpy()
+    nib = r.integers(0, 16, (N, K))
+    zp = r.integers(0, 16, (N, K // g))
+    w = O.pack_nibbles(nib)
+    z = O.pack_zeros(zp)
+    sc = r.uniform(0.005, 0.02, (N, K // g)).astype(np.float16)
+    xd, wd, zd, scd = to_dev(x16, w, z, sc)
+    out = W.mmq_fp8_gemm(xd, wd, scd, kernel=kernel, w_zeros=zd)
+    ref = O.dense_gemm(x16, w, sc, z)
+    assert maxrel(out.cpu().numpy(), ref) <= REL_TOL

@@ -1,0 +1,154 @@
+"""GPU parity of the whole expert path (w4a8_moe_apply / _run_grouped_moe) against the
+CPU oracle, at small shapes and at the BASELINE.json shapes (sampled tokens), plus
+size-independent properties at full size. Bar: max|out - ref| / max|ref| <= 1e-2."""
+import numpy as np
+import pytest
+import torch
+
+import bench
+import oracle as O
+import w4a8_fp8_wmma as W
+from w4a8_fp8_wmma import moe_experts
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+REL_TOL = 1e-2
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _need_gpu():
+    assert torch.cuda.is_available(), "GPU tests need a visible MI355X"
+
+
+def maxrel(got, ref):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    return float(np.abs(got - ref).max() / max(np.abs(ref).max(), 1e-30))
+
+
+def small_layer(seed, T, E, H, I, k, g=128, asym=True, dtype=torch.bfloat16):
+    cfg = dict(T=T, H=H, E=E, k=k, I=I, g=g, routing="uniform")
+    ws = bench.make_weights(cfg, seed, DEV)
+    if not asym:
+        ws["z13"] = None
+        ws["z2"] = None
+    x, logits = bench.make_inputs(cfg, seed + 1, DEV)
+    tw, ids = W.fused_topk(None, logits, k, True)
+    return cfg, ws, x.to(dtype), tw, ids
+
+
+def oracle_layer(cfg, ws, x, tw, ids, tokens=None, round_y=False):
+    sel = slice(None) if tokens is None else tokens
+    h = {kk: (None if v is None else v.cpu().numpy()) for kk, v in ws.items()}
+    return O.moe_layer(x.float().cpu().numpy()[sel], h["w13"], h["s13"], h["z13"], h["w2"],
+                       h["s2"], h["z2"], tw.cpu().numpy()[sel], ids.cpu().numpy()[sel],
+                       cfg["g"], round_y_fp16=round_y)
+
+
+@pytest.mark.parametrize("T", [1, 7, 32, 96, 97, 300])
+@pytest.mark.parametrize("asym", [True, False])
+def test_moe_apply_small(T, asym):
+    cfg, ws, x, tw, ids = small_layer(100 + T, T, 16, 512, 256, 4, asym=asym)
+    out = W.moe_apply(x, ws["w13"], ws["w2"], ws["s13"], ws["s2"], ws["z13"], ws["z2"], tw, ids)
+    ref = oracle_layer(cfg, ws, x, tw, ids)
+    assert out.dtype == torch.bfloat16 and out.shape == x.shape
+    assert maxrel(out.float().cpu().numpy(), ref) <= REL_TOL
+
+
+@pytest.mark.parametrize("kernel", ["scalar", "wmma", "gemv"])
+@pytest.mark.parametrize("T", [4, 160])
+def test_run_grouped_moe_kernels(kernel, T):
+    cfg, ws, x, tw, ids = small_layer(200 + T, T, 8, 256, 128, 2)
+    out = moe_experts._run_grouped_moe(x, ws["w13"], ws["w2"], ws["s13"], ws["s2"], ws["z13"],
+                                       ws["z2"], tw, ids, "silu", 8, None, False, kernel)
+    ref = oracle_layer(cfg, ws, x, tw, ids, round_y=(kernel == "scalar"))
+    assert out.dtype == x.dtype
+    assert maxrel(out.float().cpu().numpy(), ref) <= REL_TOL
+
+
+def test_fp16_input_and_router_weight_on_input():
+    cfg, ws, x, tw, ids = small_layer(300, 12, 8, 256, 128, 1, dtype=torch.float16)
+    out = moe_experts._run_grouped_moe(x, ws["w13"], ws["w2"], ws["s13"], ws["s2"], ws["z13"],
+                                       ws["z2"], tw, ids, "silu", 8, None, True, "wmma")
+    xin = (x * tw.to(x.dtype)).float()
+    ref = oracle_layer(cfg, ws, xin, torch.ones_like(tw), ids)
+    assert out.dtype == torch.float16
+    assert maxrel(out.float().cpu().numpy(), ref) <= REL_TOL
+
+
+def test_expert_map_drops_non_local_experts():
+    cfg, ws, x, tw, ids = small_layer(400, 16, 8, 256, 128, 2)
+    emap = torch.tensor([0, 1, 2, 3, -1, -1, -1, -1], dtype=torch.int32, device=DEV)
+    out = W.moe_apply(x, ws["w13"], ws["w2"], ws["s13"], ws["s2"], ws["z13"], ws["z2"], tw, ids,
+                      expert_map=emap)
+    # reference: local experts keep their weights; non-local slots get weight 0
+    twm = tw.clone()
+    twm[ids >= 4] = 0
+    ref = oracle_layer(cfg, ws, x, twm, ids.clamp(max=3))
+    assert maxrel(out.float().cpu().numpy(), ref) <= REL_TOL
+
+
+@pytest.mark.parametrize("name", ["c2", "c3", "c4", "c5"])
+def test_baseline_configs_sampled_tokens(name):
+    """Full-size BASELINE.json layers; the oracle checks 3 tokens (first, middle, last)."""
+    cfg = dict(bench.CONFIGS[name])
+    ws = bench.make_weights(cfg, 1000 + int(name[1:]) * 17, DEV)
+    x, logits = bench.make_inputs(cfg, 1000 + int(name[1:]), DEV)
+    tw, ids = W.fused_topk(None, logits, cfg["k"], True)
+    out = W.moe_apply(x, ws["w13"], ws["w2"], ws["s13"], ws["s2"], ws["z13"], ws["z2"], tw, ids)
+    T = cfg["T"]
+    tok = sorted({0, T // 2, T - 1})
+    ref = oracle_layer(cfg, ws, x, tw, ids, tokens=tok)
+    got = out.float().cpu().numpy()[tok]
+    assert maxrel(got, ref) <= REL_TOL
+    assert torch.isfinite(out.float()).all()
+
+
+def test_decode_is_deterministic_and_token_local():
+    """Decode schedule: bit-identical reruns; permuting tokens permutes outputs exactly."""
+    cfg = dict(bench.CONFIGS["c3"])
+    ws = bench.make_weights(cfg, 77, DEV)
+    x, logits = bench.make_inputs(cfg, 78, DEV)
+    tw, ids = W.fused_topk(None, logits, cfg["k"], True)
+    a = W.moe_apply(x, ws["w13"], ws["w2"], ws["s13"], ws["s2"], ws["z13"], ws["z2"], tw, ids)
+    b = W.moe_apply(x, ws["w13"], ws["w2"], ws["s13"], ws["s2"], ws["z13"], ws["z2"], tw, ids)
+    assert torch.equal(a, b)
+    perm = torch.randperm(cfg["T"], generator=torch.Generator().manual_seed(0)).to(DEV)
+    c = W.moe_apply(x[perm].contiguous(), ws["w13"], ws["w2"], ws["s13"], ws["s2"], ws["z13"],
+                    ws["z2"], tw[perm].contiguous(), ids[perm].contiguous())
+    assert torch.equal(c, a[perm])
+
+
+def test_prefill_linear_in_router_weights():
+    """out(w) is linear in the top-k weights: out(2w) == 2 out(w) up to fp32 rounding."""
+    cfg = dict(bench.CONFIGS["c4"])
+    cfg["T"] = 512
+    ws = bench.make_weights(cfg, 91, DEV)
+    x, logits = bench.make_inputs(cfg, 92, DEV)
+    tw, ids = W.fused_topk(None, logits, cfg["k"], True)
+    a = W.moe_apply(x, ws["w13"], ws["w2"], ws["s13"], ws["s2"], ws["z13"], ws["z2"], tw, ids)
+    b = W.moe_apply(x, ws["w13"], ws["w2"], ws["s13"], ws["s2"], ws["z13"], ws["z2"],
+                    (2 * tw).contiguous(), ids)
+    assert maxrel(b.float().cpu().numpy(), 2 * a.float().cpu().numpy()) <= 1e-2
+
+
+def test_graph_replay_matches_eager():
+    """The bench captures the layer in a HIP graph: every replay must equal eager."""
+    cfg, ws, x, tw, ids = small_layer(500, 32, 16, 512, 256, 4)
+    eager = W.moe_apply(x, ws["w13"], ws["w2"], ws["s13"], ws["s2"], ws["z13"], ws["z2"], tw, ids)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        W.moe_apply(x, ws["w13"], ws["w2"], ws["s13"], ws["s2"], ws["z13"], ws["z2"], tw, ids)
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = W.moe_apply(x, ws["w13"], ws["w2"], ws["s13"], ws["s2"], ws["z13"], ws["z2"], tw,
+                          ids)
+    for _ in range(4):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+        W.moe_apply(x, ws["w13"], ws["w2"], ws["s13"], ws["s2"], ws["z13"], ws["z2"], tw, ids)
+        torch.cuda.synchronize()

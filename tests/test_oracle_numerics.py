@@ -1,0 +1,159 @@
+"""Pin the oracle's numeric primitives against libraries and closed forms (CPU)."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+
+
+def torch_e4m3(x: np.ndarray) -> np.ndarray:
+    return torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(
+        torch.float8_e4m3fn).view(torch.uint8).numpy()
+
+
+def test_e4m3_encode_exhaustive_fp16_inputs():
+    # every fp16 bit pattern (subnormals, ties, overflow, inf, nan)
+    h = np.arange(65536, dtype=np.uint16).view(np.float16).astype(np.float32)
+    assert np.array_equal(O.e4m3_encode(h), torch_e4m3(h))
+
+
+def test_e4m3_encode_random_fp32():
+    r = np.random.default_rng(7)
+    x = (r.standard_normal(1 << 20) * np.exp2(r.integers(-16, 12, 1 << 20))).astype(np.float32)
+    assert np.array_equal(O.e4m3_encode(x), torch_e4m3(x))
+
+
+def test_e4m3_encode_ties_round_to_even():
+    # midpoints between adjacent e4m3 values round to the even mantissa
+    vals = O.E4M3_TO_F64[:0x7E].copy()
+    vals = np.unique(vals[np.isfinite(vals) & (vals >= 0)])
+    mids = ((vals[:-1] + vals[1:]) / 2).astype(np.float32)
+    got = O.e4m3_decode(O.e4m3_encode(mids))
+    codes_lo = O.e4m3_encode(vals[:-1].astype(np.float32))
+    codes_hi = O.e4m3_encode(vals[1:].astype(np.float32))
+    even = np.where(codes_lo % 2 == 0, vals[:-1], vals[1:])
+    assert np.array_equal(got, even.astype(np.float32))
+    assert np.array_equal(O.e4m3_encode(mids), torch_e4m3(mids))
+    del codes_hi
+
+
+def test_e4m3_decode_all_codes():
+    codes = np.arange(256, dtype=np.uint8)
+    ref = torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy()
+    assert np.array_equal(O.e4m3_decode(codes), ref, equal_nan=True)
+
+
+def test_dequant_table_exhaustive():
+    # all 16 nibbles x 16 zero-points: e4m3 byte of (n - z) == torch cast, exact in e4m3
+    for z in range(16):
+        t = O.dequant_table(z)
+        n = np.arange(16)
+        assert np.array_equal(t, torch_e4m3((n - z).astype(np.float32)))
+        assert np.array_equal(O.e4m3_decode(t), (n - z).astype(np.float32))
+
+
+def test_dequant_table_e2m1_is_exact():
+    t = O.dequant_table(0, e2m1=True)
+    assert np.array_equal(O.e4m3_decode(t), O.E2M1_LUT)
+    assert t[8] == 0x80  # -0.0 keeps its sign
+
+
+def test_dequant_codes_matches_unpack():
+    r = np.random.default_rng(1)
+    E, N, K, g = 2, 16, 256, 128
+    nib = r.integers(0, 16, (E, N, K))
+    zp = r.integers(0, 16, (E, N, K // g))
+    w = O.pack_nibbles(nib)
+    z = O.pack_zeros(zp)
+    assert np.array_equal(O.unpack_nibbles(w), nib)
+    assert np.array_equal(O.unpack_zeros(z, N), zp)
+    codes = O.dequant_codes(w, z, g)
+    expect = nib - np.repeat(zp, g, axis=-1)
+    assert np.array_equal(O.e4m3_decode(codes), expect.astype(np.float32))
+    sym = O.dequant_codes(w, None, g)
+    assert np.array_equal(O.e4m3_decode(sym), (nib - 8).astype(np.float32))
+
+
+def test_unpack_nibble_order_low_first():
+    w = np.array([[0x76543210]], dtype=np.uint32).view(np.int32)
+    assert O.unpack_nibbles(w).tolist() == [[0, 1, 2, 3, 4, 5, 6, 7]]
+    z = np.array([[[0x76543210]]], dtype=np.uint32).view(np.int32)   # (1, N/8=1, G=1)
+    assert O.unpack_zeros(z, 8)[0, :, 0].tolist() == list(range(8))
+
+
+def test_act_quant_matches_torch_reciprocal_form():
+    r = np.random.default_rng(3)
+    x = (r.standard_normal((64, 512)) * np.exp2(r.integers(-6, 6, (64, 1)))).astype(np.float16)
+    x[0] = 0                      # all-zero row -> scale floor
+    x[1, :] = np.float16(1e-4)    # tiny row
+    x[2, 5] = np.float16(60000)   # large outlier
+    q, s = O.act_quant(x)
+    xt = torch.from_numpy(x).float()
+    amax = xt.abs().amax(1)
+    st = torch.clamp(amax / 448.0, min=1e-8)
+    qt = (xt * (1.0 / st)[:, None]).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(s, st.numpy())
+    assert np.array_equal(q, qt)
+    assert s[0] == np.float32(1e-8) and np.all(q[0] == 0)
+
+
+def test_act_quant_invariants():
+    r = np.random.default_rng(4)
+    x = r.standard_normal((32, 256)).astype(np.float16)
+    q, s = O.act_quant(x)
+    deq = O.e4m3_decode(q) * s[:, None]
+    xf = x.astype(np.float32)
+    # the absmax element maps to +-448 exactly; every element within half an e4m3 ulp
+    assert np.all(np.abs(O.e4m3_decode(q)).max(1) == 448.0)
+    assert np.all(np.abs(deq - xf) <= np.abs(xf) * 2.0 ** -4 + s[:, None] * 2.0 ** -10)
+
+
+def test_silu_and_mul_against_torch():
+    r = np.random.default_rng(5)
+    g = (r.standard_normal(4096) * 4).astype(np.float16)
+    u = (r.standard_normal(4096) * 2).astype(np.float16)
+    got = O.silu_and_mul(g, u).astype(np.float64)
+    silu = torch.nn.functional.silu(torch.from_numpy(g).double()).numpy()
+    ref = silu * u.astype(np.float64)
+    # two fp16 roundings: |err| <= 2^-10 |ref| + fp16 subnormal step
+    assert np.all(np.abs(got - ref) <= np.abs(ref) * 2.0 ** -10 * 1.01 + 2.0 ** -24 * 4)
+
+
+def test_topk_softmax_bruteforce_and_ties():
+    r = np.random.default_rng(6)
+    lg = r.standard_normal((50, 64)).astype(np.float32)
+    lg[0, :] = 0.5                   # all tied -> lowest ids
+    w, ids = O.topk_softmax(lg, 8)
+    assert ids[0].tolist() == list(range(8))
+    for t in range(50):
+        order = sorted(range(64), key=lambda e: (-float(lg[t, e]), e))[:8]
+        assert ids[t].tolist() == order
+        p = np.exp(lg[t].astype(np.float64) - lg[t].max())
+        sel = p[order] / p[order].sum()
+        np.testing.assert_allclose(w[t], sel, rtol=1e-6)
+    assert np.allclose(w.sum(1), 1.0, atol=1e-6)
+
+
+def test_gather_reduce_closed_form():
+    # 2 tokens, top_k 2, P = 4 rows; slot 3 missing
+    out2 = np.array([[1, 2], [3, 4], [5, 6], [7, 8]], dtype=np.float16)
+    sti = np.array([2, 0, 1, 4], dtype=np.int32)   # row 3 is padding (sentinel 4)
+    tw = np.array([0.5, 0.25, 2.0, 1.0], dtype=np.float32)
+    out = O.gather_reduce(out2, sti, tw, np.array([4], np.int32), 2)
+    # token 0: slot0 row1 (3,4)*0.5 + slot1 row2 (5,6)*0.25 ; token 1: slot2 row0 (1,2)*2
+    assert np.allclose(out, [[3 * .5 + 5 * .25, 4 * .5 + 6 * .25], [2.0, 4.0]])
+
+
+def test_fma32_is_single_rounding():
+    a = np.float32(1 + 2 ** -23)
+    b = np.float32(1 - 2 ** -23)
+    c = np.float32(-1.0)
+    # exact a*b - 1 = -2^-46, representable; a separate multiply would round to 0
+    assert O.fma32(a, b, c) == np.float32(-(2.0 ** -46))
+
+
+@pytest.mark.parametrize("bits", [0x3F800000, 0x3F808000, 0x3F818000, 0x7F7FFFFF])
+def test_bf16_rounding(bits):
+    x = np.array([bits], np.uint32).view(np.float32)
+    ref = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(O.f32_to_bf16_bits(x), ref)
