@@ -51,6 +51,15 @@ int check_grouped(int64_t rows, int64_t K, int64_t E, int64_t N, int64_t gs, int
 }
 
 int run_grouped(GroupedArgs& a, int64_t kernel, void* ws, size_t ws_bytes, hipStream_t s) {
+    const bool mfma = mfma_supported(a.K, a.group_size);
+    // E2M1 codebook weights take the matrix-core tiles (the GEMV feeds raw nibbles)
+    const bool gemv = gemv_supported(a.K, a.group_size) && !a.e2m1;
+    if (kernel == W4A8_MOE_KERNEL_GEMV && gemv) {
+        // decode GEMV quantises its block's rows itself (bit-identical to act_quant)
+        a.x_fp8 = nullptr;
+        a.act_scales = nullptr;
+        return launch_grouped_gemv(a, s);
+    }
     Workspace w(ws, ws_bytes);
     a.x_fp8 = w.take<uint8_t>((size_t)(a.x_rows * a.K));
     a.act_scales = w.take<float>((size_t)a.x_rows);
@@ -64,9 +73,9 @@ int run_grouped(GroupedArgs& a, int64_t kernel, void* ws, size_t ws_bytes, hipSt
                                   filter ? a.sorted_ids : nullptr, filter ? a.ntp : nullptr,
                                   a.num_valid))
         return rc;
-    const bool mfma = mfma_supported(a.K, a.group_size);
-    if (kernel == W4A8_MOE_KERNEL_WMMA && mfma) return launch_grouped_mfma(a, s);
-    if (kernel == W4A8_MOE_KERNEL_GEMV && mfma) return launch_grouped_gemv(a, s);
+    // gemv for K-group counts outside its split-K table runs the matrix-core tiles
+    if ((kernel == W4A8_MOE_KERNEL_WMMA || kernel == W4A8_MOE_KERNEL_GEMV) && mfma)
+        return launch_grouped_mfma(a, s);
     return launch_grouped_scalar(a, s);
 }
 
@@ -436,11 +445,15 @@ int w4a8_moe_apply(const void* x, int x_dtype, int64_t T, int64_t H, int64_t int
     g1.epi = Epi::kSiluHalf; g1.out = h; g1.out_top_k = top_k; g1.x_fp8 = xq; g1.act_scales = s1;
     int rc;
     if (!mfma) rc = launch_grouped_scalar(g1, s);
-    else rc = pl.decode ? launch_grouped_gemv(g1, s) : launch_grouped_mfma(g1, s);
+    else if (pl.decode && !e2m1 && gemv_supported(H, group_size)) rc = launch_grouped_gemv(g1, s);
+    else rc = launch_grouped_mfma(g1, s);
     if (rc) return rc;
     stage_mark(4, s);
-    // act-quant of h over real rows only
-    if ((rc = launch_act_quant(h, false, pl.P, inter, hq, s2, true, s, sti, ntp, numel))) return rc;
+    // act-quant of h over real rows only (the decode GEMV quantises its rows itself)
+    const bool fuse_aq2 = pl.decode && !e2m1 && gemv_supported(inter, group_size);
+    if (!fuse_aq2)
+        if ((rc = launch_act_quant(h, false, pl.P, inter, hq, s2, true, s, sti, ntp, numel)))
+            return rc;
     stage_mark(5, s);
     // gemm2 (identity gather) -> per-slot rows (decode) or scatter (prefill)
     GroupedArgs g2{};
@@ -449,9 +462,13 @@ int w4a8_moe_apply(const void* x, int x_dtype, int64_t T, int64_t H, int64_t int
     g2.sorted_ids = sti; g2.P = pl.P; g2.expert_ids = eid; g2.ntp = ntp; g2.top_k = top_k;
     g2.identity_gather = true; g2.num_valid = numel; g2.block_m = pl.block_m; g2.e2m1 = e2m1;
     g2.epi = pl.decode ? Epi::kSlotF32 : Epi::kScatter; g2.out = acc;
-    g2.topk_weights = topk_weights; g2.out_top_k = top_k; g2.x_fp8 = hq; g2.act_scales = s2;
+    g2.topk_weights = topk_weights; g2.out_top_k = top_k;
+    g2.x = h; g2.x_bf16 = false;
+    g2.x_fp8 = fuse_aq2 ? nullptr : hq;
+    g2.act_scales = fuse_aq2 ? nullptr : s2;
     if (!mfma) rc = launch_grouped_scalar(g2, s);
-    else rc = pl.decode ? launch_grouped_gemv(g2, s) : launch_grouped_mfma(g2, s);
+    else if (fuse_aq2) rc = launch_grouped_gemv(g2, s);
+    else rc = launch_grouped_mfma(g2, s);
     if (rc) return rc;
     stage_mark(6, s);
     if (pl.decode)   // slots whose expert is not local / out of range contribute nothing

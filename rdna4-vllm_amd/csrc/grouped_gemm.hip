@@ -14,6 +14,9 @@
 //                            with several groups of loads in flight (replaces
 //                            moe_kernel.hip:884-1062).
 // All read prequantised activations: x_fp8 rows in k8-interleaved order + act_scales.
+#include <algorithm>
+#include <type_traits>
+
 #include "w4a8_common.h"
 #include "w4a8_internal.h"
 
@@ -23,6 +26,7 @@ namespace {
 struct Params {
     const uint8_t* xq;          // (x_rows, K) e4m3, k8-interleaved
     const float* asc;           // (x_rows,)
+    const void* xh;             // (x_rows, K) fp16/bf16 rows (fused quantisation path)
     const int32_t* w;           // (E, N, K/8)
     const __half* scales;       // (E, N, G)
     const int32_t* zeros;       // (E, N/8, G) or null
@@ -37,6 +41,7 @@ struct Params {
     int num_valid;
     int identity;
     int e2m1;
+    int xbf16;                  // xh holds bf16 (else fp16)
 };
 
 // Row resolution shared by all schedules. Returns the activation row (or -1).
@@ -206,8 +211,10 @@ __global__ void __launch_bounds__(256) grouped_mfma_kernel(Params p) {
     for (int i = 0; i < C::A_CHUNKS; ++i) {
         const int c = tid + i * 256;
         a_row[i] = c < BM * 8 ? (c >> 3) : -1;
+        // padding rows read a real row: their outputs are never stored
         const int src = c < BM * 8 ? s_src[c >> 3] : -1;
-        a_ptr[i] = src >= 0 ? p.xq + (int64_t)src * p.K + (c & 7) * 16 : nullptr;
+        a_ptr[i] = p.xq + (int64_t)(src >= 0 ? src : s_src[0] >= 0 ? s_src[0] : 0) * p.K +
+                   (c & 7) * 16;
     }
     // weights: chunk c -> tile row c/4, 32-nibble piece c%4 of the group
     int b_row[C::B_CHUNKS];
@@ -225,7 +232,7 @@ __global__ void __launch_bounds__(256) grouped_mfma_kernel(Params p) {
             n = n0 + tr;
             if (n >= p.N) n = -1;
         }
-        b_n[i] = n;
+        b_n[i] = n < 0 ? 0 : n;   // edge columns read row 0; they are never stored
     }
 
     uint4 a_reg[C::A_CHUNKS];
@@ -234,19 +241,13 @@ __global__ void __launch_bounds__(256) grouped_mfma_kernel(Params p) {
     auto load_group = [&](int g) {
 #pragma unroll
         for (int i = 0; i < C::A_CHUNKS; ++i)
-            a_reg[i] = a_ptr[i] ? *reinterpret_cast<const uint4*>(a_ptr[i] + g * kGroup)
-                                : make_uint4(0, 0, 0, 0);
+            a_reg[i] = *reinterpret_cast<const uint4*>(a_ptr[i] + g * kGroup);
 #pragma unroll
         for (int i = 0; i < C::B_CHUNKS; ++i) {
             const int n = b_n[i];
-            if (n >= 0) {
-                b_reg[i] = *reinterpret_cast<const uint4*>(
-                    we + (int64_t)n * kw_row + g * (kGroup / 8) + ((tid + i * 256) & 3) * 4);
-                b_tab[i] = table_index(ze, n, g, p.G, p.e2m1);
-            } else {
-                b_reg[i] = make_uint4(0, 0, 0, 0);
-                b_tab[i] = -1;
-            }
+            b_reg[i] = *reinterpret_cast<const uint4*>(
+                we + (int64_t)n * kw_row + g * (kGroup / 8) + ((tid + i * 256) & 3) * 4);
+            b_tab[i] = table_index(ze, n, g, p.G, p.e2m1);
         }
     };
     auto store_group = [&](int buf) {
@@ -262,14 +263,9 @@ __global__ void __launch_bounds__(256) grouped_mfma_kernel(Params p) {
         for (int i = 0; i < C::B_CHUNKS; ++i) {
             const int c = tid + i * 256;
             uint8_t* dst = B + b_row[i] * kLdsStride + (c & 3) * 32;
-            if (b_tab[i] >= 0) {
-                const v8i d = decode_frag(b_reg[i], load_table(b_tab[i]));
-                *reinterpret_cast<uint4*>(dst) = make_uint4(d[0], d[1], d[2], d[3]);
-                *reinterpret_cast<uint4*>(dst + 16) = make_uint4(d[4], d[5], d[6], d[7]);
-            } else {
-                *reinterpret_cast<uint4*>(dst) = make_uint4(0, 0, 0, 0);
-                *reinterpret_cast<uint4*>(dst + 16) = make_uint4(0, 0, 0, 0);
-            }
+            const v8i d = decode_frag(b_reg[i], load_table(b_tab[i]));
+            *reinterpret_cast<uint4*>(dst) = make_uint4(d[0], d[1], d[2], d[3]);
+            *reinterpret_cast<uint4*>(dst + 16) = make_uint4(d[4], d[5], d[6], d[7]);
         }
     };
 
@@ -282,7 +278,7 @@ __global__ void __launch_bounds__(256) grouped_mfma_kernel(Params p) {
         const int col = n0 + wn * C::NWC + jj * 16 + (lane & 15);
         t_col[j] = col;
         const bool up = C::kSilu && j >= C::NT;
-        t_srow[j] = col < ncols ? (up ? col + ncols : col) : -1;
+        t_srow[j] = col < ncols ? (up ? col + ncols : col) : 0;
     }
 
     v4f run[C::MT][C::NTT];
@@ -300,8 +296,7 @@ __global__ void __launch_bounds__(256) grouped_mfma_kernel(Params p) {
         if (g + 1 < p.G) load_group(g + 1);
         float sc[C::NTT];
 #pragma unroll
-        for (int j = 0; j < C::NTT; ++j)
-            sc[j] = t_srow[j] >= 0 ? __half2float(se[(int64_t)t_srow[j] * p.G + g]) : 0.f;
+        for (int j = 0; j < C::NTT; ++j) sc[j] = __half2float(se[(int64_t)t_srow[j] * p.G + g]);
 
         const uint8_t* A = lds + buf * (C::LDS_A + C::LDS_B);
         const uint8_t* B = A + C::LDS_A;
@@ -355,31 +350,203 @@ __global__ void __launch_bounds__(256) grouped_mfma_kernel(Params p) {
 }
 
 // =====================================================================================
-// MFMA GEMV (decode) kernel
+// MFMA GEMV (decode) kernel: split-K waves, activations in registers
 // =====================================================================================
-constexpr int kGemvMaxRows = 64;     // block_m cap (4 m-tiles)
-constexpr int kGemvUnroll = 4;       // groups of weight loads in flight per wave
+// Decode blocks hold 1..16 real rows, so the work is a stream of int4 weights. One
+// work-group takes one align block and a slice of 16-column tiles (SiLU: 16 gate columns
+// plus the matching 16 up columns). The K groups are split over KSPLIT waves, GPW groups
+// each; every wave keeps its activation fragments and their group sums in registers for
+// the whole slice, so its main loop is weight loads, nibble spreading and MFMA only, with
+// the loads of the next chunk in flight behind the current one. The KSPLIT partial sums of
+// a tile are added in LDS in a fixed order (deterministic).
+//
+// Weight nibbles enter the MFMA undecoded. The e4m3 byte with value n (0..15) is exactly
+// n * 2^-9 (subnormals 0..7; exponent field 1 for 8..15), so spreading a word's nibbles
+// into bytes (two AND, one shift) gives 2^-9 * n in the k8-interleave order. The
+// zero-point enters through sum_k a_k (n_k - z) = sum_k a_k n_k - z * sum_k a_k, where the
+// row's group sums come from one MFMA against e4m3 1.0 (scaled by 2^-9 in fp32, exact),
+// and the 2^9 rides on the activation scale. Every operand is an integer times a power of
+// two, so this is the dot product the reference forms with e4m3(n - z) operands
+// (tile_config.h:42-45) up to the MFMA's rounding. (Sums against the subnormal 2^-9 byte
+// lose accuracy inside the MFMA; against 1.0 they are exact to a few fp32 ulps.) E2M1 weights (a codebook, no
+// zero-points) take the matrix-core tiles instead.
+constexpr int kGemvMaxRows = 64;                 // block_m cap (16-row passes)
+constexpr int kGemvMaxTiles = 8;                 // tiles per team (LDS partials bound)
+constexpr uint32_t kOnesE4m3 = 0x38383838u;      // four e4m3 bytes of 1.0
+constexpr float kNibbleScale = 512.0f;
 
-template <Epi EPI, int NT>
-__global__ void __launch_bounds__(256) grouped_gemv_kernel(Params p) {
-    constexpr bool kSilu = EPI == Epi::kSiluHalf;
-    constexpr int NTT = kSilu ? 2 * NT : NT;
-    constexpr int MT_MAX = kGemvMaxRows / 16;
+template <Epi EPI, int GPW, int KSPLIT>
+struct GemvCfg {
+    static constexpr bool kSilu = EPI == Epi::kSiluHalf;
+    static constexpr int NF = kSilu ? 2 : 1;      // fragments per column tile
+    static constexpr int CT = kSilu ? 1 : 2;      // column tiles per chunk
+    static constexpr int FR = NF * CT;            // fragments per chunk and group
+    static constexpr int GC = GPW < 4 ? GPW : 4;  // groups per chunk
+    static constexpr int NB = GPW / GC;           // chunks per tile set
+    static constexpr int TEAMS = 4 / KSPLIT;      // wave teams (independent tile ranges)
+    static constexpr bool kPackedScales = GC == 2 || GC == 4;
+    static_assert(GPW % GC == 0 && (NB == 1 || NB == 2), "unsupported groups per wave");
+    static_assert(KSPLIT == 1 || KSPLIT == 2 || KSPLIT == 4, "KSPLIT divides the 4 waves");
+};
+
+__device__ __forceinline__ v8i spread_nibbles(uint4 w) {
+    constexpr uint32_t m = 0x0F0F0F0Fu;
+    return v8i{(int)(w.x & m), (int)((w.x >> 4) & m), (int)(w.y & m), (int)((w.y >> 4) & m),
+               (int)(w.z & m), (int)((w.z >> 4) & m), (int)(w.w & m), (int)((w.w >> 4) & m)};
+}
+
+// GC consecutive fp16 scales; packed two per word when the vector load is aligned.
+template <int GC>
+__device__ __forceinline__ void load_scales(const __half* ptr, uint32_t (&s)[GC]) {
+    const uint16_t* h = reinterpret_cast<const uint16_t*>(ptr);
+    if constexpr (GC == 4) {
+        const uint2 v = *reinterpret_cast<const uint2*>(h);
+        s[0] = v.x;
+        s[1] = v.y;
+    } else if constexpr (GC == 2) {
+        s[0] = *reinterpret_cast<const uint32_t*>(h);
+    } else {
+#pragma unroll
+        for (int u = 0; u < GC; ++u) s[u] = h[u];
+    }
+}
+template <int GC>
+__device__ __forceinline__ float scale_at(const uint32_t (&s)[GC], int u) {
+    uint32_t bits;
+    if constexpr (GC == 2 || GC == 4) bits = (s[u >> 1] >> (16 * (u & 1))) & 0xFFFFu;
+    else bits = s[u] & 0xFFFFu;
+    return __half2float(__ushort_as_half(static_cast<unsigned short>(bits)));
+}
+template <int GC>
+__device__ __forceinline__ void load_zero_words(const int32_t* ptr, int32_t (&z)[GC]) {
+    if constexpr (GC == 4) {
+        const int4 v = *reinterpret_cast<const int4*>(ptr);
+        z[0] = v.x; z[1] = v.y; z[2] = v.z; z[3] = v.w;
+    } else if constexpr (GC == 2) {
+        const int2 v = *reinterpret_cast<const int2*>(ptr);
+        z[0] = v.x; z[1] = v.y;
+    } else {
+#pragma unroll
+        for (int u = 0; u < GC; ++u) z[u] = ptr[u];
+    }
+}
+
+template <bool BF16>
+__device__ __forceinline__ float half_bits_to_f32(uint32_t bits) {
+    if constexpr (BF16) {
+        // bf16 -> fp16 -> f32, the cast the reference applies before quantising (moe_experts.py:596-597)
+        const float f = __uint_as_float(bits << 16);
+        return __half2float(__float2half(f));
+    } else {
+        return __half2float(__ushort_as_half(static_cast<unsigned short>(bits)));
+    }
+}
+
+// 32 consecutive fp16/bf16 values of a row -> absmax, or -> 32 e4m3 bytes (k8-interleaved).
+template <bool BF16>
+__device__ __forceinline__ float absmax32(const uint16_t* src) {
+    float m = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint4 v = reinterpret_cast<const uint4*>(src)[i];
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            m = fmaxf(m, fabsf(half_bits_to_f32<BF16>(w[j] & 0xFFFFu)));
+            m = fmaxf(m, fabsf(half_bits_to_f32<BF16>(w[j] >> 16)));
+        }
+    }
+    return m;
+}
+template <bool BF16>
+__device__ __forceinline__ v8i quant32(const uint16_t* src, float inv) {
+    v8i r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {   // 8 values per 16-byte load: k = 8i .. 8i+7
+        const uint4 v = reinterpret_cast<const uint4*>(src)[i];
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+        float f[8];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            f[2 * j] = half_bits_to_f32<BF16>(w[j] & 0xFFFFu) * inv;
+            f[2 * j + 1] = half_bits_to_f32<BF16>(w[j] >> 16) * inv;
+        }
+        r[2 * i] = (int)pack4_e4m3(f[0], f[2], f[4], f[6]);
+        r[2 * i + 1] = (int)pack4_e4m3(f[1], f[3], f[5], f[7]);
+    }
+    return r;
+}
+
+template <Epi EPI, int GPW, int KSPLIT>
+__global__ void __launch_bounds__(256, 2) grouped_gemv_kernel(Params p, int tpt) {
+    using C = GemvCfg<EPI, GPW, KSPLIT>;
+    extern __shared__ __attribute__((aligned(16))) uint8_t s_dyn[];   // KSPLIT > 1 partials
     __shared__ int s_src[kGemvMaxRows];
     __shared__ int s_slot[kGemvMaxRows];
     __shared__ int s_pad[kGemvMaxRows];
+    __shared__ float s_amax[4][16];
+    __shared__ float s_asc[16];
     __shared__ int s_mreal;
+    v4f* s_part = reinterpret_cast<v4f*>(s_dyn);   // [wave][tile][NF][lane]
 
     const int64_t row0 = (int64_t)blockIdx.y * p.block_m;
     const int ntp = p.ntp ? p.ntp[0] : (int)p.P;
     if (row0 >= ntp || row0 >= p.P) return;
-    const int e = p.expert_ids ? p.expert_ids[row0 / p.block_m] : 0;
+    const int e = p.expert_ids ? p.expert_ids[blockIdx.y] : 0;
     if (e < 0 || e >= p.E) return;
+
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
+    const int q = lane >> 4;           // k quarter of a group / D row quad of this lane
+    const int c16 = lane & 15;         // B column / A row of this lane
+    const int team = wave / KSPLIT;
+    const int g0 = (wave % KSPLIT) * GPW;
+    const int ncols = C::kSilu ? p.N / 2 : p.N;
+    const int ntiles = (ncols + 15) / 16;
+    const int kw_row = p.K / 8;
+    const int t_begin = (blockIdx.x * C::TEAMS + team) * tpt;
+    const int t_end = min(ntiles, t_begin + tpt);
+    const int nsets = t_end > t_begin ? (t_end - t_begin + C::CT - 1) / C::CT : 0;
+    const int nch = nsets * C::NB;
+    const int32_t* we = p.w + (int64_t)e * p.N * kw_row;
+    const __half* se = p.scales + (int64_t)e * p.N * p.G;
+    const int32_t* ze = p.zeros ? p.zeros + (int64_t)e * (p.N / 8) * p.G : nullptr;
+    constexpr float wscale = kNibbleScale;
 
-    // compact the block's real rows (wave 0, ballot prefix)
+    // weight row of fragment f in the tile set starting at tile t (edge columns read row 0:
+    // never stored, and the loads stay unconditional)
+    auto row_of = [&](int t, int f) -> int {
+        const int tt = t + f % C::CT;
+        const int col = tt * 16 + c16;
+        const bool up = C::kSilu && f >= C::CT;
+        return (tt < t_end && col < ncols) ? (up ? col + ncols : col) : 0;
+    };
+
+    uint4 wv[2][C::GC][C::FR];
+    uint32_t sw[2][C::FR][C::GC];
+    int32_t zw[2][C::FR][C::GC];
+    auto issue = [&](int c, auto bufc) {
+        constexpr int b = decltype(bufc)::value;
+        const int t = t_begin + (c / C::NB) * C::CT;
+        const int g = g0 + (c % C::NB) * C::GC;
+#pragma unroll
+        for (int f = 0; f < C::FR; ++f) {
+            const int n = row_of(t, f);
+            const int32_t* wr = we + (int64_t)n * kw_row + g * (kGroup / 8) + q * 4;
+#pragma unroll
+            for (int u = 0; u < C::GC; ++u)
+                wv[b][u][f] = *reinterpret_cast<const uint4*>(wr + u * (kGroup / 8));
+            load_scales<C::GC>(se + (int64_t)n * p.G + g, sw[b][f]);
+            if (ze) load_zero_words<C::GC>(ze + (int64_t)(n >> 3) * p.G + g, zw[b][f]);
+        }
+    };
+    using B0 = std::integral_constant<int, 0>;
+    using B1 = std::integral_constant<int, 1>;
+    // the first two chunks are in flight across the prologue
+    if (nch > 0) issue(0, B0{});
+    if (nch > 1) issue(1, B1{});
+
     if (wave == 0) {
         int slot = -1, src = -1;
         if (lane < p.block_m) src = resolve_row(p, row0 + lane, ntp, slot);
@@ -391,102 +558,169 @@ __global__ void __launch_bounds__(256) grouped_gemv_kernel(Params p) {
     }
     __syncthreads();
     const int mreal = s_mreal;
-    if (mreal == 0) return;
-    const int mtiles = (mreal + 15) >> 4;
 
-    const int ncols = kSilu ? p.N / 2 : p.N;
-    const int kw_row = p.K / 8;
-    const int32_t* we = p.w + (int64_t)e * p.N * kw_row;
-    const __half* se = p.scales + (int64_t)e * p.N * p.G;
-    const int32_t* ze = p.zeros ? p.zeros + (int64_t)e * (p.N / 8) * p.G : nullptr;
+    for (int m0 = 0; m0 < mreal; m0 += 16) {
+        if (m0 > 0) {
+            __syncthreads();                 // LDS partials of the previous pass consumed
+            if (nch > 0) issue(0, B0{});
+            if (nch > 1) issue(1, B1{});
+        }
+        // ---- activation fragments of rows m0 + c16 for this wave's groups ----
+        const int mrow = m0 + c16;
+        const int src = s_src[mrow < mreal ? mrow : m0];   // pad rows repeat a real row
+        v8i af[GPW];
+        float my_asc;
+        if (p.xq) {
+            const uint8_t* xr = p.xq + (int64_t)src * p.K + q * 32;
+#pragma unroll
+            for (int u = 0; u < GPW; ++u) {
+                const uint4 lo = *reinterpret_cast<const uint4*>(xr + (g0 + u) * kGroup);
+                const uint4 hi = *reinterpret_cast<const uint4*>(xr + (g0 + u) * kGroup + 16);
+                af[u] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w,
+                            (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+            }
+            my_asc = p.asc[src];
+        } else {
+            // per-row quantisation in place, bit-identical to act_quant_kernel
+            const uint16_t* xr = reinterpret_cast<const uint16_t*>(p.xh) + (int64_t)src * p.K + q * 32;
+            float amax = 0.f;
+#pragma unroll
+            for (int u = 0; u < GPW; ++u)
+                amax = fmaxf(amax, p.xbf16 ? absmax32<true>(xr + (g0 + u) * kGroup)
+                                           : absmax32<false>(xr + (g0 + u) * kGroup));
+            amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
+            amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+            if constexpr (KSPLIT > 1) {
+                if (q == 0) s_amax[wave][c16] = amax;
+                __syncthreads();
+#pragma unroll
+                for (int j = 0; j < KSPLIT; ++j) amax = fmaxf(amax, s_amax[team * KSPLIT + j][c16]);
+            }
+            my_asc = act_scale_from_absmax(amax);
+            const float inv = 1.0f / my_asc;
+#pragma unroll
+            for (int u = 0; u < GPW; ++u)
+                af[u] = p.xbf16 ? quant32<true>(xr + (g0 + u) * kGroup, inv)
+                                : quant32<false>(xr + (g0 + u) * kGroup, inv);
+        }
+        if (wave == 0 && q == 0) s_asc[c16] = my_asc * wscale;
+        v4f sa[GPW];   // 2^-9 * group sums of rows 4q..4q+3
+#pragma unroll
+        for (int u = 0; u < GPW; ++u) {
+            const int one = (int)kOnesE4m3;
+            sa[u] = mfma_16x16x128(af[u], v8i{one, one, one, one, one, one, one, one},
+                                   v4f{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sa[u][r] *= 1.0f / kNibbleScale;
+        }
+        float asc4[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) asc4[r] = __shfl(my_asc, 4 * q + r, 64) * wscale;
 
-    // this wave's tiles: output column tile base, lane's weight row per tile
-    const int col0 = (blockIdx.x * 4 + wave) * NT * 16;
-    int t_n[NTT];    // weight row feeding this lane's B fragment == scale row of its D column
-#pragma unroll
-    for (int j = 0; j < NTT; ++j) {
-        const int col = col0 + (j % NT) * 16 + (lane & 15);
-        const bool up = kSilu && j >= NT;
-        t_n[j] = col < ncols ? (up ? col + ncols : col) : -1;
-    }
-    // activation row pointers for each m-tile (lane's A row)
-    const uint8_t* a_ptr[MT_MAX];
-#pragma unroll
-    for (int i = 0; i < MT_MAX; ++i) {
-        const int m = i * 16 + (lane & 15);
-        a_ptr[i] = (m < mreal) ? p.xq + (int64_t)s_src[m] * p.K + (lane >> 4) * 32 : nullptr;
-    }
+        auto store = [&](int m, int col, float ra, float rb, float a) {
+            const int64_t row_pad = s_pad[m];
+            const int slot = s_slot[m];
+            if constexpr (EPI == Epi::kHalf) {
+                reinterpret_cast<__half*>(p.out)[row_pad * p.N + col] = __float2half(ra * a);
+            } else if constexpr (EPI == Epi::kSiluHalf) {
+                reinterpret_cast<__half*>(p.out)[row_pad * ncols + col] =
+                    silu_mul_h(__float2half(ra * a), __float2half(rb * a));
+            } else if constexpr (EPI == Epi::kScatter) {
+                atomicAdd(reinterpret_cast<float*>(p.out) + (int64_t)(slot / p.out_top_k) * p.N + col,
+                          p.tw[slot] * ra * a);
+            } else {
+                reinterpret_cast<float*>(p.out)[(int64_t)slot * p.N + col] = ra * a;
+            }
+        };
 
-    v4f run[MT_MAX][NTT];
+        v4f run[C::FR];
 #pragma unroll
-    for (int i = 0; i < MT_MAX; ++i)
-#pragma unroll
-        for (int j = 0; j < NTT; ++j) run[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+        for (int f = 0; f < C::FR; ++f) run[f] = v4f{0.f, 0.f, 0.f, 0.f};
 
-    for (int g0 = 0; g0 < p.G; g0 += kGemvUnroll) {
-        uint4 wv[kGemvUnroll][NTT];
-        int tab[kGemvUnroll][NTT];
-        float sc[kGemvUnroll][NTT];
+        auto consume = [&](int c, auto bufc) {
+            constexpr int b = decltype(bufc)::value;
+            constexpr int gb = C::NB == 2 ? b : 0;   // chunk parity == group batch when NB == 2
+            const int t = t_begin + (c / C::NB) * C::CT;
 #pragma unroll
-        for (int u = 0; u < kGemvUnroll; ++u) {
-            const int g = g0 + u;
+            for (int f = 0; f < C::FR; ++f) {
+                const int zsh = (row_of(t, f) & 7) * 4;
 #pragma unroll
-            for (int j = 0; j < NTT; ++j) {
-                const int n = t_n[j];
-                if (g < p.G && n >= 0) {
-                    wv[u][j] = *reinterpret_cast<const uint4*>(
-                        we + (int64_t)n * kw_row + g * (kGroup / 8) + (lane >> 4) * 4);
-                    tab[u][j] = table_index(ze, n, g, p.G, p.e2m1);
-                    sc[u][j] = __half2float(se[(int64_t)n * p.G + g]);
+                for (int u = 0; u < C::GC; ++u) {
+                    const int ua = gb * C::GC + u;
+                    v4f acc = mfma_16x16x128(af[ua], spread_nibbles(wv[b][u][f]),
+                                             v4f{0.f, 0.f, 0.f, 0.f});
+                    const float z = ze ? (float)((zw[b][f][u] >> zsh) & 0xF) : 8.0f;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[r] = fmaf(-z, sa[ua][r], acc[r]);
+                    const float s = scale_at<C::GC>(sw[b][f], u);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) run[f][r] = fmaf(acc[r], s, run[f][r]);
+                }
+            }
+            if (c % C::NB != C::NB - 1) return;
+            // tile set complete
+#pragma unroll
+            for (int ct = 0; ct < C::CT; ++ct) {
+                const int tt = t + ct;
+                if (tt >= t_end) continue;
+                if constexpr (KSPLIT > 1) {
+#pragma unroll
+                    for (int nf = 0; nf < C::NF; ++nf)
+                        s_part[((wave * tpt + (tt - t_begin)) * C::NF + nf) * 64 + lane] =
+                            run[nf * C::CT + ct];
                 } else {
-                    wv[u][j] = make_uint4(0, 0, 0, 0);
-                    tab[u][j] = 8;
-                    sc[u][j] = 0.f;
+                    const int col = tt * 16 + c16;
+                    if (col < ncols) {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const int m = m0 + 4 * q + r;
+                            if (m >= mreal) continue;
+                            store(m, col, run[ct][r], C::kSilu ? run[C::CT + ct][r] : 0.f, asc4[r]);
+                        }
+                    }
                 }
             }
-        }
 #pragma unroll
-        for (int u = 0; u < kGemvUnroll; ++u) {
-            const int g = g0 + u;
-            if (g >= p.G) break;
-            v8i bf[NTT];
-#pragma unroll
-            for (int j = 0; j < NTT; ++j) bf[j] = decode_frag(wv[u][j], load_table(tab[u][j]));
-#pragma unroll
-            for (int i = 0; i < MT_MAX; ++i) {
-                if (i >= mtiles) break;
-                v8i af = v8i{0, 0, 0, 0, 0, 0, 0, 0};
-                if (a_ptr[i]) {
-                    const uint4 lo = *reinterpret_cast<const uint4*>(a_ptr[i] + g * kGroup);
-                    const uint4 hi = *reinterpret_cast<const uint4*>(a_ptr[i] + g * kGroup + 16);
-                    af = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w,
-                             (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-                }
-#pragma unroll
-                for (int j = 0; j < NTT; ++j) {
-                    const v4f acc = mfma_16x16x128(af, bf[j], v4f{0.f, 0.f, 0.f, 0.f});
-#pragma unroll
-                    for (int r = 0; r < 4; ++r)
-                        run[i][j][r] = fmaf(acc[r], sc[u][j], run[i][j][r]);
-                }
-            }
-        }
-    }
+            for (int f = 0; f < C::FR; ++f) run[f] = v4f{0.f, 0.f, 0.f, 0.f};
+        };
 
-    // epilogue: D lane holds rows 4*(lane/16)+r of each m-tile, column lane%16
+        for (int c = 0; c < nch; c += 2) {
+            consume(c, B0{});
+            if (c + 2 < nch) issue(c + 2, B0{});
+            if (c + 1 < nch) {
+                consume(c + 1, B1{});
+                if (c + 3 < nch) issue(c + 3, B1{});
+            }
+        }
+
+        if constexpr (KSPLIT > 1) {
+            __syncthreads();
+            // sum the KSPLIT partials of every (team, tile, lane) in wave order, then store
+            const int items = C::TEAMS * tpt * 64;
+            for (int i = tid; i < items; i += 256) {
+                const int tm = i / (tpt * 64);
+                const int tl = (i >> 6) % tpt;
+                const int l = i & 63;
+                const int tt = (blockIdx.x * C::TEAMS + tm) * tpt + tl;
+                const int col = tt * 16 + (l & 15);
+                if (tt >= ntiles || col >= ncols) continue;
+                v4f sum[C::NF];
 #pragma unroll
-    for (int i = 0; i < MT_MAX; ++i) {
-        if (i >= mtiles) break;
+                for (int nf = 0; nf < C::NF; ++nf) {
+                    sum[nf] = s_part[(((tm * KSPLIT) * tpt + tl) * C::NF + nf) * 64 + l];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int m = i * 16 + (lane >> 4) * 4 + r;
-            if (m >= mreal) continue;
+                    for (int j = 1; j < KSPLIT; ++j) {
+                        const v4f v = s_part[(((tm * KSPLIT + j) * tpt + tl) * C::NF + nf) * 64 + l];
 #pragma unroll
-            for (int j = 0; j < NT; ++j) {
-                const int col = col0 + j * 16 + (lane & 15);
-                if (col >= ncols) continue;
-                const float rb = kSilu ? run[i][j + (kSilu ? NT : 0)][r] : 0.f;
-                store_out<EPI>(p, s_pad[m], s_src[m], s_slot[m], col, run[i][j][r], rb);
+                        for (int r = 0; r < 4; ++r) sum[nf][r] += v[r];
+                    }
+                }
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int mi = 4 * (l >> 4) + r;
+                    if (m0 + mi >= mreal) continue;
+                    store(m0 + mi, col, sum[0][r], C::kSilu ? sum[C::NF - 1][r] : 0.f, s_asc[mi]);
+                }
             }
         }
     }
@@ -496,6 +730,7 @@ Params make_params(const GroupedArgs& a) {
     Params p;
     p.xq = a.x_fp8;
     p.asc = a.act_scales;
+    p.xh = a.x;
     p.w = a.w;
     p.scales = reinterpret_cast<const __half*>(a.scales);
     p.zeros = a.zeros;
@@ -515,6 +750,7 @@ Params make_params(const GroupedArgs& a) {
     p.num_valid = (int)a.num_valid;
     p.identity = a.identity_gather ? 1 : 0;
     p.e2m1 = a.e2m1 ? 1 : 0;
+    p.xbf16 = a.x_bf16 ? 1 : 0;
     return p;
 }
 
@@ -556,18 +792,80 @@ int launch_mfma_e(const Params& p, hipStream_t s) {
     return W4A8_ERR_INVALID;
 }
 
-template <Epi EPI>
-int launch_gemv_e(const Params& p, hipStream_t s) {
-    constexpr int NT = 1;
-    const int ncols = EPI == Epi::kSiluHalf ? p.N / 2 : p.N;
-    const int cols_per_block = 4 * NT * 16;
-    dim3 grid((unsigned)((ncols + cols_per_block - 1) / cols_per_block),
+// Split of the K groups over waves: G == GPW * KSPLIT for the shapes below; others run
+// the matrix-core tiles.
+struct GemvSplit {
+    int gpw, ksplit;
+};
+GemvSplit gemv_split(int G) {
+    switch (G) {
+        case 1: return {1, 1};
+        case 2: return {2, 1};
+        case 3: return {3, 1};
+        case 4: return {4, 1};
+        case 8: return {4, 2};
+        case 12: return {3, 4};
+        case 16: return {4, 4};
+        default: return {0, 0};
+    }
+}
+
+// Column tiles per wave team: enough work per work-group to hide the prologue (~32 KB of
+// weights per wave), fewer when the grid would otherwise leave CUs idle.
+int gemv_default_tpt(const Params& p, int ntiles, int frag_bytes_per_tile_wave, int teams) {
+    const int64_t blocks = std::min<int64_t>((p.P + p.block_m - 1) / p.block_m, p.num_valid);
+    int tpt = std::max(1, (32 * 1024) / frag_bytes_per_tile_wave);
+    tpt = std::min(tpt, kGemvMaxTiles);
+    // keep >= ~1024 work-groups when the routing touches few blocks (T = 1 decode)
+    while (tpt > 1 && blocks * ((ntiles + teams * tpt - 1) / (teams * tpt)) < 1024) tpt >>= 1;
+    return tpt;
+}
+
+template <Epi EPI, int GPW, int KSPLIT>
+int launch_gemv_t(const Params& p, int tpt, hipStream_t s) {
+    using C = GemvCfg<EPI, GPW, KSPLIT>;
+    const int ncols = C::kSilu ? p.N / 2 : p.N;
+    const int ntiles = (ncols + 15) / 16;
+    if (tpt <= 0) tpt = gemv_default_tpt(p, ntiles, GPW * C::NF * 1024, C::TEAMS);
+    tpt = std::min(tpt, kGemvMaxTiles);
+    const size_t lds = KSPLIT > 1 ? (size_t)4 * tpt * C::NF * 64 * sizeof(v4f) : 0;
+    static bool attr_set = false;
+    if (!attr_set) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&grouped_gemv_kernel<EPI, GPW, KSPLIT>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize,
+                                4 * kGemvMaxTiles * C::NF * 64 * (int)sizeof(v4f)) != hipSuccess) {
+            set_error("grouped_gemv_kernel: cannot reserve dynamic LDS");
+            return W4A8_ERR_HIP;
+        }
+        attr_set = true;
+    }
+    dim3 grid((unsigned)((ntiles + C::TEAMS * tpt - 1) / (C::TEAMS * tpt)),
               (unsigned)((p.P + p.block_m - 1) / p.block_m));
-    grouped_gemv_kernel<EPI, NT><<<grid, 256, 0, s>>>(p);
+    grouped_gemv_kernel<EPI, GPW, KSPLIT><<<grid, 256, lds, s>>>(p, tpt);
     return check_launch("grouped_gemv_kernel");
 }
 
+template <Epi EPI>
+int launch_gemv_e(const Params& p, int tpt, hipStream_t s) {
+    const GemvSplit sp = gemv_split(p.G);
+    switch (sp.gpw * 8 + sp.ksplit) {
+        case 1 * 8 + 1: return launch_gemv_t<EPI, 1, 1>(p, tpt, s);
+        case 2 * 8 + 1: return launch_gemv_t<EPI, 2, 1>(p, tpt, s);
+        case 3 * 8 + 1: return launch_gemv_t<EPI, 3, 1>(p, tpt, s);
+        case 4 * 8 + 1: return launch_gemv_t<EPI, 4, 1>(p, tpt, s);
+        case 4 * 8 + 2: return launch_gemv_t<EPI, 4, 2>(p, tpt, s);
+        case 3 * 8 + 4: return launch_gemv_t<EPI, 3, 4>(p, tpt, s);
+        case 4 * 8 + 4: return launch_gemv_t<EPI, 4, 4>(p, tpt, s);
+    }
+    set_error("gemv grouped GEMM: unsupported number of K groups");
+    return W4A8_ERR_INVALID;
+}
+
 }  // namespace
+
+bool gemv_supported(int64_t K, int64_t group_size) {
+    return mfma_supported(K, group_size) && gemv_split((int)(K / group_size)).gpw > 0;
+}
 
 bool mfma_supported(int64_t K, int64_t group_size) {
     return group_size == kGroup && K % kGroup == 0;
@@ -597,20 +895,32 @@ int launch_grouped_mfma(const GroupedArgs& a, hipStream_t s) {
     return W4A8_ERR_INVALID;
 }
 
-int launch_grouped_gemv(const GroupedArgs& a, hipStream_t s) {
+int launch_grouped_gemv_tpt(const GroupedArgs& a, int tpt, hipStream_t s) {
     const Params p = make_params(a);
     if (p.P == 0) return W4A8_OK;
     if (p.block_m > kGemvMaxRows) {
         set_error("gemv grouped GEMM: block_m must be <= 64");
         return W4A8_ERR_INVALID;
     }
+    if (!gemv_supported(a.K, a.group_size)) {
+        set_error("gemv grouped GEMM: K / group_size must be one of 1,2,3,4,8,12,16");
+        return W4A8_ERR_INVALID;
+    }
+    if (a.e2m1) {
+        set_error("gemv grouped GEMM: E2M1 weights run on the matrix-core tiles");
+        return W4A8_ERR_INVALID;
+    }
     switch (a.epi) {
-        case Epi::kHalf: return launch_gemv_e<Epi::kHalf>(p, s);
-        case Epi::kSiluHalf: return launch_gemv_e<Epi::kSiluHalf>(p, s);
-        case Epi::kScatter: return launch_gemv_e<Epi::kScatter>(p, s);
-        case Epi::kSlotF32: return launch_gemv_e<Epi::kSlotF32>(p, s);
+        case Epi::kHalf: return launch_gemv_e<Epi::kHalf>(p, tpt, s);
+        case Epi::kSiluHalf: return launch_gemv_e<Epi::kSiluHalf>(p, tpt, s);
+        case Epi::kScatter: return launch_gemv_e<Epi::kScatter>(p, tpt, s);
+        case Epi::kSlotF32: return launch_gemv_e<Epi::kSlotF32>(p, tpt, s);
     }
     return W4A8_ERR_INVALID;
+}
+
+int launch_grouped_gemv(const GroupedArgs& a, hipStream_t s) {
+    return launch_grouped_gemv_tpt(a, 0, s);
 }
 
 }  // namespace w4a8

@@ -107,6 +107,10 @@ struct GroupedArgs {
 int launch_grouped_scalar(const GroupedArgs& a, hipStream_t stream);
 int launch_grouped_mfma(const GroupedArgs& a, hipStream_t stream);   // prefill tiles
 int launch_grouped_gemv(const GroupedArgs& a, hipStream_t stream);   // decode GEMV
+// Same, with an explicit column-tile count per wave team (0 = default heuristic).
+int launch_grouped_gemv_tpt(const GroupedArgs& a, int tiles_per_team, hipStream_t stream);
 bool mfma_supported(int64_t K, int64_t group_size);
+// mfma_supported and K / group_size in {1,2,3,4,8,12,16} (split-K table of the GEMV)
+bool gemv_supported(int64_t K, int64_t group_size);
 
 }  // namespace w4a8
