@@ -261,6 +261,8 @@ def moe_align(topk_ids, block_m: int, num_experts: int, expert_map=None):
     flat = ids.reshape(-1)
     if expert_map is not None:
         em = np.asarray(expert_map).astype(np.int64)
+        # vLLM passes global_num_experts with a global -> local map of that length
+        assert em.size == num_experts, "expert_map must have num_experts (global) entries"
         flat = np.where((flat >= 0) & (flat < em.size), em[np.clip(flat, 0, em.size - 1)], -1)
     P = align_alloc_len(numel, num_experts, block_m)
     sorted_ids = np.full(P, numel, dtype=np.int32)

@@ -138,11 +138,17 @@ void carve_apply(WS& w, const ApplyPlan& pl, int64_t T, int64_t H, int64_t inter
 }
 
 constexpr int kStageEvents = 8;
-thread_local hipEvent_t g_stage_events[kStageEvents];
+constexpr int kStageCalib = 8;   // optional 9th event: recorded right after event 1
+thread_local hipEvent_t g_stage_events[kStageEvents + 1];
 thread_local bool g_stage_on = false;
+thread_local bool g_stage_calib = false;
 
 inline void stage_mark(int i, hipStream_t s) {
-    if (g_stage_on) (void)hipEventRecord(g_stage_events[i], s);
+    if (!g_stage_on) return;
+    (void)hipEventRecord(g_stage_events[i], s);
+    // an empty bracket directly after a kernel launch: the marker latency every stage
+    // time includes
+    if (i == 1 && g_stage_calib) (void)hipEventRecord(g_stage_events[kStageCalib], s);
 }
 
 struct SizeProbe {
@@ -372,11 +378,13 @@ int w4a8_mmq_fp8_gemm(const void* x_f16, int64_t M, int64_t K, const int32_t* w_
 int w4a8_moe_apply_set_stage_events(void* const* events, int count) {
     clear_error();
     if (count == 0) { g_stage_on = false; return W4A8_OK; }
-    W4A8_REQUIRE(count == kStageEvents && events != nullptr, "stage events: need exactly 8 events");
-    for (int i = 0; i < kStageEvents; ++i) {
+    W4A8_REQUIRE((count == kStageEvents || count == kStageEvents + 1) && events != nullptr,
+                 "stage events: need 8 events (or 9 with the calibration event)");
+    for (int i = 0; i < count; ++i) {
         W4A8_REQUIRE(events[i] != nullptr, "stage events: null event");
         g_stage_events[i] = reinterpret_cast<hipEvent_t>(events[i]);
     }
+    g_stage_calib = count == kStageEvents + 1;
     g_stage_on = true;
     return W4A8_OK;
 }
