@@ -110,7 +110,7 @@ class HipEvents:
             self.hip.hipEventDestroy(e)
 
 
-STAGES = ["align", "act_quant_x", "acc_clear", "gemm1_silu", "act_quant_h", "gemm2",
+STAGES = ["align", "act_quant_x", "reserved", "gemm1_silu", "act_quant_h", "gemm2",
           "reduce_cast"]
 
 
@@ -272,7 +272,7 @@ def main():
         achieved = g1_flops / (g1_ms * 1e-3) / 1e12
         roof = dict(bound="mfma", achieved=round(achieved, 1), peak=FP8_PEAK_TFLOPS,
                     unit="TFLOP/s", frac=round(achieved / FP8_PEAK_TFLOPS, 4), traffic=None,
-                    kernel="grouped_mfma_kernel<kSiluHalf> (gemm1+SiLU)",
+                    kernel="prefill_mfma_kernel<kSiluHalf, 4> (gemm1+SiLU)",
                     algorithmic_flops=g1_flops, avg_ms=round(g1_ms, 5))
     layer_s = ms_per_step * 1e-3
     value = T / layer_s

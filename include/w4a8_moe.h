@@ -192,7 +192,7 @@ W4A8_API int w4a8_moe_apply(const void* x, int x_dtype, int64_t T, int64_t H, in
 
 /* Optional per-stage timing of w4a8_moe_apply on the calling thread: when count == 8,
  * the next w4a8_moe_apply calls record events[0] before the first launch and events[i]
- * after stage i (1 align, 2 act-quant x, 3 accumulator clear, 4 gemm1+SiLU, 5 act-quant
+ * after stage i (1 align, 2 act-quant x, 3 reserved (empty), 4 gemm1+SiLU, 5 act-quant
  * h, 6 gemm2, 7 reduce/cast) on their stream. With count == 9, events[8] is recorded
  * immediately after events[1] (an empty bracket right after a kernel: the marker latency
  * included in every stage time). Events are hipEvent_t handles owned by the caller;

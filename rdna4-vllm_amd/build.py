@@ -39,8 +39,15 @@ def hipcc() -> str:
     return cand
 
 
+# Per-file extras: the prefill tiles keep MFMA results in VGPRs (the fp32 scale fold reads
+# every result once; from AGPRs each read would cost an extra v_accvgpr_read).
+EXTRA_FLAGS = {
+    "prefill_gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+}
+
+
 def _compile(src: Path, obj: Path) -> None:
-    cmd = [hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *HIPCC_FLAGS, *EXTRA_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{r.stdout}\n{r.stderr}")

@@ -63,19 +63,23 @@ int run_grouped(GroupedArgs& a, int64_t kernel, void* ws, size_t ws_bytes, hipSt
     Workspace w(ws, ws_bytes);
     a.x_fp8 = w.take<uint8_t>((size_t)(a.x_rows * a.K));
     a.act_scales = w.take<float>((size_t)a.x_rows);
+    float* gsum = w.take<float>((size_t)(a.x_rows * ((a.K + 127) / 128)));
     if ((a.x_rows > 0 && ws == nullptr) || !w.ok()) {
         set_error("workspace smaller than w4a8_moe_gemm_workspace_size()");
         return W4A8_ERR_WORKSPACE;
     }
+    // gemv for K-group counts outside its split-K table runs the matrix-core tiles
+    const bool tiles = (kernel == W4A8_MOE_KERNEL_WMMA || kernel == W4A8_MOE_KERNEL_GEMV) && mfma;
+    const bool prefill = tiles && prefill_supported(a.K, a.group_size, a.e2m1);
+    a.act_group_sums = prefill ? gsum : nullptr;
     // identity-gathered inputs (gemm2 / scatter) have one row per padded row: skip padding.
     const bool filter = a.identity_gather && a.sorted_ids != nullptr;
     if (int rc = launch_act_quant(a.x, a.x_bf16, a.x_rows, a.K, a.x_fp8, a.act_scales, true, s,
                                   filter ? a.sorted_ids : nullptr, filter ? a.ntp : nullptr,
-                                  a.num_valid))
+                                  a.num_valid, a.act_group_sums))
         return rc;
-    // gemv for K-group counts outside its split-K table runs the matrix-core tiles
-    if ((kernel == W4A8_MOE_KERNEL_WMMA || kernel == W4A8_MOE_KERNEL_GEMV) && mfma)
-        return launch_grouped_mfma(a, s);
+    if (prefill) return launch_grouped_prefill(a, s);
+    if (tiles) return launch_grouped_mfma(a, s);
     return launch_grouped_scalar(a, s);
 }
 
@@ -102,7 +106,7 @@ namespace w4a8 {
 namespace {
 constexpr int64_t kGemvMaxM = 96;   // moe_experts.py:563 GEMV_MAX_M
 constexpr int64_t kDecodeBlockM = 16;
-constexpr int64_t kPrefillBlockM = 64;
+constexpr int64_t kPrefillBlockM = 64;    // 64-row tiles; empty 16-row fragments are skipped
 
 struct ApplyPlan {
     bool decode;
@@ -122,7 +126,8 @@ template <typename WS>
 void carve_apply(WS& w, const ApplyPlan& pl, int64_t T, int64_t H, int64_t inter, int64_t E,
                  int64_t top_k, int32_t** sti, int32_t** eid, int32_t** ntp, void** align_ws,
                  size_t* align_bytes, uint8_t** xq, float** s1, __half** h, uint8_t** hq,
-                 float** s2, float** acc) {
+                 float** s2, float** acc, float** gs1, float** gs2, __half** y,
+                 int32_t** s2r) {
     *sti = w.template take<int32_t>((size_t)pl.P);
     *eid = w.template take<int32_t>((size_t)pl.nblk);
     *ntp = w.template take<int32_t>(1);
@@ -133,8 +138,14 @@ void carve_apply(WS& w, const ApplyPlan& pl, int64_t T, int64_t H, int64_t inter
     *h = w.template take<__half>((size_t)(pl.P * inter));
     *hq = w.template take<uint8_t>((size_t)(pl.P * inter));
     *s2 = w.template take<float>((size_t)pl.P);
-    // decode: per-slot fp32 rows (T*k, H); prefill: fp32 (T, H) scatter accumulator
-    *acc = w.template take<float>((size_t)((pl.decode ? T * top_k : T) * H));
+    // decode: per-slot fp32 rows (T*k, H); prefill: fp16 rows (P, H) in padded order and the
+    // slot -> padded-row map the combine reads
+    *acc = pl.decode ? w.template take<float>((size_t)(T * top_k * H)) : nullptr;
+    *y = pl.decode ? nullptr : w.template take<__half>((size_t)(pl.P * H));
+    *s2r = pl.decode ? nullptr : w.template take<int32_t>((size_t)(T * top_k));
+    // prefill: per-group sums of the quantised rows (zero-point term of the tiles)
+    *gs1 = pl.decode ? nullptr : w.template take<float>((size_t)(T * ((H + 127) / 128)));
+    *gs2 = pl.decode ? nullptr : w.template take<float>((size_t)(pl.P * ((inter + 127) / 128)));
 }
 
 constexpr int kStageEvents = 8;
@@ -232,6 +243,7 @@ size_t w4a8_moe_gemm_workspace_size(int64_t x_rows, int64_t K) {
     WorkspaceSize s;
     s.take<uint8_t>((size_t)(x_rows * K));
     s.take<float>((size_t)x_rows);
+    s.take<float>((size_t)(x_rows * ((K + 127) / 128)));   // per-group sums (prefill tiles)
     return s.used;
 }
 
@@ -394,8 +406,9 @@ size_t w4a8_moe_apply_workspace_size(int64_t T, int64_t H, int64_t inter, int64_
     const ApplyPlan pl = plan_apply(T, E, top_k);
     SizeProbe sp;
     int32_t *a, *b, *c; void* d; size_t db; uint8_t* e; float* f; __half* g; uint8_t* h;
-    float *i, *j;
-    carve_apply(sp, pl, T, H, inter, E, top_k, &a, &b, &c, &d, &db, &e, &f, &g, &h, &i, &j);
+    float *i, *j, *k, *l; __half* m; int32_t* n;
+    carve_apply(sp, pl, T, H, inter, E, top_k, &a, &b, &c, &d, &db, &e, &f, &g, &h, &i, &j, &k,
+                &l, &m, &n);
     return sp.s.used;
 }
 
@@ -422,9 +435,9 @@ int w4a8_moe_apply(const void* x, int x_dtype, int64_t T, int64_t H, int64_t int
     const ApplyPlan pl = plan_apply(T, E, top_k);
     Workspace w(workspace, workspace_bytes);
     int32_t *sti, *eid, *ntp; void* aws; size_t abytes; uint8_t* xq; float* s1; __half* h;
-    uint8_t* hq; float* s2; float* acc;
+    uint8_t* hq; float* s2; float* acc; float* gs1; float* gs2; __half* y; int32_t* s2r;
     carve_apply(w, pl, T, H, inter, E, top_k, &sti, &eid, &ntp, &aws, &abytes, &xq, &s1, &h, &hq,
-                &s2, &acc);
+                &s2, &acc, &gs1, &gs2, &y, &s2r);
     if (workspace == nullptr || !w.ok()) {
         set_error("moe_apply: workspace smaller than w4a8_moe_apply_workspace_size()");
         return W4A8_ERR_WORKSPACE;
@@ -434,16 +447,19 @@ int w4a8_moe_apply(const void* x, int x_dtype, int64_t T, int64_t H, int64_t int
     const int64_t numel = T * top_k;
     stage_mark(0, s);
     if (int rc = launch_align(topk_ids, numel, E, pl.block_m, expert_map, sti, pl.P, eid, ntp,
-                              aws, abytes, s))
+                              aws, abytes, s, s2r))
         return rc;
     stage_mark(1, s);
-    if (int rc = launch_act_quant(x, bf16, T, H, xq, s1, true, s)) return rc;
+    const bool mfma = mfma_supported(H, group_size) && mfma_supported(inter, group_size);
+    // prefill tiles need the per-group sums of the quantised rows (zero-point term)
+    const bool pf1 = !pl.decode && mfma && prefill_supported(H, group_size, e2m1);
+    const bool pf2 = !pl.decode && mfma && prefill_supported(inter, group_size, e2m1);
+    if (int rc = launch_act_quant(x, bf16, T, H, xq, s1, true, s, nullptr, nullptr, 0,
+                                  pf1 ? gs1 : nullptr))
+        return rc;
     stage_mark(2, s);
-    if (!pl.decode)
-        if (int rc = launch_zero_f32(acc, T * H, s)) return rc;
     stage_mark(3, s);
 
-    const bool mfma = mfma_supported(H, group_size) && mfma_supported(inter, group_size);
     // gemm1 + SiLU*mul -> h (P, inter)
     GroupedArgs g1{};
     g1.x_rows = T; g1.K = H; g1.w = w13; g1.scales = static_cast<const uint16_t*>(w13_scales_f16);
@@ -451,16 +467,19 @@ int w4a8_moe_apply(const void* x, int x_dtype, int64_t T, int64_t H, int64_t int
     g1.sorted_ids = sti; g1.P = pl.P; g1.expert_ids = eid; g1.ntp = ntp; g1.top_k = top_k;
     g1.identity_gather = false; g1.num_valid = numel; g1.block_m = pl.block_m; g1.e2m1 = e2m1;
     g1.epi = Epi::kSiluHalf; g1.out = h; g1.out_top_k = top_k; g1.x_fp8 = xq; g1.act_scales = s1;
+    g1.act_group_sums = pf1 ? gs1 : nullptr;
     int rc;
     if (!mfma) rc = launch_grouped_scalar(g1, s);
     else if (pl.decode && !e2m1 && gemv_supported(H, group_size)) rc = launch_grouped_gemv(g1, s);
+    else if (pf1) rc = launch_grouped_prefill(g1, s);
     else rc = launch_grouped_mfma(g1, s);
     if (rc) return rc;
     stage_mark(4, s);
     // act-quant of h over real rows only (the decode GEMV quantises its rows itself)
     const bool fuse_aq2 = pl.decode && !e2m1 && gemv_supported(inter, group_size);
     if (!fuse_aq2)
-        if ((rc = launch_act_quant(h, false, pl.P, inter, hq, s2, true, s, sti, ntp, numel)))
+        if ((rc = launch_act_quant(h, false, pl.P, inter, hq, s2, true, s, sti, ntp, numel,
+                                   pf2 ? gs2 : nullptr)))
             return rc;
     stage_mark(5, s);
     // gemm2 (identity gather) -> per-slot rows (decode) or scatter (prefill)
@@ -469,21 +488,24 @@ int w4a8_moe_apply(const void* x, int x_dtype, int64_t T, int64_t H, int64_t int
     g2.zeros = w2_zeros; g2.E = E; g2.N = H; g2.group_size = group_size;
     g2.sorted_ids = sti; g2.P = pl.P; g2.expert_ids = eid; g2.ntp = ntp; g2.top_k = top_k;
     g2.identity_gather = true; g2.num_valid = numel; g2.block_m = pl.block_m; g2.e2m1 = e2m1;
-    g2.epi = pl.decode ? Epi::kSlotF32 : Epi::kScatter; g2.out = acc;
+    g2.epi = pl.decode ? Epi::kSlotF32 : Epi::kHalf; g2.out = pl.decode ? (void*)acc : (void*)y;
     g2.topk_weights = topk_weights; g2.out_top_k = top_k;
     g2.x = h; g2.x_bf16 = false;
     g2.x_fp8 = fuse_aq2 ? nullptr : hq;
     g2.act_scales = fuse_aq2 ? nullptr : s2;
+    g2.act_group_sums = pf2 ? gs2 : nullptr;
     if (!mfma) rc = launch_grouped_scalar(g2, s);
     else if (fuse_aq2) rc = launch_grouped_gemv(g2, s);
+    else if (pf2) rc = launch_grouped_prefill(g2, s);
     else rc = launch_grouped_mfma(g2, s);
     if (rc) return rc;
     stage_mark(6, s);
-    if (pl.decode)   // slots whose expert is not local / out of range contribute nothing
+    // slots whose expert is not local / out of range contribute nothing
+    if (pl.decode)
         rc = launch_slot_reduce(acc, topk_weights, topk_ids, expert_map, E, T, H, top_k, out,
                                 bf16, s);
     else
-        rc = launch_cast_f32(acc, T * H, out, bf16, s);
+        rc = launch_row_reduce(y, s2r, topk_weights, T, H, top_k, out, bf16, s);
     stage_mark(7, s);
     return rc;
 }

@@ -21,11 +21,13 @@ __device__ __forceinline__ float load_act(const void* x, int64_t i) {
 // One wave per row: absmax, scale, quantise (moe_kernel.hip:87-127).
 // Optional row filter (sorted_ids/ntp/num_valid): rows that are padding in the
 // moe_align layout are skipped, so uninitialised padding rows are never read.
+// Optional gsum (rows, K/128): the sum of the e4m3 values of each 128-wide group, which
+// the prefill GEMM uses for its zero-point term (needs K % 128 == 0).
 template <bool BF16>
 __global__ void __launch_bounds__(256) act_quant_kernel(
     const void* __restrict__ x, int64_t rows, int K, uint8_t* __restrict__ q,
     float* __restrict__ scales, bool k8, const int32_t* __restrict__ sorted_ids,
-    const int32_t* __restrict__ ntp, int64_t num_valid) {
+    const int32_t* __restrict__ ntp, int64_t num_valid, float* __restrict__ gsum) {
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
     if (row >= rows) return;
@@ -40,19 +42,34 @@ __global__ void __launch_bounds__(256) act_quant_kernel(
     const float s = act_scale_from_absmax(amax);
     if (lane == 0) scales[row] = s;
     const float inv = 1.0f / s;
-    for (int k = lane * 8; k < K; k += 64 * 8) {
-        float v[8];
+    // every lane runs every 512-wide pass (inactive lanes add zero) so the group-sum
+    // shuffles always see a full wave
+    for (int k0 = 0; k0 < K; k0 += 64 * 8) {
+        const int k = k0 + lane * 8;
+        uint32_t lo = 0, hi = 0;
+        if (k < K) {
+            float v[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = load_act<BF16>(x, base + k + j) * inv;
-        uint32_t lo, hi;
-        if (k8) {
-            lo = pack4_e4m3(v[0], v[2], v[4], v[6]);
-            hi = pack4_e4m3(v[1], v[3], v[5], v[7]);
-        } else {
-            lo = pack4_e4m3(v[0], v[1], v[2], v[3]);
-            hi = pack4_e4m3(v[4], v[5], v[6], v[7]);
+            for (int j = 0; j < 8; ++j) v[j] = load_act<BF16>(x, base + k + j) * inv;
+            if (k8) {
+                lo = pack4_e4m3(v[0], v[2], v[4], v[6]);
+                hi = pack4_e4m3(v[1], v[3], v[5], v[7]);
+            } else {
+                lo = pack4_e4m3(v[0], v[1], v[2], v[3]);
+                hi = pack4_e4m3(v[4], v[5], v[6], v[7]);
+            }
+            *reinterpret_cast<uint2*>(q + base + k) = make_uint2(lo, hi);
         }
-        *reinterpret_cast<uint2*>(q + base + k) = make_uint2(lo, hi);
+        if (gsum != nullptr) {
+            // lanes 16j..16j+15 hold group k/128 of this pass: fixed-order tree sum
+            float t = 0.f;
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+                t += e4m3_to_f32((lo >> (8 * b)) & 0xFF) + e4m3_to_f32((hi >> (8 * b)) & 0xFF);
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) t += __shfl_xor(t, o, 64);
+            if ((lane & 15) == 0 && k < K) gsum[row * (K / 128) + k / 128] = t;
+        }
     }
 }
 
@@ -148,6 +165,44 @@ __global__ void slot_reduce_kernel(const float* __restrict__ y, const float* __r
     }
 }
 
+// Prefill combine (moe_kernel.hip:1241-1258 with the inverse map built by the align):
+// eight columns per thread, fp32 accumulation over j ascending.
+template <bool BF16>
+__global__ void row_reduce_kernel(const __half* __restrict__ y, const int32_t* __restrict__ s2r,
+                                  const float* __restrict__ tw, int64_t T, int N, int top_k,
+                                  void* __restrict__ out) {
+    const int64_t t = blockIdx.y;
+    const int n = (blockIdx.x * blockDim.x + threadIdx.x) * 8;
+    if (n >= N || t >= T) return;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < top_k; ++j) {
+        const int32_t r = s2r[t * top_k + j];
+        if (r < 0) continue;
+        const float w = tw[t * top_k + j];
+        const uint4 v = *reinterpret_cast<const uint4*>(y + (int64_t)r * N + n);
+        const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            acc[2 * i] = fmaf(w, __half2float(__ushort_as_half((unsigned short)(u[i] & 0xFFFFu))), acc[2 * i]);
+            acc[2 * i + 1] = fmaf(w, __half2float(__ushort_as_half((unsigned short)(u[i] >> 16))), acc[2 * i + 1]);
+        }
+    }
+    uint32_t o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if constexpr (BF16) {
+            const uint32_t lo = __bfloat16_as_ushort(__float2bfloat16(acc[2 * i]));
+            const uint32_t hi = __bfloat16_as_ushort(__float2bfloat16(acc[2 * i + 1]));
+            o[i] = lo | (hi << 16);
+        } else {
+            const uint32_t lo = __half_as_ushort(__float2half(acc[2 * i]));
+            const uint32_t hi = __half_as_ushort(__float2half(acc[2 * i + 1]));
+            o[i] = lo | (hi << 16);
+        }
+    }
+    *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(out) + t * N + n) = make_uint4(o[0], o[1], o[2], o[3]);
+}
+
 template <bool BF16>
 __global__ void cast_f32_kernel(const float* __restrict__ in, int64_t n, void* __restrict__ out) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -173,15 +228,19 @@ inline unsigned blocks_for(int64_t n, int per) { return (unsigned)((n + per - 1)
 
 int launch_act_quant(const void* x, bool x_bf16, int64_t rows, int64_t K, uint8_t* x_fp8,
                      float* scales, bool k8, hipStream_t stream, const int32_t* sorted_ids,
-                     const int32_t* ntp, int64_t num_valid) {
+                     const int32_t* ntp, int64_t num_valid, float* group_sums) {
     if (rows == 0) return W4A8_OK;
+    if (group_sums != nullptr && K % 128 != 0) {
+        set_error("act_quant: group sums need K % 128 == 0");
+        return W4A8_ERR_INVALID;
+    }
     dim3 grid(blocks_for(rows, kWavesPerBlock)), block(64 * kWavesPerBlock);
     if (x_bf16)
         act_quant_kernel<true><<<grid, block, 0, stream>>>(x, rows, (int)K, x_fp8, scales, k8,
-                                                          sorted_ids, ntp, num_valid);
+                                                          sorted_ids, ntp, num_valid, group_sums);
     else
         act_quant_kernel<false><<<grid, block, 0, stream>>>(x, rows, (int)K, x_fp8, scales, k8,
-                                                           sorted_ids, ntp, num_valid);
+                                                           sorted_ids, ntp, num_valid, group_sums);
     return check_launch("act_quant_kernel");
 }
 
@@ -235,6 +294,22 @@ int launch_slot_reduce(const float* y, const float* tw, const int32_t* ids,
         slot_reduce_kernel<false><<<grid, 256, 0, stream>>>(y, tw, ids, emap, (int)E, T, (int)N,
                                                            (int)top_k, out);
     return check_launch("slot_reduce_kernel");
+}
+
+int launch_row_reduce(const void* y, const int32_t* s2r, const float* tw, int64_t T,
+                      int64_t N, int64_t top_k, void* out, bool out_bf16, hipStream_t stream) {
+    if (T == 0 || N == 0) return W4A8_OK;
+    if (N % 8 != 0) {
+        set_error("row_reduce: N must be a multiple of 8");
+        return W4A8_ERR_INVALID;
+    }
+    dim3 grid(blocks_for(N / 8, 256), (unsigned)T);
+    const __half* yh = static_cast<const __half*>(y);
+    if (out_bf16)
+        row_reduce_kernel<true><<<grid, 256, 0, stream>>>(yh, s2r, tw, T, (int)N, (int)top_k, out);
+    else
+        row_reduce_kernel<false><<<grid, 256, 0, stream>>>(yh, s2r, tw, T, (int)N, (int)top_k, out);
+    return check_launch("row_reduce_kernel");
 }
 
 int launch_cast_f32(const float* in, int64_t n, void* out, bool out_bf16, hipStream_t stream) {

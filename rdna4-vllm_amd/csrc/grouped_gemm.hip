@@ -19,40 +19,10 @@
 
 #include "w4a8_common.h"
 #include "w4a8_internal.h"
+#include "grouped_params.h"
 
 namespace w4a8 {
 namespace {
-
-struct Params {
-    const uint8_t* xq;          // (x_rows, K) e4m3, k8-interleaved
-    const float* asc;           // (x_rows,)
-    const void* xh;             // (x_rows, K) fp16/bf16 rows (fused quantisation path)
-    const int32_t* w;           // (E, N, K/8)
-    const __half* scales;       // (E, N, G)
-    const int32_t* zeros;       // (E, N/8, G) or null
-    const int32_t* sorted_ids;
-    const int32_t* expert_ids;
-    const int32_t* ntp;
-    void* out;
-    const float* tw;
-    int64_t P;
-    int K, N, G, E;
-    int top_k, out_top_k, block_m;
-    int num_valid;
-    int identity;
-    int e2m1;
-    int xbf16;                  // xh holds bf16 (else fp16)
-};
-
-// Row resolution shared by all schedules. Returns the activation row (or -1).
-__device__ __forceinline__ int resolve_row(const Params& p, int64_t r, int ntp, int& slot) {
-    slot = -1;
-    if (r >= p.P || r >= ntp) return -1;
-    const int s = p.sorted_ids ? p.sorted_ids[r] : (int)r;   // dense: identity rows
-    if (s < 0 || s >= p.num_valid) return -1;
-    slot = s;
-    return p.identity ? (int)r : s / p.top_k;
-}
 
 template <Epi EPI>
 __device__ __forceinline__ void store_out(const Params& p, int64_t row_pad, int src, int slot,
@@ -128,10 +98,6 @@ __global__ void __launch_bounds__(256) grouped_scalar_kernel(Params p) {
 // =====================================================================================
 // MFMA helpers
 // =====================================================================================
-__device__ __forceinline__ v4f mfma_16x16x128(const v8i& a, const v8i& b, const v4f& c) {
-    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
-}
-
 // 4 words (32 nibbles, k = 0..31 of a fragment) -> 8 dwords of e4m3 (k8-interleaved).
 __device__ __forceinline__ v8i decode_frag(uint4 wv, uint4 t) {
     uint32_t o[8];
@@ -148,7 +114,6 @@ __device__ __forceinline__ v8i decode_frag(uint4 wv, uint4 t) {
 // =====================================================================================
 // MFMA tiled (prefill) kernel
 // =====================================================================================
-constexpr int kGroup = 128;          // K per group == K per MFMA
 constexpr int kLdsStride = kGroup + 16;
 
 template <Epi EPI, int BM, int BN>
@@ -373,7 +338,6 @@ __global__ void __launch_bounds__(256) grouped_mfma_kernel(Params p) {
 constexpr int kGemvMaxRows = 64;                 // block_m cap (16-row passes)
 constexpr int kGemvMaxTiles = 8;                 // tiles per team (LDS partials bound)
 constexpr uint32_t kOnesE4m3 = 0x38383838u;      // four e4m3 bytes of 1.0
-constexpr float kNibbleScale = 512.0f;
 
 template <Epi EPI, int GPW, int KSPLIT>
 struct GemvCfg {
@@ -388,12 +352,6 @@ struct GemvCfg {
     static_assert(GPW % GC == 0 && (NB == 1 || NB == 2), "unsupported groups per wave");
     static_assert(KSPLIT == 1 || KSPLIT == 2 || KSPLIT == 4, "KSPLIT divides the 4 waves");
 };
-
-__device__ __forceinline__ v8i spread_nibbles(uint4 w) {
-    constexpr uint32_t m = 0x0F0F0F0Fu;
-    return v8i{(int)(w.x & m), (int)((w.x >> 4) & m), (int)(w.y & m), (int)((w.y >> 4) & m),
-               (int)(w.z & m), (int)((w.z >> 4) & m), (int)(w.w & m), (int)((w.w >> 4) & m)};
-}
 
 // GC consecutive fp16 scales; packed two per word when the vector load is aligned.
 template <int GC>
@@ -724,34 +682,6 @@ __global__ void __launch_bounds__(256, 2) grouped_gemv_kernel(Params p, int tpt)
             }
         }
     }
-}
-
-Params make_params(const GroupedArgs& a) {
-    Params p;
-    p.xq = a.x_fp8;
-    p.asc = a.act_scales;
-    p.xh = a.x;
-    p.w = a.w;
-    p.scales = reinterpret_cast<const __half*>(a.scales);
-    p.zeros = a.zeros;
-    p.sorted_ids = a.sorted_ids;
-    p.expert_ids = a.expert_ids;
-    p.ntp = a.ntp;
-    p.out = a.out;
-    p.tw = a.topk_weights;
-    p.P = a.P;
-    p.K = (int)a.K;
-    p.N = (int)a.N;
-    p.G = (int)(a.K / a.group_size);
-    p.E = (int)a.E;
-    p.top_k = (int)a.top_k;
-    p.out_top_k = (int)a.out_top_k;
-    p.block_m = (int)a.block_m;
-    p.num_valid = (int)a.num_valid;
-    p.identity = a.identity_gather ? 1 : 0;
-    p.e2m1 = a.e2m1 ? 1 : 0;
-    p.xbf16 = a.x_bf16 ? 1 : 0;
-    return p;
 }
 
 template <Epi EPI>

@@ -121,7 +121,8 @@ __device__ void write_layout(const int* cnt, const int* eoff, int E, int64_t blo
 __global__ void __launch_bounds__(kAlignThreads) align_small_kernel(
     const int32_t* __restrict__ ids, int64_t numel, int E, int64_t block_m,
     const int32_t* __restrict__ emap, int32_t* __restrict__ sorted_ids, int64_t sorted_len,
-    int32_t* __restrict__ expert_ids, int32_t* __restrict__ ntp) {
+    int32_t* __restrict__ expert_ids, int32_t* __restrict__ ntp,
+    int32_t* __restrict__ slot_to_row) {
     __shared__ ChunkScratch s;
     __shared__ int eoff[kMaxExperts];
     int rank;
@@ -133,6 +134,7 @@ __global__ void __launch_bounds__(kAlignThreads) align_small_kernel(
     if (tid < E) eoff[tid] = off;
     __syncthreads();
     if (e >= 0) sorted_ids[eoff[e] + rank] = tid;
+    if (slot_to_row != nullptr && tid < numel) slot_to_row[tid] = e >= 0 ? eoff[e] + rank : -1;
     write_layout(s.hist, eoff, E, block_m, numel, total, sorted_ids, sorted_len, expert_ids,
                  ntp);
 }
@@ -184,14 +186,15 @@ __global__ void __launch_bounds__(kAlignThreads) align_scan_kernel(
 __global__ void __launch_bounds__(kAlignThreads) align_place_kernel(
     const int32_t* __restrict__ ids, int64_t numel, int E, const int32_t* __restrict__ emap,
     const int32_t* __restrict__ chunk_base, const int32_t* __restrict__ eoff,
-    int32_t* __restrict__ sorted_ids) {
+    int32_t* __restrict__ sorted_ids, int32_t* __restrict__ slot_to_row) {
     __shared__ ChunkScratch s;
     int rank;
     const int64_t base = (int64_t)blockIdx.x * kChunk;
     const int e = chunk_rank(ids, numel, base, emap, E, s, rank);
-    if (e >= 0)
-        sorted_ids[eoff[e] + chunk_base[(int64_t)blockIdx.x * E + e] + rank] =
-            (int32_t)(base + threadIdx.x);
+    const int64_t slot = base + threadIdx.x;
+    const int row = e >= 0 ? eoff[e] + chunk_base[(int64_t)blockIdx.x * E + e] + rank : -1;
+    if (e >= 0) sorted_ids[row] = (int32_t)slot;
+    if (slot_to_row != nullptr && slot < numel) slot_to_row[slot] = row;
 }
 
 // ---- router: one wave per token ----
@@ -267,7 +270,7 @@ size_t align_workspace_bytes(int64_t numel, int64_t num_experts) {
 int launch_align(const int32_t* ids, int64_t numel, int64_t E, int64_t block_m,
                  const int32_t* emap, int32_t* sorted_ids, int64_t sorted_len,
                  int32_t* expert_ids, int32_t* ntp, void* ws, size_t ws_bytes,
-                 hipStream_t stream) {
+                 hipStream_t stream, int32_t* slot_to_row) {
     if (E > kMaxExperts) {
         set_error("moe_align: num_experts must be <= 1024");
         return W4A8_ERR_INVALID;
@@ -275,7 +278,7 @@ int launch_align(const int32_t* ids, int64_t numel, int64_t E, int64_t block_m,
     if (numel <= kChunk) {
         align_small_kernel<<<1, kAlignThreads, 0, stream>>>(ids, numel, (int)E, block_m, emap,
                                                            sorted_ids, sorted_len, expert_ids,
-                                                           ntp);
+                                                           ntp, slot_to_row);
         return check_launch("align_small_kernel");
     }
     const int64_t nchunks = (numel + kChunk - 1) / kChunk;
@@ -295,7 +298,7 @@ int launch_align(const int32_t* ids, int64_t numel, int64_t E, int64_t block_m,
     if (int rc = check_launch("align_scan_kernel")) return rc;
     align_place_kernel<<<(unsigned)nchunks, kAlignThreads, 0, stream>>>(ids, numel, (int)E, emap,
                                                                         counts, eoff,
-                                                                        sorted_ids);
+                                                                        sorted_ids, slot_to_row);
     return check_launch("align_place_kernel");
 }
 

@@ -46,7 +46,7 @@ struct WorkspaceSize {
 int launch_act_quant(const void* x, bool x_bf16, int64_t rows, int64_t K, uint8_t* x_fp8,
                      float* scales, bool k8_interleave, hipStream_t stream,
                      const int32_t* sorted_ids = nullptr, const int32_t* ntp = nullptr,
-                     int64_t num_valid = 0);
+                     int64_t num_valid = 0, float* group_sums = nullptr);
 int launch_dequant(const int32_t* w, const int32_t* z, int64_t E, int64_t N, int64_t K,
                    int64_t gs, bool e2m1, uint8_t* out, hipStream_t stream);
 int launch_silu_and_mul(const void* in, int64_t rows, int64_t inter, void* out,
@@ -57,7 +57,7 @@ size_t align_workspace_bytes(int64_t numel, int64_t num_experts);
 int launch_align(const int32_t* topk_ids, int64_t numel, int64_t E, int64_t block_m,
                  const int32_t* expert_map, int32_t* sorted_ids, int64_t sorted_len,
                  int32_t* expert_ids, int32_t* ntp, void* ws, size_t ws_bytes,
-                 hipStream_t stream);
+                 hipStream_t stream, int32_t* slot_to_row = nullptr);   // optional inverse map
 int launch_gather_reduce(const void* out2, int64_t P, int64_t N, const int32_t* sorted_ids,
                          const float* tw, int64_t m_tk, const int32_t* ntp, int64_t top_k,
                          float* out, int32_t* slot_to_row, hipStream_t stream);
@@ -67,6 +67,10 @@ int launch_slot_reduce(const float* y, const float* tw, const int32_t* topk_ids,
                        const int32_t* expert_map, int64_t E, int64_t T, int64_t N,
                        int64_t top_k, void* out, bool out_bf16, hipStream_t stream);
 int launch_cast_f32(const float* in, int64_t n, void* out, bool out_bf16, hipStream_t stream);
+// out[t, n] = cast(sum_{j asc} w[t*k+j] * f32(y[slot_to_row[t*k+j], n])), y fp16 (rows, N);
+// rows < 0 (slots dropped by expert_map) contribute nothing. N % 8 == 0.
+int launch_row_reduce(const void* y, const int32_t* slot_to_row, const float* tw, int64_t T,
+                      int64_t N, int64_t top_k, void* out, bool out_bf16, hipStream_t stream);
 int launch_zero_f32(float* p, int64_t n, hipStream_t stream);
 
 // Grouped GEMM epilogue modes.
@@ -102,11 +106,15 @@ struct GroupedArgs {
     // scratch for the prequantised path
     uint8_t* x_fp8;         // (x_rows, K) k8-interleaved, or null
     float* act_scales;      // (x_rows,)
+    float* act_group_sums;  // (x_rows, K/128) per-group sums of the e4m3 values, or null
 };
 
 int launch_grouped_scalar(const GroupedArgs& a, hipStream_t stream);
 int launch_grouped_mfma(const GroupedArgs& a, hipStream_t stream);   // prefill tiles
 int launch_grouped_gemv(const GroupedArgs& a, hipStream_t stream);   // decode GEMV
+// Prefill tiles with raw-nibble B in registers; needs x_fp8, act_scales and act_group_sums.
+int launch_grouped_prefill(const GroupedArgs& a, hipStream_t stream);
+bool prefill_supported(int64_t K, int64_t group_size, bool e2m1);   // g128, K <= 4096, no E2M1
 // Same, with an explicit column-tile count per wave team (0 = default heuristic).
 int launch_grouped_gemv_tpt(const GroupedArgs& a, int tiles_per_team, hipStream_t stream);
 bool mfma_supported(int64_t K, int64_t group_size);
