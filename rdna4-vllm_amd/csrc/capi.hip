@@ -104,6 +104,7 @@ int check_launch(const char* what) {
 // ---------------------------------------------------------------------------------------
 namespace w4a8 {
 namespace {
+constexpr int64_t kAlignSmallMax = 1024;  // numel handled by the one-work-group align
 constexpr int64_t kGemvMaxM = 96;   // moe_experts.py:563 GEMV_MAX_M
 constexpr int64_t kDecodeBlockM = 16;
 constexpr int64_t kPrefillBlockM = 64;    // 64-row tiles; empty 16-row fragments are skipped
@@ -445,18 +446,26 @@ int w4a8_moe_apply(const void* x, int x_dtype, int64_t T, int64_t H, int64_t int
     const bool bf16 = x_dtype == W4A8_DTYPE_BF16;
     const bool e2m1 = weight_is_e2m1 != 0;
     const int64_t numel = T * top_k;
-    stage_mark(0, s);
-    if (int rc = launch_align(topk_ids, numel, E, pl.block_m, expert_map, sti, pl.P, eid, ntp,
-                              aws, abytes, s, s2r))
-        return rc;
-    stage_mark(1, s);
     const bool mfma = mfma_supported(H, group_size) && mfma_supported(inter, group_size);
     // prefill tiles need the per-group sums of the quantised rows (zero-point term)
     const bool pf1 = !pl.decode && mfma && prefill_supported(H, group_size, e2m1);
     const bool pf2 = !pl.decode && mfma && prefill_supported(inter, group_size, e2m1);
-    if (int rc = launch_act_quant(x, bf16, T, H, xq, s1, true, s, nullptr, nullptr, 0,
-                                  pf1 ? gs1 : nullptr))
-        return rc;
+    stage_mark(0, s);
+    if (pl.decode && numel <= kAlignSmallMax) {
+        // one launch: align in work-group 0, act-quant of x in the others
+        if (int rc = launch_align_quant(topk_ids, numel, E, pl.block_m, expert_map, sti, pl.P,
+                                        eid, ntp, s2r, x, bf16, T, H, xq, s1, nullptr, s))
+            return rc;
+        stage_mark(1, s);
+    } else {
+        if (int rc = launch_align(topk_ids, numel, E, pl.block_m, expert_map, sti, pl.P, eid,
+                                  ntp, aws, abytes, s, s2r))
+            return rc;
+        stage_mark(1, s);
+        if (int rc = launch_act_quant(x, bf16, T, H, xq, s1, true, s, nullptr, nullptr, 0,
+                                      pf1 ? gs1 : nullptr))
+            return rc;
+    }
     stage_mark(2, s);
     stage_mark(3, s);
 

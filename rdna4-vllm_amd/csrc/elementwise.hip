@@ -1,28 +1,16 @@
 // Activation quantisation, int4 dequant, SiLU*mul, reductions and casts (gfx950).
 #include "w4a8_common.h"
 #include "w4a8_internal.h"
+#include "act_quant.h"
 
 namespace w4a8 {
 namespace {
 
 constexpr int kWavesPerBlock = 4;
 
-template <bool BF16>
-__device__ __forceinline__ float load_act(const void* x, int64_t i) {
-    if constexpr (BF16) {
-        // Reference casts bf16 activations to fp16 first (moe_experts.py:596).
-        const float f = __bfloat162float(reinterpret_cast<const __hip_bfloat16*>(x)[i]);
-        return __half2float(__float2half(f));
-    } else {
-        return __half2float(reinterpret_cast<const __half*>(x)[i]);
-    }
-}
-
-// One wave per row: absmax, scale, quantise (moe_kernel.hip:87-127).
+// One wave per row (moe_kernel.hip:87-127).
 // Optional row filter (sorted_ids/ntp/num_valid): rows that are padding in the
 // moe_align layout are skipped, so uninitialised padding rows are never read.
-// Optional gsum (rows, K/128): the sum of the e4m3 values of each 128-wide group, which
-// the prefill GEMM uses for its zero-point term (needs K % 128 == 0).
 template <bool BF16>
 __global__ void __launch_bounds__(256) act_quant_kernel(
     const void* __restrict__ x, int64_t rows, int K, uint8_t* __restrict__ q,
@@ -32,45 +20,7 @@ __global__ void __launch_bounds__(256) act_quant_kernel(
     const int64_t row = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
     if (row >= rows) return;
     if (sorted_ids != nullptr && (row >= ntp[0] || sorted_ids[row] >= num_valid)) return;
-    const int64_t base = row * K;
-    float amax = 0.0f;
-    for (int k = lane * 8; k < K; k += 64 * 8) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(load_act<BF16>(x, base + k + j)));
-    }
-    amax = wave_max(amax);
-    const float s = act_scale_from_absmax(amax);
-    if (lane == 0) scales[row] = s;
-    const float inv = 1.0f / s;
-    // every lane runs every 512-wide pass (inactive lanes add zero) so the group-sum
-    // shuffles always see a full wave
-    for (int k0 = 0; k0 < K; k0 += 64 * 8) {
-        const int k = k0 + lane * 8;
-        uint32_t lo = 0, hi = 0;
-        if (k < K) {
-            float v[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) v[j] = load_act<BF16>(x, base + k + j) * inv;
-            if (k8) {
-                lo = pack4_e4m3(v[0], v[2], v[4], v[6]);
-                hi = pack4_e4m3(v[1], v[3], v[5], v[7]);
-            } else {
-                lo = pack4_e4m3(v[0], v[1], v[2], v[3]);
-                hi = pack4_e4m3(v[4], v[5], v[6], v[7]);
-            }
-            *reinterpret_cast<uint2*>(q + base + k) = make_uint2(lo, hi);
-        }
-        if (gsum != nullptr) {
-            // lanes 16j..16j+15 hold group k/128 of this pass: fixed-order tree sum
-            float t = 0.f;
-#pragma unroll
-            for (int b = 0; b < 4; ++b)
-                t += e4m3_to_f32((lo >> (8 * b)) & 0xFF) + e4m3_to_f32((hi >> (8 * b)) & 0xFF);
-#pragma unroll
-            for (int o = 1; o < 16; o <<= 1) t += __shfl_xor(t, o, 64);
-            if ((lane & 15) == 0 && k < K) gsum[row * (K / 128) + k / 128] = t;
-        }
-    }
+    quantize_row<BF16>(x, row, K, q, scales, k8, gsum, lane);
 }
 
 // One thread per (row, 8-wide k chunk): decode 8 nibbles through the same table path the
@@ -145,6 +95,7 @@ __global__ void slot_reduce_kernel(const float* __restrict__ y, const float* __r
     const int n = (blockIdx.x * blockDim.x + threadIdx.x) * 4;
     if (n >= N || t >= T) return;
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
     for (int j = 0; j < top_k; ++j) {
         int e = ids[t * top_k + j];
         if (emap != nullptr) e = (e >= 0 && e < E) ? emap[e] : -1;

@@ -13,6 +13,7 @@
 // into expert offsets. Small inputs (one chunk) run all three phases in one launch.
 #include "w4a8_common.h"
 #include "w4a8_internal.h"
+#include "act_quant.h"
 
 namespace w4a8 {
 namespace {
@@ -118,7 +119,8 @@ __device__ void write_layout(const int* cnt, const int* eoff, int E, int64_t blo
 }
 
 // Single launch for numel <= kChunk.
-__global__ void __launch_bounds__(kAlignThreads) align_small_kernel(
+// Whole align for numel <= kChunk inside one work-group of kAlignThreads threads.
+__device__ __forceinline__ void align_small_body(
     const int32_t* __restrict__ ids, int64_t numel, int E, int64_t block_m,
     const int32_t* __restrict__ emap, int32_t* __restrict__ sorted_ids, int64_t sorted_len,
     int32_t* __restrict__ expert_ids, int32_t* __restrict__ ntp,
@@ -137,6 +139,15 @@ __global__ void __launch_bounds__(kAlignThreads) align_small_kernel(
     if (slot_to_row != nullptr && tid < numel) slot_to_row[tid] = e >= 0 ? eoff[e] + rank : -1;
     write_layout(s.hist, eoff, E, block_m, numel, total, sorted_ids, sorted_len, expert_ids,
                  ntp);
+}
+
+__global__ void __launch_bounds__(kAlignThreads) align_small_kernel(
+    const int32_t* __restrict__ ids, int64_t numel, int E, int64_t block_m,
+    const int32_t* __restrict__ emap, int32_t* __restrict__ sorted_ids, int64_t sorted_len,
+    int32_t* __restrict__ expert_ids, int32_t* __restrict__ ntp,
+    int32_t* __restrict__ slot_to_row) {
+    align_small_body(ids, numel, E, block_m, emap, sorted_ids, sorted_len, expert_ids, ntp,
+                     slot_to_row);
 }
 
 // Multi-chunk phase 1: per-chunk histograms -> counts[chunk][E].
@@ -200,6 +211,9 @@ __global__ void __launch_bounds__(kAlignThreads) align_place_kernel(
 // ---- router: one wave per token ----
 constexpr int kRouterMaxPerLane = 16;   // E <= 1024
 
+// NV = logits per lane (E <= 64 * NV). Loads are unconditional (clamped index, the
+// out-of-range entries masked to -inf afterwards) so they issue together.
+template <int NV>
 __global__ void __launch_bounds__(256) topk_softmax_kernel(
     const float* __restrict__ logits, int64_t T, int E, int top_k, bool renorm,
     float* __restrict__ tw, int32_t* __restrict__ tids) {
@@ -207,21 +221,19 @@ __global__ void __launch_bounds__(256) topk_softmax_kernel(
     const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (t >= T) return;
     const float* l = logits + t * E;
-    float v[kRouterMaxPerLane];
+    float v[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) v[i] = l[min(lane + 64 * i, E - 1)];
     float m = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < kRouterMaxPerLane; ++i) {
-        const int e = lane + 64 * i;
-        v[i] = (e < E) ? l[e] : -INFINITY;
+    for (int i = 0; i < NV; ++i) {
+        if (lane + 64 * i >= E) v[i] = -INFINITY;
         m = fmaxf(m, v[i]);
     }
     m = wave_max(m);
     float ssum = 0.f;
 #pragma unroll
-    for (int i = 0; i < kRouterMaxPerLane; ++i) {
-        const int e = lane + 64 * i;
-        if (e < E) ssum += expf(v[i] - m);
-    }
+    for (int i = 0; i < NV; ++i) ssum += lane + 64 * i < E ? expf(v[i] - m) : 0.f;
     ssum = wave_sum(ssum);
     uint32_t taken = 0;   // bit i: v[i] already selected
     float wsel = 0.f;     // this lane's output weight (lane j < top_k holds pick j)
@@ -232,7 +244,7 @@ __global__ void __launch_bounds__(256) topk_softmax_kernel(
         float bv = -INFINITY;
         int be = 0x7FFFFFFF;
 #pragma unroll
-        for (int i = 0; i < kRouterMaxPerLane; ++i) {
+        for (int i = 0; i < NV; ++i) {
             const int e = lane + 64 * i;
             if (e < E && !(taken & (1u << i)) && (v[i] > bv || (v[i] == bv && e < be))) {
                 bv = v[i];
@@ -254,6 +266,24 @@ __global__ void __launch_bounds__(256) topk_softmax_kernel(
         tw[t * top_k + lane] = renorm ? wsel / sum_sel : wsel;
         tids[t * top_k + lane] = isel;
     }
+}
+
+// Decode prologue in one launch: work-group 0 builds the align layout (numel <= kChunk),
+// work-groups 1.. quantise 16 activation rows each (one wave per row).
+template <bool BF16>
+__global__ void __launch_bounds__(kAlignThreads) align_quant_kernel(
+    const int32_t* __restrict__ ids, int64_t numel, int E, int64_t block_m,
+    const int32_t* __restrict__ emap, int32_t* __restrict__ sorted_ids, int64_t sorted_len,
+    int32_t* __restrict__ expert_ids, int32_t* __restrict__ ntp,
+    int32_t* __restrict__ slot_to_row, const void* __restrict__ x, int64_t rows, int K,
+    uint8_t* __restrict__ xq, float* __restrict__ xs, float* __restrict__ gsum) {
+    if (blockIdx.x > 0) {
+        const int64_t row = (int64_t)(blockIdx.x - 1) * (kAlignThreads / 64) + (threadIdx.x >> 6);
+        if (row < rows) quantize_row<BF16>(x, row, K, xq, xs, true, gsum, threadIdx.x & 63);
+        return;
+    }
+    align_small_body(ids, numel, E, block_m, emap, sorted_ids, sorted_len, expert_ids, ntp,
+                     slot_to_row);
 }
 
 }  // namespace
@@ -309,9 +339,34 @@ int launch_topk_softmax(const float* logits, int64_t T, int64_t E, int64_t top_k
         return W4A8_ERR_INVALID;
     }
     if (T == 0) return W4A8_OK;
-    topk_softmax_kernel<<<(unsigned)((T + 3) / 4), 256, 0, stream>>>(logits, T, (int)E,
-                                                                    (int)top_k, renorm, w, ids);
+    const dim3 grid((unsigned)((T + 3) / 4));
+    if (E <= 64) topk_softmax_kernel<1><<<grid, 256, 0, stream>>>(logits, T, (int)E, (int)top_k, renorm, w, ids);
+    else if (E <= 128) topk_softmax_kernel<2><<<grid, 256, 0, stream>>>(logits, T, (int)E, (int)top_k, renorm, w, ids);
+    else if (E <= 256) topk_softmax_kernel<4><<<grid, 256, 0, stream>>>(logits, T, (int)E, (int)top_k, renorm, w, ids);
+    else if (E <= 512) topk_softmax_kernel<8><<<grid, 256, 0, stream>>>(logits, T, (int)E, (int)top_k, renorm, w, ids);
+    else topk_softmax_kernel<16><<<grid, 256, 0, stream>>>(logits, T, (int)E, (int)top_k, renorm, w, ids);
     return check_launch("topk_softmax_kernel");
+}
+
+int launch_align_quant(const int32_t* ids, int64_t numel, int64_t E, int64_t block_m,
+                       const int32_t* emap, int32_t* sorted_ids, int64_t sorted_len,
+                       int32_t* expert_ids, int32_t* ntp, int32_t* slot_to_row,
+                       const void* x, bool x_bf16, int64_t rows, int64_t K, uint8_t* xq,
+                       float* xs, float* gsum, hipStream_t stream) {
+    if (E > kMaxExperts || numel > kChunk) {
+        set_error("align_quant: needs num_experts <= 1024 and numel <= 1024");
+        return W4A8_ERR_INVALID;
+    }
+    const unsigned grid = 1u + (unsigned)((rows + kAlignThreads / 64 - 1) / (kAlignThreads / 64));
+    if (x_bf16)
+        align_quant_kernel<true><<<grid, kAlignThreads, 0, stream>>>(
+            ids, numel, (int)E, block_m, emap, sorted_ids, sorted_len, expert_ids, ntp,
+            slot_to_row, x, rows, (int)K, xq, xs, gsum);
+    else
+        align_quant_kernel<false><<<grid, kAlignThreads, 0, stream>>>(
+            ids, numel, (int)E, block_m, emap, sorted_ids, sorted_len, expert_ids, ntp,
+            slot_to_row, x, rows, (int)K, xq, xs, gsum);
+    return check_launch("align_quant_kernel");
 }
 
 }  // namespace w4a8
