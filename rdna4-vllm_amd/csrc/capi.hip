@@ -54,17 +54,28 @@ int run_grouped(GroupedArgs& a, int64_t kernel, void* ws, size_t ws_bytes, hipSt
     const bool mfma = mfma_supported(a.K, a.group_size);
     // E2M1 codebook weights take the matrix-core tiles (the GEMV feeds raw nibbles)
     const bool gemv = gemv_supported(a.K, a.group_size) && !a.e2m1;
-    if (kernel == W4A8_MOE_KERNEL_GEMV && gemv) {
-        // decode GEMV quantises its block's rows itself (bit-identical to act_quant)
-        a.x_fp8 = nullptr;
-        a.act_scales = nullptr;
-        return launch_grouped_gemv(a, s);
-    }
     Workspace w(ws, ws_bytes);
     a.x_fp8 = w.take<uint8_t>((size_t)(a.x_rows * a.K));
     a.act_scales = w.take<float>((size_t)a.x_rows);
     float* gsum = w.take<float>((size_t)(a.x_rows * ((a.K + 127) / 128)));
-    if ((a.x_rows > 0 && ws == nullptr) || !w.ok()) {
+    const bool have_ws = !(a.x_rows > 0 && ws == nullptr) && w.ok();
+    // identity-gathered inputs (gemm2 / scatter) have one row per padded row: skip padding.
+    const bool filter = a.identity_gather && a.sorted_ids != nullptr;
+    if (kernel == W4A8_MOE_KERNEL_GEMV && gemv) {
+        if (!have_ws) {
+            // no workspace: the GEMV quantises its block's rows itself (bit-identical to
+            // act_quant, but repeated by every work-group that reads a row)
+            a.x_fp8 = nullptr;
+            a.act_scales = nullptr;
+            return launch_grouped_gemv(a, s);
+        }
+        if (int rc = launch_act_quant(a.x, a.x_bf16, a.x_rows, a.K, a.x_fp8, a.act_scales, true,
+                                      s, filter ? a.sorted_ids : nullptr,
+                                      filter ? a.ntp : nullptr, a.num_valid, nullptr))
+            return rc;
+        return launch_grouped_gemv(a, s);
+    }
+    if (!have_ws) {
         set_error("workspace smaller than w4a8_moe_gemm_workspace_size()");
         return W4A8_ERR_WORKSPACE;
     }
@@ -72,8 +83,6 @@ int run_grouped(GroupedArgs& a, int64_t kernel, void* ws, size_t ws_bytes, hipSt
     const bool tiles = (kernel == W4A8_MOE_KERNEL_WMMA || kernel == W4A8_MOE_KERNEL_GEMV) && mfma;
     const bool prefill = tiles && prefill_supported(a.K, a.group_size, a.e2m1);
     a.act_group_sums = prefill ? gsum : nullptr;
-    // identity-gathered inputs (gemm2 / scatter) have one row per padded row: skip padding.
-    const bool filter = a.identity_gather && a.sorted_ids != nullptr;
     if (int rc = launch_act_quant(a.x, a.x_bf16, a.x_rows, a.K, a.x_fp8, a.act_scales, true, s,
                                   filter ? a.sorted_ids : nullptr, filter ? a.ntp : nullptr,
                                   a.num_valid, a.act_group_sums))
@@ -484,12 +493,12 @@ int w4a8_moe_apply(const void* x, int x_dtype, int64_t T, int64_t H, int64_t int
     else rc = launch_grouped_mfma(g1, s);
     if (rc) return rc;
     stage_mark(4, s);
-    // act-quant of h over real rows only (the decode GEMV quantises its rows itself)
-    const bool fuse_aq2 = pl.decode && !e2m1 && gemv_supported(inter, group_size);
-    if (!fuse_aq2)
-        if ((rc = launch_act_quant(h, false, pl.P, inter, hq, s2, true, s, sti, ntp, numel,
-                                   pf2 ? gs2 : nullptr)))
-            return rc;
+    // act-quant of h over real rows only, once per row (quantising inside the decode GEMV
+    // would repeat it for every work-group that reads the row)
+    const bool gemv2 = pl.decode && !e2m1 && gemv_supported(inter, group_size);
+    if ((rc = launch_act_quant(h, false, pl.P, inter, hq, s2, true, s, sti, ntp, numel,
+                               pf2 ? gs2 : nullptr)))
+        return rc;
     stage_mark(5, s);
     // gemm2 (identity gather) -> per-slot rows (decode) or scatter (prefill)
     GroupedArgs g2{};
@@ -500,11 +509,11 @@ int w4a8_moe_apply(const void* x, int x_dtype, int64_t T, int64_t H, int64_t int
     g2.epi = pl.decode ? Epi::kSlotF32 : Epi::kHalf; g2.out = pl.decode ? (void*)acc : (void*)y;
     g2.topk_weights = topk_weights; g2.out_top_k = top_k;
     g2.x = h; g2.x_bf16 = false;
-    g2.x_fp8 = fuse_aq2 ? nullptr : hq;
-    g2.act_scales = fuse_aq2 ? nullptr : s2;
+    g2.x_fp8 = hq;
+    g2.act_scales = s2;
     g2.act_group_sums = pf2 ? gs2 : nullptr;
     if (!mfma) rc = launch_grouped_scalar(g2, s);
-    else if (fuse_aq2) rc = launch_grouped_gemv(g2, s);
+    else if (gemv2) rc = launch_grouped_gemv(g2, s);
     else if (pf2) rc = launch_grouped_prefill(g2, s);
     else rc = launch_grouped_mfma(g2, s);
     if (rc) return rc;

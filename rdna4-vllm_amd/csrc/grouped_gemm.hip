@@ -400,64 +400,53 @@ __device__ __forceinline__ float half_bits_to_f32(uint32_t bits) {
     }
 }
 
-// 32 consecutive fp16/bf16 values of a row -> absmax, or -> 32 e4m3 bytes (k8-interleaved).
-template <bool BF16>
-__device__ __forceinline__ float absmax32(const uint16_t* src) {
-    float m = 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint4 v = reinterpret_cast<const uint4*>(src)[i];
-        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            m = fmaxf(m, fabsf(half_bits_to_f32<BF16>(w[j] & 0xFFFFu)));
-            m = fmaxf(m, fabsf(half_bits_to_f32<BF16>(w[j] >> 16)));
-        }
-    }
-    return m;
-}
-template <bool BF16>
-__device__ __forceinline__ v8i quant32(const uint16_t* src, float inv) {
-    v8i r;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {   // 8 values per 16-byte load: k = 8i .. 8i+7
-        const uint4 v = reinterpret_cast<const uint4*>(src)[i];
-        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-        float f[8];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            f[2 * j] = half_bits_to_f32<BF16>(w[j] & 0xFFFFu) * inv;
-            f[2 * j + 1] = half_bits_to_f32<BF16>(w[j] >> 16) * inv;
-        }
-        r[2 * i] = (int)pack4_e4m3(f[0], f[2], f[4], f[6]);
-        r[2 * i + 1] = (int)pack4_e4m3(f[1], f[3], f[5], f[7]);
-    }
-    return r;
+// fp16 or bf16 bits -> f32 with the input dtype chosen at run time (no divergent callees,
+// so the raw row words stay in registers)
+__device__ __forceinline__ float act_bits_to_f32(uint32_t bits, bool bf16) {
+    return bf16 ? half_bits_to_f32<true>(bits) : half_bits_to_f32<false>(bits);
 }
 
-template <Epi EPI, int GPW, int KSPLIT>
+// Decode GEMV. One work-group per (block of block_m sorted rows, range of column tiles).
+// Loads are issued in dependency levels so that no wait drains the weight stream: (1) list
+// length, expert id and the block's sorted ids; (2) this pass's activation rows; (3) the
+// first two weight chunks. Waiting for (2) then leaves (3) in flight, and the chunk loop
+// keeps two chunks in flight after that. Row compaction (real rows first) is computed by
+// every wave from a ballot, so the prologue has no work-group barrier.
+// AQ: x is fp16/bf16 and each pass quantises its rows in registers, bit-identical to
+// act_quant_kernel (the row absmax is combined across the KSPLIT waves through LDS).
+template <Epi EPI, int GPW, int KSPLIT, bool AQ>
 __global__ void __launch_bounds__(256, 2) grouped_gemv_kernel(Params p, int tpt) {
     using C = GemvCfg<EPI, GPW, KSPLIT>;
     extern __shared__ __attribute__((aligned(16))) uint8_t s_dyn[];   // KSPLIT > 1 partials
-    __shared__ int s_src[kGemvMaxRows];
-    __shared__ int s_slot[kGemvMaxRows];
-    __shared__ int s_pad[kGemvMaxRows];
     __shared__ float s_amax[4][16];
-    __shared__ float s_asc[16];
-    __shared__ int s_mreal;
+    __shared__ int s_opad[4][16];
+    __shared__ int s_oslot[4][16];
+    __shared__ float s_oasc[4][16];
     v4f* s_part = reinterpret_cast<v4f*>(s_dyn);   // [wave][tile][NF][lane]
-
-    const int64_t row0 = (int64_t)blockIdx.y * p.block_m;
-    const int ntp = p.ntp ? p.ntp[0] : (int)p.P;
-    if (row0 >= ntp || row0 >= p.P) return;
-    const int e = p.expert_ids ? p.expert_ids[blockIdx.y] : 0;
-    if (e < 0 || e >= p.E) return;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int q = lane >> 4;           // k quarter of a group / D row quad of this lane
     const int c16 = lane & 15;         // B column / A row of this lane
+    const int64_t row0 = (int64_t)blockIdx.y * p.block_m;
+
+    // ---- level 1: independent metadata loads ----
+    const int ntp = p.ntp ? p.ntp[0] : (int)p.P;
+    const int e = p.expert_ids ? p.expert_ids[blockIdx.y] : 0;
+    const int64_t myrow = row0 + lane;   // lane l resolves padded row row0 + l (block_m <= 64)
+    const bool in_blk = lane < p.block_m && myrow < p.P;
+    const int sid = in_blk ? (p.sorted_ids ? p.sorted_ids[myrow] : (int)myrow) : -1;
+    if (row0 >= ntp || row0 >= p.P) return;
+    if (e < 0 || e >= p.E) return;
+    int slot = -1, src = -1;
+    if (in_blk && myrow < ntp && sid >= 0 && sid < p.num_valid) {
+        slot = sid;
+        src = p.identity ? (int)myrow : sid / p.top_k;
+    }
+    const uint64_t vmask = __ballot(src >= 0);
+    const int mreal = __popcll(vmask);
+
     const int team = wave / KSPLIT;
     const int g0 = (wave % KSPLIT) * GPW;
     const int ncols = C::kSilu ? p.N / 2 : p.N;
@@ -501,35 +490,17 @@ __global__ void __launch_bounds__(256, 2) grouped_gemv_kernel(Params p, int tpt)
     };
     using B0 = std::integral_constant<int, 0>;
     using B1 = std::integral_constant<int, 1>;
-    // the first two chunks are in flight across the prologue
-    if (nch > 0) issue(0, B0{});
-    if (nch > 1) issue(1, B1{});
-
-    if (wave == 0) {
-        int slot = -1, src = -1;
-        if (lane < p.block_m) src = resolve_row(p, row0 + lane, ntp, slot);
-        const bool v = src >= 0;
-        const uint64_t mask = __ballot(v);
-        const int pos = __popcll(mask & ((1ull << lane) - 1ull));
-        if (v) { s_src[pos] = src; s_slot[pos] = slot; s_pad[pos] = (int)(row0 + lane); }
-        if (lane == 0) s_mreal = __popcll(mask);
-    }
-    __syncthreads();
-    const int mreal = s_mreal;
 
     for (int m0 = 0; m0 < mreal; m0 += 16) {
-        if (m0 > 0) {
-            __syncthreads();                 // LDS partials of the previous pass consumed
-            if (nch > 0) issue(0, B0{});
-            if (nch > 1) issue(1, B1{});
-        }
-        // ---- activation fragments of rows m0 + c16 for this wave's groups ----
-        const int mrow = m0 + c16;
-        const int src = s_src[mrow < mreal ? mrow : m0];   // pad rows repeat a real row
+        if (m0 > 0) __syncthreads();   // LDS partials / row maxima of the previous pass consumed
+        // A row m0 + c16 of this pass (pad rows repeat the last real row)
+        const int asrc = __shfl(src, nth_set_bit(vmask, min(m0 + c16, mreal - 1)), 64);
+
+        // ---- level 2: activation rows ----
         v8i af[GPW];
         float my_asc;
-        if (p.xq) {
-            const uint8_t* xr = p.xq + (int64_t)src * p.K + q * 32;
+        if constexpr (!AQ) {
+            const uint8_t* xr = p.xq + (int64_t)asrc * p.K + q * 32;
 #pragma unroll
             for (int u = 0; u < GPW; ++u) {
                 const uint4 lo = *reinterpret_cast<const uint4*>(xr + (g0 + u) * kGroup);
@@ -537,20 +508,46 @@ __global__ void __launch_bounds__(256, 2) grouped_gemv_kernel(Params p, int tpt)
                 af[u] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w,
                             (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
             }
-            my_asc = p.asc[src];
+            my_asc = p.asc[asrc];
+            // ---- level 3: the first two weight chunks ----
+            if (nch > 0) issue(0, B0{});
+            if (nch > 1) issue(1, B1{});
         } else {
-            // per-row quantisation in place, bit-identical to act_quant_kernel
-            const uint16_t* xr = reinterpret_cast<const uint16_t*>(p.xh) + (int64_t)src * p.K + q * 32;
-            float amax = 0.f;
+            // the first weight chunks go out with the raw rows; the wait for the rows then
+            // also covers those chunks, which were issued just before them
+            if (nch > 0) issue(0, B0{});
+            if (nch > 1) issue(1, B1{});
+            const uint16_t* xr = reinterpret_cast<const uint16_t*>(p.xh) + (int64_t)asrc * p.K + q * 32;
+            const bool bf16 = p.xbf16;
+            uint4 raw[GPW][4];   // 32 values of group g0 + u: k = 8i .. 8i+7 in raw[u][i]
 #pragma unroll
             for (int u = 0; u < GPW; ++u)
-                amax = fmaxf(amax, p.xbf16 ? absmax32<true>(xr + (g0 + u) * kGroup)
-                                           : absmax32<false>(xr + (g0 + u) * kGroup));
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    raw[u][i] = reinterpret_cast<const uint4*>(xr + (g0 + u) * kGroup)[i];
+            // absmax on the magnitude bits: both conversions are monotone in them, so the
+            // max converts to the same value as the max of the converted values (NaNs,
+            // which fmaxf skips, count as 0)
+            const uint32_t nan_above = bf16 ? 0x7F80u : 0x7C00u;
+            uint32_t mbits = 0;
+#pragma unroll
+            for (int u = 0; u < GPW; ++u)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t w[4] = {raw[u][i].x, raw[u][i].y, raw[u][i].z, raw[u][i].w};
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const uint32_t lo = w[j] & 0x7FFFu, hi = (w[j] >> 16) & 0x7FFFu;
+                        mbits = max(mbits, lo > nan_above ? 0u : lo);
+                        mbits = max(mbits, hi > nan_above ? 0u : hi);
+                    }
+                }
+            float amax = act_bits_to_f32(mbits, bf16);
             amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
             amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
             if constexpr (KSPLIT > 1) {
                 if (q == 0) s_amax[wave][c16] = amax;
-                __syncthreads();
+                lds_barrier();
 #pragma unroll
                 for (int j = 0; j < KSPLIT; ++j) amax = fmaxf(amax, s_amax[team * KSPLIT + j][c16]);
             }
@@ -558,10 +555,19 @@ __global__ void __launch_bounds__(256, 2) grouped_gemv_kernel(Params p, int tpt)
             const float inv = 1.0f / my_asc;
 #pragma unroll
             for (int u = 0; u < GPW; ++u)
-                af[u] = p.xbf16 ? quant32<true>(xr + (g0 + u) * kGroup, inv)
-                                : quant32<false>(xr + (g0 + u) * kGroup, inv);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {   // k8-interleaved bytes, as act_quant_kernel
+                    const uint32_t w[4] = {raw[u][i].x, raw[u][i].y, raw[u][i].z, raw[u][i].w};
+                    float f[8];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        f[2 * j] = act_bits_to_f32(w[j] & 0xFFFFu, bf16) * inv;
+                        f[2 * j + 1] = act_bits_to_f32(w[j] >> 16, bf16) * inv;
+                    }
+                    af[u][2 * i] = (int)pack4_e4m3(f[0], f[2], f[4], f[6]);
+                    af[u][2 * i + 1] = (int)pack4_e4m3(f[1], f[3], f[5], f[7]);
+                }
         }
-        if (wave == 0 && q == 0) s_asc[c16] = my_asc * wscale;
         v4f sa[GPW];   // 2^-9 * group sums of rows 4q..4q+3
 #pragma unroll
         for (int u = 0; u < GPW; ++u) {
@@ -571,23 +577,34 @@ __global__ void __launch_bounds__(256, 2) grouped_gemv_kernel(Params p, int tpt)
 #pragma unroll
             for (int r = 0; r < 4; ++r) sa[u][r] *= 1.0f / kNibbleScale;
         }
-        float asc4[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) asc4[r] = __shfl(my_asc, 4 * q + r, 64) * wscale;
 
-        auto store = [&](int m, int col, float ra, float rb, float a) {
-            const int64_t row_pad = s_pad[m];
-            const int slot = s_slot[m];
+        // per-wave table of this pass's 16 output rows (padded row, slot, scale), read back
+        // at store time instead of being held in registers across the chunk loop
+        if (q == 0) {
+            const int j = nth_set_bit(vmask, min(m0 + c16, mreal - 1));
+            s_opad[wave][c16] = (int)(row0 + j);
+            s_oasc[wave][c16] = my_asc * wscale;
+        }
+        {
+            const int j = nth_set_bit(vmask, min(m0 + c16, mreal - 1));
+            const int sl = __shfl(slot, j, 64);   // all lanes active here
+            if (q == 0) s_oslot[wave][c16] = sl;
+        }
+        auto store = [&](int r, int col, float ra, float rb) {
+            const int mi = 4 * q + r;
+            const int64_t opad = s_opad[wave][mi];
+            const int oslot = s_oslot[wave][mi];
+            const float a = s_oasc[wave][mi];
             if constexpr (EPI == Epi::kHalf) {
-                reinterpret_cast<__half*>(p.out)[row_pad * p.N + col] = __float2half(ra * a);
+                reinterpret_cast<__half*>(p.out)[opad * p.N + col] = __float2half(ra * a);
             } else if constexpr (EPI == Epi::kSiluHalf) {
-                reinterpret_cast<__half*>(p.out)[row_pad * ncols + col] =
+                reinterpret_cast<__half*>(p.out)[opad * ncols + col] =
                     silu_mul_h(__float2half(ra * a), __float2half(rb * a));
             } else if constexpr (EPI == Epi::kScatter) {
-                atomicAdd(reinterpret_cast<float*>(p.out) + (int64_t)(slot / p.out_top_k) * p.N + col,
-                          p.tw[slot] * ra * a);
+                atomicAdd(reinterpret_cast<float*>(p.out) + (int64_t)(oslot / p.out_top_k) * p.N + col,
+                          p.tw[oslot] * ra * a);
             } else {
-                reinterpret_cast<float*>(p.out)[(int64_t)slot * p.N + col] = ra * a;
+                reinterpret_cast<float*>(p.out)[(int64_t)oslot * p.N + col] = ra * a;
             }
         };
 
@@ -631,9 +648,8 @@ __global__ void __launch_bounds__(256, 2) grouped_gemv_kernel(Params p, int tpt)
                     if (col < ncols) {
 #pragma unroll
                         for (int r = 0; r < 4; ++r) {
-                            const int m = m0 + 4 * q + r;
-                            if (m >= mreal) continue;
-                            store(m, col, run[ct][r], C::kSilu ? run[C::CT + ct][r] : 0.f, asc4[r]);
+                            if (m0 + 4 * q + r >= mreal) continue;
+                            store(r, col, run[ct][r], C::kSilu ? run[C::CT + ct][r] : 0.f);
                         }
                     }
                 }
@@ -653,31 +669,30 @@ __global__ void __launch_bounds__(256, 2) grouped_gemv_kernel(Params p, int tpt)
 
         if constexpr (KSPLIT > 1) {
             __syncthreads();
-            // sum the KSPLIT partials of every (team, tile, lane) in wave order, then store
+            // sum the KSPLIT partials of every (team, tile, lane) in wave order, then store;
+            // i & 63 == lane, so the rows and scales are this lane's own
             const int items = C::TEAMS * tpt * 64;
             for (int i = tid; i < items; i += 256) {
                 const int tm = i / (tpt * 64);
                 const int tl = (i >> 6) % tpt;
-                const int l = i & 63;
                 const int tt = (blockIdx.x * C::TEAMS + tm) * tpt + tl;
-                const int col = tt * 16 + (l & 15);
+                const int col = tt * 16 + c16;
                 if (tt >= ntiles || col >= ncols) continue;
                 v4f sum[C::NF];
 #pragma unroll
                 for (int nf = 0; nf < C::NF; ++nf) {
-                    sum[nf] = s_part[(((tm * KSPLIT) * tpt + tl) * C::NF + nf) * 64 + l];
+                    sum[nf] = s_part[(((tm * KSPLIT) * tpt + tl) * C::NF + nf) * 64 + lane];
 #pragma unroll
                     for (int j = 1; j < KSPLIT; ++j) {
-                        const v4f v = s_part[(((tm * KSPLIT + j) * tpt + tl) * C::NF + nf) * 64 + l];
+                        const v4f v = s_part[(((tm * KSPLIT + j) * tpt + tl) * C::NF + nf) * 64 + lane];
 #pragma unroll
                         for (int r = 0; r < 4; ++r) sum[nf][r] += v[r];
                     }
                 }
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const int mi = 4 * (l >> 4) + r;
-                    if (m0 + mi >= mreal) continue;
-                    store(m0 + mi, col, sum[0][r], C::kSilu ? sum[C::NF - 1][r] : 0.f, s_asc[mi]);
+                    if (m0 + 4 * q + r >= mreal) continue;
+                    store(r, col, sum[0][r], C::kSilu ? sum[C::NF - 1][r] : 0.f);
                 }
             }
         }
@@ -751,6 +766,23 @@ int gemv_default_tpt(const Params& p, int ntiles, int frag_bytes_per_tile_wave, 
     return tpt;
 }
 
+template <Epi EPI, int GPW, int KSPLIT, bool AQ>
+int launch_gemv_a(const Params& p, int tpt, dim3 grid, size_t lds, hipStream_t s) {
+    using C = GemvCfg<EPI, GPW, KSPLIT>;
+    static bool attr_set = false;
+    if (!attr_set) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&grouped_gemv_kernel<EPI, GPW, KSPLIT, AQ>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize,
+                                4 * kGemvMaxTiles * C::NF * 64 * (int)sizeof(v4f)) != hipSuccess) {
+            set_error("grouped_gemv_kernel: cannot reserve dynamic LDS");
+            return W4A8_ERR_HIP;
+        }
+        attr_set = true;
+    }
+    grouped_gemv_kernel<EPI, GPW, KSPLIT, AQ><<<grid, 256, lds, s>>>(p, tpt);
+    return check_launch("grouped_gemv_kernel");
+}
+
 template <Epi EPI, int GPW, int KSPLIT>
 int launch_gemv_t(const Params& p, int tpt, hipStream_t s) {
     using C = GemvCfg<EPI, GPW, KSPLIT>;
@@ -759,20 +791,10 @@ int launch_gemv_t(const Params& p, int tpt, hipStream_t s) {
     if (tpt <= 0) tpt = gemv_default_tpt(p, ntiles, GPW * C::NF * 1024, C::TEAMS);
     tpt = std::min(tpt, kGemvMaxTiles);
     const size_t lds = KSPLIT > 1 ? (size_t)4 * tpt * C::NF * 64 * sizeof(v4f) : 0;
-    static bool attr_set = false;
-    if (!attr_set) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&grouped_gemv_kernel<EPI, GPW, KSPLIT>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize,
-                                4 * kGemvMaxTiles * C::NF * 64 * (int)sizeof(v4f)) != hipSuccess) {
-            set_error("grouped_gemv_kernel: cannot reserve dynamic LDS");
-            return W4A8_ERR_HIP;
-        }
-        attr_set = true;
-    }
-    dim3 grid((unsigned)((ntiles + C::TEAMS * tpt - 1) / (C::TEAMS * tpt)),
-              (unsigned)((p.P + p.block_m - 1) / p.block_m));
-    grouped_gemv_kernel<EPI, GPW, KSPLIT><<<grid, 256, lds, s>>>(p, tpt);
-    return check_launch("grouped_gemv_kernel");
+    const dim3 grid((unsigned)((ntiles + C::TEAMS * tpt - 1) / (C::TEAMS * tpt)),
+                    (unsigned)((p.P + p.block_m - 1) / p.block_m));
+    if (p.xq) return launch_gemv_a<EPI, GPW, KSPLIT, false>(p, tpt, grid, lds, s);
+    return launch_gemv_a<EPI, GPW, KSPLIT, true>(p, tpt, grid, lds, s);
 }
 
 template <Epi EPI>

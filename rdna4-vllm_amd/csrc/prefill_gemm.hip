@@ -56,15 +56,6 @@ __device__ __forceinline__ bool prefill_item(int nblocks, int ntiles, int& m_blo
     return true;
 }
 
-// Work-group barrier for LDS hand-off only. __syncthreads() also orders global memory, so
-// the compiler waits for every load in flight (vmcnt(0)) before it, which would drain the
-// weight prefetch every group; fencing LDS alone waits for the LDS writes only.
-__device__ __forceinline__ void lds_barrier() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
 template <int A_CHUNKS>
 __device__ __forceinline__ void pf_load_a(uint4 (&reg)[A_CHUNKS], const uint8_t* __restrict__ xq,
                                           const uint32_t (&src)[A_CHUNKS], int gg) {

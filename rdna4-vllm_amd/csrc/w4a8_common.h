@@ -32,6 +32,13 @@ constexpr int kE2m1Table = 16;
 
 using v8i = int __attribute__((ext_vector_type(8)));
 using v4i = int __attribute__((ext_vector_type(4)));
+
+// 16-byte streaming load (slc/nt): weights are read once per launch, so keep them from
+// displacing reused data in the caches.
+__device__ __forceinline__ uint4 load_stream16(const void* p) {
+    const v4i v = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(p));
+    return make_uint4((uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w);
+}
 using v4f = float __attribute__((ext_vector_type(4)));
 using v16f = float __attribute__((ext_vector_type(16)));
 
@@ -105,6 +112,33 @@ __device__ __forceinline__ int table_index(const int* __restrict__ zeros_e, int 
 __device__ __host__ __forceinline__ int k8_pos(int k) {
     const int r = k & 7;
     return (k & ~7) | ((r >> 1) | ((r & 1) << 2));
+}
+
+// Work-group barrier for LDS hand-off only. __syncthreads() also orders global memory, so
+// the compiler waits for every load in flight (vmcnt(0)) before it, which would drain the
+// loads in flight; fencing LDS alone waits for the LDS writes only.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Index of the k-th (0-based) set bit of m; k < popcount(m).
+__device__ __forceinline__ int nth_set_bit(uint64_t m, int k) {
+    int pos = 0;
+#pragma unroll
+    for (int w = 32; w >= 1; w >>= 1) {
+        const uint64_t low = m & ((1ull << w) - 1ull);
+        const int c = __popcll(low);
+        if (k >= c) {
+            k -= c;
+            m >>= w;
+            pos += w;
+        } else {
+            m = low;
+        }
+    }
+    return pos;
 }
 
 // Wave64 reductions.

@@ -175,6 +175,35 @@ def test_moe_gemm_vs_oracle(kernel, asym, case):
     assert maxrel(got, ref[valid]) <= REL_TOL
 
 
+@pytest.mark.parametrize("case", [(32, 8, 512, 2048, 8, 16, 128), (24, 16, 256, 512, 4, 16, 128),
+                                  (9, 8, 384, 1024, 2, 32, 128), (40, 8, 256, 1536, 2, 64, 128)])
+def test_gemv_in_kernel_quant_matches_prequant(case):
+    """With no workspace the decode GEMV quantises its rows in registers; that path must give
+    the bytes act_quant gives, so both calls agree bit for bit."""
+    from w4a8_fp8_wmma._lib import lib as L
+    from w4a8_fp8_wmma._ops import _ptr, _stream, _workspace
+    T, E, N, K, k, bm, g = case
+    x, w, z, sc, ids, _ = make_case(sum(case), T, E, N, K, k, g)
+    sti, eid, ntp = O.moe_align(ids, bm, E)
+    xd, wd, zd, scd, stid, eidd, ntpd = to_dev(x, w, z, sc, sti, eid, ntp)
+    P = sti.size
+    outs = []
+    for with_ws in (True, False):
+        out = torch.full((P, N), float("nan"), dtype=torch.float16, device=DEV)
+        ws = _workspace(L.w4a8_moe_gemm_workspace_size(T, K), xd.device)
+        rc = L.w4a8_mmq_fp8_moe_gemm(
+            _ptr(xd), T, K, _ptr(wd), _ptr(scd), _ptr(zd), E, N, g, _ptr(stid), P, _ptr(eidd),
+            _ptr(ntpd), k, bm, 7, 0, _ptr(out), ws.data_ptr() if with_ws else None,
+            ws.numel() if with_ws else 0, _stream(xd))
+        assert rc == 0, L.w4a8_last_error()
+        outs.append(out)
+    torch.cuda.synchronize()
+    valid = torch.from_numpy((np.arange(P) < ntp[0]) & (sti < T * k)).to(DEV)
+    assert torch.equal(outs[0][valid], outs[1][valid])
+    ref, vmask = O.grouped_gemm_padded(x, w, sc, z, sti, eid, ntp, k, bm)
+    assert maxrel(outs[1].cpu().numpy()[vmask], ref[vmask]) <= REL_TOL
+
+
 @pytest.mark.parametrize("case", [(64, 8, 256, 256, 2, 16, 128), (128, 8, 512, 512, 2, 64, 128),
                                   (256, 4, 1024, 2048, 2, 128, 128), (16, 16, 256, 256, 4, 16, 32)])
 def test_gemm1_silu_fused_bit_exact_to_unfused(case):
