@@ -58,8 +58,7 @@ __device__ __forceinline__ void quantize_row(const void* __restrict__ x, int64_t
 #pragma unroll
             for (int b = 0; b < 4; ++b)
                 t += e4m3_to_f32((lo >> (8 * b)) & 0xFF) + e4m3_to_f32((hi >> (8 * b)) & 0xFF);
-#pragma unroll
-            for (int o = 1; o < 16; o <<= 1) t += __shfl_xor(t, o, 64);
+            t = lane_allreduce<4>(t, SumOp{});
             if ((lane & 15) == 0 && k < K) gsum[row * (K / 128) + k / 128] = t;
         }
     }

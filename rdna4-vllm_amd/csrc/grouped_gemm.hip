@@ -349,6 +349,9 @@ struct GemvCfg {
     static constexpr int NB = GPW / GC;           // chunks per tile set
     static constexpr int TEAMS = 4 / KSPLIT;      // wave teams (independent tile ranges)
     static constexpr bool kPackedScales = GC == 2 || GC == 4;
+    // 4-group chunks (one per tile set): the scales and zero-point words of all chunks are
+    // loaded once per work-group into LDS instead of alongside every chunk
+    static constexpr bool kStagedSZ = GC == 4 && NB == 1;
     static_assert(GPW % GC == 0 && (NB == 1 || NB == 2), "unsupported groups per wave");
     static_assert(KSPLIT == 1 || KSPLIT == 2 || KSPLIT == 4, "KSPLIT divides the 4 waves");
 };
@@ -408,10 +411,11 @@ __device__ __forceinline__ float act_bits_to_f32(uint32_t bits, bool bf16) {
 
 // Decode GEMV. One work-group per (block of block_m sorted rows, range of column tiles).
 // Loads are issued in dependency levels so that no wait drains the weight stream: (1) list
-// length, expert id and the block's sorted ids; (2) this pass's activation rows; (3) the
-// first two weight chunks. Waiting for (2) then leaves (3) in flight, and the chunk loop
-// keeps two chunks in flight after that. Row compaction (real rows first) is computed by
-// every wave from a ballot, so the prologue has no work-group barrier.
+// length, expert id and the block's sorted ids; (2) this pass's activation rows (and, for
+// 4-group chunks, every scale and zero-point word the wave will use); (3) the first two
+// weight chunks. Waiting for (2) then leaves (3) in flight, and the chunk loop keeps two
+// chunks in flight after that. Row compaction (real rows first) is computed by every wave
+// from a ballot, so the prologue has no work-group barrier.
 // AQ: x is fp16/bf16 and each pass quantises its rows in registers, bit-identical to
 // act_quant_kernel (the row absmax is combined across the KSPLIT waves through LDS).
 template <Epi EPI, int GPW, int KSPLIT, bool AQ>
@@ -422,11 +426,17 @@ __global__ void __launch_bounds__(256, 2) grouped_gemv_kernel(Params p, int tpt)
     __shared__ int s_opad[4][16];
     __shared__ int s_oslot[4][16];
     __shared__ float s_oasc[4][16];
+    // staged scales (4 fp16 per row) and zero-point words (4 groups per 8 rows) of every
+    // chunk of the wave: [chunk][fragment][column] and [chunk][fragment][column / 8]
+    __shared__ uint2 s_sc[4][C::kStagedSZ ? kGemvMaxTiles * C::FR * 16 : 1];
+    __shared__ uint4 s_zw[4][C::kStagedSZ ? kGemvMaxTiles * C::FR * 2 : 1];
     v4f* s_part = reinterpret_cast<v4f*>(s_dyn);   // [wave][tile][NF][lane]
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    // wave-uniform (the compiler cannot prove tid >> 6 uniform): keeps the tile range and
+    // the chunk loop scalar, so the loop and its wait counts are not per-lane
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int q = lane >> 4;           // k quarter of a group / D row quad of this lane
     const int c16 = lane & 15;         // B column / A row of this lane
     const int64_t row0 = (int64_t)blockIdx.y * p.block_m;
@@ -461,35 +471,72 @@ __global__ void __launch_bounds__(256, 2) grouped_gemv_kernel(Params p, int tpt)
     const int32_t* ze = p.zeros ? p.zeros + (int64_t)e * (p.N / 8) * p.G : nullptr;
     constexpr float wscale = kNibbleScale;
 
-    // weight row of fragment f in the tile set starting at tile t (edge columns read row 0:
-    // never stored, and the loads stay unconditional)
-    auto row_of = [&](int t, int f) -> int {
+    // weight row of fragment f, column c in the tile set starting at tile t (edge columns
+    // read row 0: never stored, and the loads stay unconditional)
+    auto row_of_col = [&](int t, int f, int c) -> int {
         const int tt = t + f % C::CT;
-        const int col = tt * 16 + c16;
+        const int col = tt * 16 + c;
         const bool up = C::kSilu && f >= C::CT;
         return (tt < t_end && col < ncols) ? (up ? col + ncols : col) : 0;
     };
+    auto row_of = [&](int t, int f) -> int { return row_of_col(t, f, c16); };
 
-    uint4 wv[2][C::GC][C::FR];
-    uint32_t sw[2][C::FR][C::GC];
-    int32_t zw[2][C::FR][C::GC];
+    // Issues are unconditional: a chunk past the end (c >= nch) loads the expert's first
+    // 16 bytes in every lane instead, so every step of the chunk loop has the same loads in
+    // flight and the compiler's wait counts stay exact (a conditional issue makes it wait
+    // for everything at the join). Word u * FR + f of a chunk = group u, fragment f,
+    // quarter q of this lane's column.
+    uint4 wv[2][C::GC * C::FR];
+    uint32_t sw[2][C::kStagedSZ ? 1 : C::FR][C::GC];
+    int32_t zw[2][C::kStagedSZ ? 1 : C::FR][C::GC];
     auto issue = [&](int c, auto bufc) {
         constexpr int b = decltype(bufc)::value;
+        const bool live = c < nch;
         const int t = t_begin + (c / C::NB) * C::CT;
-        const int g = g0 + (c % C::NB) * C::GC;
+        const int g = live ? g0 + (c % C::NB) * C::GC : g0;
 #pragma unroll
         for (int f = 0; f < C::FR; ++f) {
-            const int n = row_of(t, f);
-            const int32_t* wr = we + (int64_t)n * kw_row + g * (kGroup / 8) + q * 4;
+            const int n = live ? row_of(t, f) : 0;
+            const int32_t* wr = we + (live ? (int64_t)n * kw_row + g * (kGroup / 8) + q * 4 : 0);
 #pragma unroll
             for (int u = 0; u < C::GC; ++u)
-                wv[b][u][f] = *reinterpret_cast<const uint4*>(wr + u * (kGroup / 8));
-            load_scales<C::GC>(se + (int64_t)n * p.G + g, sw[b][f]);
-            if (ze) load_zero_words<C::GC>(ze + (int64_t)(n >> 3) * p.G + g, zw[b][f]);
+                wv[b][u * C::FR + f] =
+                    *reinterpret_cast<const uint4*>(wr + (live ? u * (kGroup / 8) : 0));
+            if constexpr (!C::kStagedSZ) {
+                load_scales<C::GC>(se + (int64_t)n * p.G + g, sw[b][f]);
+                // symmetric weights load (and ignore) scale words instead: same load count
+                load_zero_words<C::GC>(ze ? ze + (int64_t)(n >> 3) * p.G + g
+                                          : reinterpret_cast<const int32_t*>(p.scales),
+                                       zw[b][f]);
+            }
         }
     };
     using B0 = std::integral_constant<int, 0>;
     using B1 = std::integral_constant<int, 1>;
+
+    // ---- level 2a (4-group chunks): every scale / zero-point word of the wave's chunks ----
+    constexpr int kScEntries = C::kStagedSZ ? kGemvMaxTiles * C::FR * 16 : 1;
+    constexpr int kZwEntries = C::kStagedSZ ? kGemvMaxTiles * C::FR * 2 : 1;
+    uint2 sc_reg[(kScEntries + 63) / 64];
+    uint4 zw_reg;
+    if constexpr (C::kStagedSZ) {
+#pragma unroll
+        for (int i = 0; i < (kScEntries + 63) / 64; ++i) {
+            const int en = i * 64 + lane;
+            const int c = en / (C::FR * 16);
+            const int f = (en / 16) % C::FR;
+            const int n = c < nch ? row_of_col(t_begin + c * C::CT, f, en & 15) : 0;
+            sc_reg[i] = *reinterpret_cast<const uint2*>(se + (int64_t)n * p.G + g0);
+        }
+        {
+            const int en = min(lane, kZwEntries - 1);
+            const int c = en / (C::FR * 2);
+            const int f = (en / 2) % C::FR;
+            const int n = c < nch ? row_of_col(t_begin + c * C::CT, f, (en & 1) * 8) : 0;
+            zw_reg = *reinterpret_cast<const uint4*>(
+                ze ? ze + (int64_t)(n >> 3) * p.G + g0 : reinterpret_cast<const int32_t*>(p.scales));
+        }
+    }
 
     for (int m0 = 0; m0 < mreal; m0 += 16) {
         if (m0 > 0) __syncthreads();   // LDS partials / row maxima of the previous pass consumed
@@ -510,13 +557,13 @@ __global__ void __launch_bounds__(256, 2) grouped_gemv_kernel(Params p, int tpt)
             }
             my_asc = p.asc[asrc];
             // ---- level 3: the first two weight chunks ----
-            if (nch > 0) issue(0, B0{});
-            if (nch > 1) issue(1, B1{});
+            issue(0, B0{});
+            issue(1, B1{});
         } else {
             // the first weight chunks go out with the raw rows; the wait for the rows then
             // also covers those chunks, which were issued just before them
-            if (nch > 0) issue(0, B0{});
-            if (nch > 1) issue(1, B1{});
+            issue(0, B0{});
+            issue(1, B1{});
             const uint16_t* xr = reinterpret_cast<const uint16_t*>(p.xh) + (int64_t)asrc * p.K + q * 32;
             const bool bf16 = p.xbf16;
             uint4 raw[GPW][4];   // 32 values of group g0 + u: k = 8i .. 8i+7 in raw[u][i]
@@ -543,8 +590,12 @@ __global__ void __launch_bounds__(256, 2) grouped_gemv_kernel(Params p, int tpt)
                     }
                 }
             float amax = act_bits_to_f32(mbits, bf16);
-            amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
-            amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+            {   // the 4 quarter-lanes of each row: lanes l, l ^ 16, l ^ 32, l ^ 48
+                const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(amax), __float_as_uint(amax), false, false);
+                amax = fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+                const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(amax), __float_as_uint(amax), false, false);
+                amax = fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+            }
             if constexpr (KSPLIT > 1) {
                 if (q == 0) s_amax[wave][c16] = amax;
                 lds_barrier();
@@ -576,6 +627,14 @@ __global__ void __launch_bounds__(256, 2) grouped_gemv_kernel(Params p, int tpt)
                                    v4f{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
             for (int r = 0; r < 4; ++r) sa[u][r] *= 1.0f / kNibbleScale;
+        }
+        if constexpr (C::kStagedSZ) {
+            // the staged words were loaded before the activation rows: in registers by now
+            if (m0 == 0) {
+#pragma unroll
+                for (int i = 0; i < (kScEntries + 63) / 64; ++i) s_sc[wave][i * 64 + lane] = sc_reg[i];
+                if (lane < kZwEntries) s_zw[wave][lane] = zw_reg;
+            }
         }
 
         // per-wave table of this pass's 16 output rows (padded row, slot, scale), read back
@@ -619,15 +678,33 @@ __global__ void __launch_bounds__(256, 2) grouped_gemv_kernel(Params p, int tpt)
 #pragma unroll
             for (int f = 0; f < C::FR; ++f) {
                 const int zsh = (row_of(t, f) & 7) * 4;
+                uint32_t scw[C::GC];
+                int32_t zwd[C::GC];
+                if constexpr (C::kStagedSZ) {
+                    const uint2 sv = s_sc[wave][(c * C::FR + f) * 16 + c16];
+                    const uint4 zv = s_zw[wave][(c * C::FR + f) * 2 + (c16 >> 3)];
+                    scw[0] = sv.x;
+                    scw[1] = sv.y;
+                    zwd[0] = (int32_t)zv.x;
+                    zwd[1] = (int32_t)zv.y;
+                    zwd[2] = (int32_t)zv.z;
+                    zwd[3] = (int32_t)zv.w;
+                } else {
+#pragma unroll
+                    for (int u = 0; u < C::GC; ++u) {
+                        scw[u] = sw[b][f][u];
+                        zwd[u] = zw[b][f][u];
+                    }
+                }
 #pragma unroll
                 for (int u = 0; u < C::GC; ++u) {
                     const int ua = gb * C::GC + u;
-                    v4f acc = mfma_16x16x128(af[ua], spread_nibbles(wv[b][u][f]),
+                    v4f acc = mfma_16x16x128(af[ua], spread_nibbles(wv[b][u * C::FR + f]),
                                              v4f{0.f, 0.f, 0.f, 0.f});
-                    const float z = ze ? (float)((zw[b][f][u] >> zsh) & 0xF) : 8.0f;
+                    const float z = ze ? (float)((zwd[u] >> zsh) & 0xF) : 8.0f;
 #pragma unroll
                     for (int r = 0; r < 4; ++r) acc[r] = fmaf(-z, sa[ua][r], acc[r]);
-                    const float s = scale_at<C::GC>(sw[b][f], u);
+                    const float s = scale_at<C::GC>(scw, u);
 #pragma unroll
                     for (int r = 0; r < 4; ++r) run[f][r] = fmaf(acc[r], s, run[f][r]);
                 }
@@ -660,11 +737,9 @@ __global__ void __launch_bounds__(256, 2) grouped_gemv_kernel(Params p, int tpt)
 
         for (int c = 0; c < nch; c += 2) {
             consume(c, B0{});
-            if (c + 2 < nch) issue(c + 2, B0{});
-            if (c + 1 < nch) {
-                consume(c + 1, B1{});
-                if (c + 3 < nch) issue(c + 3, B1{});
-            }
+            issue(c + 2, B0{});
+            if (c + 1 < nch) consume(c + 1, B1{});
+            issue(c + 3, B1{});
         }
 
         if constexpr (KSPLIT > 1) {
@@ -755,14 +830,15 @@ GemvSplit gemv_split(int G) {
     }
 }
 
-// Column tiles per wave team: enough work per work-group to hide the prologue (~32 KB of
-// weights per wave), fewer when the grid would otherwise leave CUs idle.
+// Column tiles per wave team: enough work per work-group to hide the prologue (~64 KB of
+// weights per wave), fewer when the grid would otherwise leave CUs idle (two work-groups
+// per CU fit; 512 keeps every CU of a 256-CU part busy).
 int gemv_default_tpt(const Params& p, int ntiles, int frag_bytes_per_tile_wave, int teams) {
     const int64_t blocks = std::min<int64_t>((p.P + p.block_m - 1) / p.block_m, p.num_valid);
-    int tpt = std::max(1, (32 * 1024) / frag_bytes_per_tile_wave);
+    int tpt = std::max(1, (64 * 1024) / frag_bytes_per_tile_wave);
     tpt = std::min(tpt, kGemvMaxTiles);
-    // keep >= ~1024 work-groups when the routing touches few blocks (T = 1 decode)
-    while (tpt > 1 && blocks * ((ntiles + teams * tpt - 1) / (teams * tpt)) < 1024) tpt >>= 1;
+    // keep >= ~512 work-groups when the routing touches few blocks (T = 1 decode)
+    while (tpt > 1 && blocks * ((ntiles + teams * tpt - 1) / (teams * tpt)) < 512) tpt >>= 1;
     return tpt;
 }
 

@@ -213,6 +213,40 @@ constexpr int kRouterMaxPerLane = 16;   // E <= 1024
 
 // NV = logits per lane (E <= 64 * NV). Loads are unconditional (clamped index, the
 // out-of-range entries masked to -inf afterwards) so they issue together.
+// (value desc, expert asc) maximum over the wave; every lane gets it.
+__device__ __forceinline__ void argmax_pick(float& bv, int& be, float ov, int oe) {
+    if (ov > bv || (ov == bv && oe < be)) {
+        bv = ov;
+        be = oe;
+    }
+}
+template <int S>
+__device__ __forceinline__ void argmax_dpp(float& bv, int& be) {
+    const float ov = __uint_as_float(dpp_step<S>(__float_as_uint(bv)));
+    const int oe = (int)dpp_step<S>((uint32_t)be);
+    argmax_pick(bv, be, ov, oe);
+}
+__device__ __forceinline__ void wave_argmax(float& bv, int& be) {
+    argmax_dpp<0>(bv, be);
+    argmax_dpp<1>(bv, be);
+    argmax_dpp<2>(bv, be);
+    argmax_dpp<3>(bv, be);
+    {
+        const auto rv = __builtin_amdgcn_permlane16_swap(__float_as_uint(bv), __float_as_uint(bv), false, false);
+        const auto re = __builtin_amdgcn_permlane16_swap((uint32_t)be, (uint32_t)be, false, false);
+        bv = __uint_as_float(rv[0]);
+        be = (int)re[0];
+        argmax_pick(bv, be, __uint_as_float(rv[1]), (int)re[1]);
+    }
+    {
+        const auto rv = __builtin_amdgcn_permlane32_swap(__float_as_uint(bv), __float_as_uint(bv), false, false);
+        const auto re = __builtin_amdgcn_permlane32_swap((uint32_t)be, (uint32_t)be, false, false);
+        bv = __uint_as_float(rv[0]);
+        be = (int)re[0];
+        argmax_pick(bv, be, __uint_as_float(rv[1]), (int)re[1]);
+    }
+}
+
 template <int NV>
 __global__ void __launch_bounds__(256) topk_softmax_kernel(
     const float* __restrict__ logits, int64_t T, int E, int top_k, bool renorm,
@@ -251,12 +285,7 @@ __global__ void __launch_bounds__(256) topk_softmax_kernel(
                 be = e;
             }
         }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            const float ov = __shfl_xor(bv, o, 64);
-            const int oe = __shfl_xor(be, o, 64);
-            if (ov > bv || (ov == bv && oe < be)) { bv = ov; be = oe; }
-        }
+        wave_argmax(bv, be);
         if ((be & 63) == lane) taken |= 1u << (be >> 6);
         const float p = expf(bv - m) / ssum;
         sum_sel += p;

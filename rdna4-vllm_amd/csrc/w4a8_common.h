@@ -141,17 +141,50 @@ __device__ __forceinline__ int nth_set_bit(uint64_t m, int k) {
     return pos;
 }
 
-// Wave64 reductions.
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+// Cross-lane moves on the VALU, without the LDS round trip of ds_bpermute (__shfl): DPP
+// inside rows of 16 lanes, the gfx950 permlane swaps across rows and halves. lane_step<S>
+// pairs lane l with a lane of the other half of its 2^(S+1)-lane group: lane l ^ 1, l ^ 2,
+// then the mirrored lane of the 8- and 16-lane groups. Once the smaller groups hold one
+// value each (true inside every reduction below) the mirrored lane holds what lane
+// l ^ (1 << S) holds, so these reductions equal the xor butterfly bit for bit. Every lane
+// of the wave must be active.
+template <int S>
+__device__ __forceinline__ uint32_t dpp_step(uint32_t v) {
+    static_assert(S >= 0 && S < 4, "DPP steps stay inside a row of 16 lanes");
+    constexpr int ctrl = S == 0 ? 0xB1 : S == 1 ? 0x4E : S == 2 ? 0x141 : 0x140;
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, ctrl, 0xF, 0xF, false);
+}
+
+// v combined over aligned groups of 2^LOG2 lanes (op commutative and associative).
+template <int LOG2, typename Op>
+__device__ __forceinline__ float lane_allreduce(float v, Op op) {
+    if constexpr (LOG2 > 0) v = op(v, __uint_as_float(dpp_step<0>(__float_as_uint(v))));
+    if constexpr (LOG2 > 1) v = op(v, __uint_as_float(dpp_step<1>(__float_as_uint(v))));
+    if constexpr (LOG2 > 2) v = op(v, __uint_as_float(dpp_step<2>(__float_as_uint(v))));
+    if constexpr (LOG2 > 3) v = op(v, __uint_as_float(dpp_step<3>(__float_as_uint(v))));
+    if constexpr (LOG2 > 4) {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v),
+                                                        false, false);
+        v = op(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    }
+    if constexpr (LOG2 > 5) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v),
+                                                        false, false);
+        v = op(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    }
     return v;
 }
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
+
+struct MaxOp {
+    __device__ float operator()(float a, float b) const { return fmaxf(a, b); }
+};
+struct SumOp {
+    __device__ float operator()(float a, float b) const { return a + b; }
+};
+
+// Wave64 reductions (every lane gets the result).
+__device__ __forceinline__ float wave_max(float v) { return lane_allreduce<6>(v, MaxOp{}); }
+__device__ __forceinline__ float wave_sum(float v) { return lane_allreduce<6>(v, SumOp{}); }
 
 // Activation scale from an fp32 absmax (moe_kernel.hip:117-118).
 __device__ __forceinline__ float act_scale_from_absmax(float amax) {
