@@ -125,7 +125,10 @@ def cpu_baseline(cfg, ws, x, tw, ids, out_gpu, budget_s):
         cores = max([i.get("num_threads", 1) for i in threadpool_info()] + [1])
     except Exception:  # noqa: BLE001
         cores = 1
-    host = {k: v.cpu().numpy() for k, v in ws.items()}
+    host = {k: (None if v is None else v.cpu().numpy()) for k, v in ws.items()}
+    for k in ("w13", "w2"):   # the oracle reads the op layout
+        if host[k].ndim == 5:
+            host[k] = O.unrepack_fragments(host[k])
     xf = x.float().cpu().numpy()
     twn, idn = tw.cpu().numpy(), ids.cpu().numpy()
     T = xf.shape[0]
@@ -162,6 +165,10 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--layout", choices=["fragments", "op"], default="fragments",
+                    help="weights as stored after loading: the gfx950 fragment layout "
+                         "(repacked once per weight set, outside the timed region) or the "
+                         "reference op layout")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -182,6 +189,13 @@ def main():
     per_set = E * (b13 + b2)
     R = args.rotate or max(4, math.ceil(1.0e9 / per_set))
     sets = [make_weights(cfg, 1000 + cfgno * 17 + r, dev) for r in range(R)]
+    if args.layout == "fragments":
+        # load-time repack (the process_weights_after_loading step); op-layout copies freed
+        for ws in sets:
+            ws["w13"] = W.repack_fragments(ws["w13"])
+            ws["w2"] = W.repack_fragments(ws["w2"])
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
     x, logits = make_inputs(cfg, 1000 + cfgno, dev)
     torch.cuda.synchronize()
 
@@ -296,6 +310,7 @@ def main():
                    "T": T, "H": H, "E": E, "top_k": k, "I": I, "group": g,
                    "routing": cfg["routing"], "weight_sets_rotated": R,
                    "timing": "hip-graph replay" if graphs is not None else "eager",
+                   "weight_layout": args.layout,
                    "parallelism": "1 GPU"},
         "roofline": roof,
         "layer": {"distinct_experts": distinct, "algorithmic_bytes": layer_bytes,

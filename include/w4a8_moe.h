@@ -190,6 +190,31 @@ W4A8_API int w4a8_moe_apply(const void* x, int x_dtype, int64_t T, int64_t H, in
                    const int32_t* expert_map, int weight_is_e2m1, void* out,
                    void* workspace, size_t workspace_bytes, void* stream);
 
+/* Load-time repack of int4 weights from the op layout (E, N, K/8) int32 (moe_kernel.hip:7-17)
+ * into the fragment layout the gfx950 kernels stream: per expert, 16-row tile t and 128-wide
+ * K group g, one 1 KB block whose 16-byte lane l holds row 16t + l % 16, k in
+ * [128g + 32 (l / 16), +32) (the fp8 MFMA B operand of lane l); blocks ordered (e, t, g).
+ * A pure permutation of 16-byte words (same size). Needs N % 16 == 0, K % 128 == 0; out
+ * must not alias w_packed. No reference counterpart: the reference streams the op layout,
+ * and its load hook (moe_experts.py:1277-1306) is where a caller runs this once. */
+W4A8_API int w4a8_repack_int4_fragments(const int32_t* w_packed, int64_t E, int64_t N, int64_t K,
+                                        int32_t* out, void* stream);
+
+/* w4a8_moe_apply on weights repacked by w4a8_repack_int4_fragments (w13 and w2); scales
+ * and zero-points stay in the op layout. Same workspace (w4a8_moe_apply_workspace_size) and
+ * bit-identical results. Needs group_size 128, int4 weights (no E2M1), and hidden and
+ * intermediate sizes that are multiples of 128 with K/128 in {1,2,3,4,8,12,16} and <= 32.
+ * No reference counterpart (the reference's composition, moe_experts.py:493-665, runs on
+ * the op layout). */
+W4A8_API int w4a8_moe_apply_fragments(const void* x, int x_dtype, int64_t T, int64_t H,
+                                      int64_t inter, int64_t E, int64_t top_k, int64_t group_size,
+                                      const int32_t* w13_frag, const void* w13_scales_f16,
+                                      const int32_t* w13_zeros, const int32_t* w2_frag,
+                                      const void* w2_scales_f16, const int32_t* w2_zeros,
+                                      const float* topk_weights, const int32_t* topk_ids,
+                                      const int32_t* expert_map, void* out, void* workspace,
+                                      size_t workspace_bytes, void* stream);
+
 /* Optional per-stage timing of w4a8_moe_apply on the calling thread: when count == 8,
  * the next w4a8_moe_apply calls record events[0] before the first launch and events[i]
  * after stage i (1 align, 2 act-quant x, 3 reserved (empty), 4 gemm1+SiLU, 5 act-quant

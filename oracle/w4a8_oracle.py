@@ -45,6 +45,9 @@ PINNING = {
         "against the unpacked ground truth (reference test property) + round trips",
     "moe_layer": "float64 un-quantised MoE within the fp8 quantisation error bound; "
                  "composition equals the per-stage oracle chain",
+    "repack_fragments": "per-element brute force of the layout definition on tiny shapes "
+                        "(nibble of row n, k lands in lane n % 16 + 16 * ((k % 128) // 32)); "
+                        "inverse restores the op layout exactly",
 }
 
 # --------------------------------------------------------------------------- #
@@ -150,6 +153,29 @@ def pack_nibbles(nib) -> np.ndarray:
     for j in range(8):
         w |= nib[..., j] << (4 * j)
     return w.astype(np.uint32).view(np.int32)
+
+
+def repack_fragments(w_packed) -> np.ndarray:
+    """Op layout (E, N, K/8) int32 -> fragment layout (E, N/16, K/128, 64, 4) int32.
+
+    Not a reference function: the gfx950 kernels' load-time layout. Block (e, t, g) lane l
+    (16 bytes = 4 words) holds row n = 16t + l % 16, words 16g + 4 (l // 16) .. +3, i.e.
+    k in [128g + 32 (l // 16), +32): the raw-nibble fp8 MFMA B operand of lane l."""
+    w = np.asarray(w_packed)
+    E, N, K8 = w.shape
+    G = K8 // 16
+    assert N % 16 == 0 and K8 % 16 == 0
+    # (E, t, c, g, q, word) -> (E, t, g, q, c, word); lane = 16 q + c
+    v = w.reshape(E, N // 16, 16, G, 4, 4).transpose(0, 1, 3, 4, 2, 5)
+    return np.ascontiguousarray(v).reshape(E, N // 16, G, 64, 4)
+
+
+def unrepack_fragments(w_frag) -> np.ndarray:
+    """Inverse of repack_fragments: (E, N/16, K/128, 64, 4) -> (E, N, K/8)."""
+    f = np.asarray(w_frag)
+    E, NT, G = f.shape[:3]
+    v = f.reshape(E, NT, G, 4, 16, 4).transpose(0, 1, 4, 2, 3, 5)
+    return np.ascontiguousarray(v).reshape(E, NT * 16, G * 16)
 
 
 def unpack_zeros(w_zeros, N: int) -> np.ndarray:

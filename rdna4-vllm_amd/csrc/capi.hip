@@ -183,6 +183,124 @@ struct SizeProbe {
 
 using namespace w4a8;
 
+namespace w4a8 {
+// frag: w13 / w2 in the fragment layout (launch_repack_fragments); only the GEMV and the
+// prefill tiles read it, so every other schedule is refused up front.
+int moe_apply_impl(const void* x, int x_dtype, int64_t T, int64_t H, int64_t inter, int64_t E,
+                   int64_t top_k, int64_t group_size, const int32_t* w13,
+                   const void* w13_scales_f16, const int32_t* w13_zeros, const int32_t* w2,
+                   const void* w2_scales_f16, const int32_t* w2_zeros,
+                   const float* topk_weights, const int32_t* topk_ids,
+                   const int32_t* expert_map, int weight_is_e2m1, void* out, void* workspace,
+                   size_t workspace_bytes, void* stream, bool frag) {
+    W4A8_REQUIRE(x_dtype == W4A8_DTYPE_F16 || x_dtype == W4A8_DTYPE_BF16, "x dtype must be fp16 or bf16");
+    W4A8_REQUIRE(T >= 0 && H > 0 && inter > 0 && E > 0 && top_k > 0, "moe_apply: invalid sizes");
+    W4A8_REQUIRE(group_size > 0 && H % group_size == 0 && inter % group_size == 0 &&
+                 group_size % 16 == 0 && group_size <= kMaxGroupSize,
+                 "moe_apply: group_size must divide hidden and intermediate, mult of 16, <= 128");
+    W4A8_REQUIRE(H % 8 == 0 && inter % 8 == 0, "moe_apply: sizes must be multiples of 8");
+    W4A8_REQUIRE(!(weight_is_e2m1 && (w13_zeros || w2_zeros)),
+                 "mxfp4 (E2M1) weights are symmetric; w_zeros must be empty");
+    W4A8_REQUIRE(!frag || (!weight_is_e2m1 && group_size == 128 && H % 128 == 0 &&
+                           inter % 128 == 0 && gemv_supported(H, group_size) &&
+                           gemv_supported(inter, group_size) &&
+                           prefill_supported(H, group_size, false) &&
+                           prefill_supported(inter, group_size, false)),
+                 "fragment-layout weights need int4 g128 with hidden and intermediate sizes "
+                 "the GEMV and the prefill tiles take");
+    if (T == 0) return W4A8_OK;
+    W4A8_REQUIRE(x && w13 && w13_scales_f16 && w2 && w2_scales_f16 && topk_weights && topk_ids && out,
+                 "moe_apply: null pointer");
+    hipStream_t s = as_stream(stream);
+    const ApplyPlan pl = plan_apply(T, E, top_k);
+    Workspace w(workspace, workspace_bytes);
+    int32_t *sti, *eid, *ntp; void* aws; size_t abytes; uint8_t* xq; float* s1; __half* h;
+    uint8_t* hq; float* s2; float* acc; float* gs1; float* gs2; __half* y; int32_t* s2r;
+    carve_apply(w, pl, T, H, inter, E, top_k, &sti, &eid, &ntp, &aws, &abytes, &xq, &s1, &h, &hq,
+                &s2, &acc, &gs1, &gs2, &y, &s2r);
+    if (workspace == nullptr || !w.ok()) {
+        set_error("moe_apply: workspace smaller than w4a8_moe_apply_workspace_size()");
+        return W4A8_ERR_WORKSPACE;
+    }
+    const bool bf16 = x_dtype == W4A8_DTYPE_BF16;
+    const bool e2m1 = weight_is_e2m1 != 0;
+    const int64_t numel = T * top_k;
+    const bool mfma = mfma_supported(H, group_size) && mfma_supported(inter, group_size);
+    // prefill tiles need the per-group sums of the quantised rows (zero-point term)
+    const bool pf1 = !pl.decode && mfma && prefill_supported(H, group_size, e2m1);
+    const bool pf2 = !pl.decode && mfma && prefill_supported(inter, group_size, e2m1);
+    stage_mark(0, s);
+    if (pl.decode && numel <= kAlignSmallMax) {
+        // one launch: align in work-group 0, act-quant of x in the others
+        if (int rc = launch_align_quant(topk_ids, numel, E, pl.block_m, expert_map, sti, pl.P,
+                                        eid, ntp, s2r, x, bf16, T, H, xq, s1, nullptr, s))
+            return rc;
+        stage_mark(1, s);
+    } else {
+        if (int rc = launch_align(topk_ids, numel, E, pl.block_m, expert_map, sti, pl.P, eid,
+                                  ntp, aws, abytes, s, s2r))
+            return rc;
+        stage_mark(1, s);
+        if (int rc = launch_act_quant(x, bf16, T, H, xq, s1, true, s, nullptr, nullptr, 0,
+                                      pf1 ? gs1 : nullptr))
+            return rc;
+    }
+    stage_mark(2, s);
+    stage_mark(3, s);
+
+    // gemm1 + SiLU*mul -> h (P, inter)
+    GroupedArgs g1{};
+    g1.x_rows = T; g1.K = H; g1.w = w13; g1.scales = static_cast<const uint16_t*>(w13_scales_f16);
+    g1.zeros = w13_zeros; g1.E = E; g1.N = 2 * inter; g1.group_size = group_size;
+    g1.sorted_ids = sti; g1.P = pl.P; g1.expert_ids = eid; g1.ntp = ntp; g1.top_k = top_k;
+    g1.identity_gather = false; g1.num_valid = numel; g1.block_m = pl.block_m; g1.e2m1 = e2m1;
+    g1.epi = Epi::kSiluHalf; g1.out = h; g1.out_top_k = top_k; g1.x_fp8 = xq; g1.act_scales = s1;
+    g1.act_group_sums = pf1 ? gs1 : nullptr;
+    g1.w_frag = frag;
+    int rc;
+    if (!mfma) rc = launch_grouped_scalar(g1, s);
+    else if (pl.decode && !e2m1 && gemv_supported(H, group_size)) rc = launch_grouped_gemv(g1, s);
+    else if (pf1) rc = launch_grouped_prefill(g1, s);
+    else rc = launch_grouped_mfma(g1, s);
+    if (rc) return rc;
+    stage_mark(4, s);
+    // act-quant of h over real rows only, once per row (quantising inside the decode GEMV
+    // would repeat it for every work-group that reads the row)
+    const bool gemv2 = pl.decode && !e2m1 && gemv_supported(inter, group_size);
+    if ((rc = launch_act_quant(h, false, pl.P, inter, hq, s2, true, s, sti, ntp, numel,
+                               pf2 ? gs2 : nullptr)))
+        return rc;
+    stage_mark(5, s);
+    // gemm2 (identity gather) -> per-slot rows (decode) or scatter (prefill)
+    GroupedArgs g2{};
+    g2.x_rows = pl.P; g2.K = inter; g2.w = w2; g2.scales = static_cast<const uint16_t*>(w2_scales_f16);
+    g2.zeros = w2_zeros; g2.E = E; g2.N = H; g2.group_size = group_size;
+    g2.sorted_ids = sti; g2.P = pl.P; g2.expert_ids = eid; g2.ntp = ntp; g2.top_k = top_k;
+    g2.identity_gather = true; g2.num_valid = numel; g2.block_m = pl.block_m; g2.e2m1 = e2m1;
+    g2.epi = pl.decode ? Epi::kSlotF32 : Epi::kHalf; g2.out = pl.decode ? (void*)acc : (void*)y;
+    g2.topk_weights = topk_weights; g2.out_top_k = top_k;
+    g2.x = h; g2.x_bf16 = false;
+    g2.x_fp8 = hq;
+    g2.act_scales = s2;
+    g2.act_group_sums = pf2 ? gs2 : nullptr;
+    g2.w_frag = frag;
+    if (!mfma) rc = launch_grouped_scalar(g2, s);
+    else if (gemv2) rc = launch_grouped_gemv(g2, s);
+    else if (pf2) rc = launch_grouped_prefill(g2, s);
+    else rc = launch_grouped_mfma(g2, s);
+    if (rc) return rc;
+    stage_mark(6, s);
+    // slots whose expert is not local / out of range contribute nothing
+    if (pl.decode)
+        rc = launch_slot_reduce(acc, topk_weights, topk_ids, expert_map, E, T, H, top_k, out,
+                                bf16, s);
+    else
+        rc = launch_row_reduce(y, s2r, topk_weights, T, H, top_k, out, bf16, s);
+    stage_mark(7, s);
+    return rc;
+}
+}  // namespace w4a8
+
 extern "C" {
 
 int w4a8_abi_version(void) { return 1; }
@@ -430,102 +548,34 @@ int w4a8_moe_apply(const void* x, int x_dtype, int64_t T, int64_t H, int64_t int
                    const int32_t* expert_map, int weight_is_e2m1, void* out, void* workspace,
                    size_t workspace_bytes, void* stream) {
     clear_error();
-    W4A8_REQUIRE(x_dtype == W4A8_DTYPE_F16 || x_dtype == W4A8_DTYPE_BF16, "x dtype must be fp16 or bf16");
-    W4A8_REQUIRE(T >= 0 && H > 0 && inter > 0 && E > 0 && top_k > 0, "moe_apply: invalid sizes");
-    W4A8_REQUIRE(group_size > 0 && H % group_size == 0 && inter % group_size == 0 &&
-                 group_size % 16 == 0 && group_size <= kMaxGroupSize,
-                 "moe_apply: group_size must divide hidden and intermediate, mult of 16, <= 128");
-    W4A8_REQUIRE(H % 8 == 0 && inter % 8 == 0, "moe_apply: sizes must be multiples of 8");
-    W4A8_REQUIRE(!(weight_is_e2m1 && (w13_zeros || w2_zeros)),
-                 "mxfp4 (E2M1) weights are symmetric; w_zeros must be empty");
-    if (T == 0) return W4A8_OK;
-    W4A8_REQUIRE(x && w13 && w13_scales_f16 && w2 && w2_scales_f16 && topk_weights && topk_ids && out,
-                 "moe_apply: null pointer");
-    hipStream_t s = as_stream(stream);
-    const ApplyPlan pl = plan_apply(T, E, top_k);
-    Workspace w(workspace, workspace_bytes);
-    int32_t *sti, *eid, *ntp; void* aws; size_t abytes; uint8_t* xq; float* s1; __half* h;
-    uint8_t* hq; float* s2; float* acc; float* gs1; float* gs2; __half* y; int32_t* s2r;
-    carve_apply(w, pl, T, H, inter, E, top_k, &sti, &eid, &ntp, &aws, &abytes, &xq, &s1, &h, &hq,
-                &s2, &acc, &gs1, &gs2, &y, &s2r);
-    if (workspace == nullptr || !w.ok()) {
-        set_error("moe_apply: workspace smaller than w4a8_moe_apply_workspace_size()");
-        return W4A8_ERR_WORKSPACE;
-    }
-    const bool bf16 = x_dtype == W4A8_DTYPE_BF16;
-    const bool e2m1 = weight_is_e2m1 != 0;
-    const int64_t numel = T * top_k;
-    const bool mfma = mfma_supported(H, group_size) && mfma_supported(inter, group_size);
-    // prefill tiles need the per-group sums of the quantised rows (zero-point term)
-    const bool pf1 = !pl.decode && mfma && prefill_supported(H, group_size, e2m1);
-    const bool pf2 = !pl.decode && mfma && prefill_supported(inter, group_size, e2m1);
-    stage_mark(0, s);
-    if (pl.decode && numel <= kAlignSmallMax) {
-        // one launch: align in work-group 0, act-quant of x in the others
-        if (int rc = launch_align_quant(topk_ids, numel, E, pl.block_m, expert_map, sti, pl.P,
-                                        eid, ntp, s2r, x, bf16, T, H, xq, s1, nullptr, s))
-            return rc;
-        stage_mark(1, s);
-    } else {
-        if (int rc = launch_align(topk_ids, numel, E, pl.block_m, expert_map, sti, pl.P, eid,
-                                  ntp, aws, abytes, s, s2r))
-            return rc;
-        stage_mark(1, s);
-        if (int rc = launch_act_quant(x, bf16, T, H, xq, s1, true, s, nullptr, nullptr, 0,
-                                      pf1 ? gs1 : nullptr))
-            return rc;
-    }
-    stage_mark(2, s);
-    stage_mark(3, s);
+    return moe_apply_impl(x, x_dtype, T, H, inter, E, top_k, group_size, w13, w13_scales_f16,
+                          w13_zeros, w2, w2_scales_f16, w2_zeros, topk_weights, topk_ids,
+                          expert_map, weight_is_e2m1, out, workspace, workspace_bytes, stream,
+                          false);
+}
 
-    // gemm1 + SiLU*mul -> h (P, inter)
-    GroupedArgs g1{};
-    g1.x_rows = T; g1.K = H; g1.w = w13; g1.scales = static_cast<const uint16_t*>(w13_scales_f16);
-    g1.zeros = w13_zeros; g1.E = E; g1.N = 2 * inter; g1.group_size = group_size;
-    g1.sorted_ids = sti; g1.P = pl.P; g1.expert_ids = eid; g1.ntp = ntp; g1.top_k = top_k;
-    g1.identity_gather = false; g1.num_valid = numel; g1.block_m = pl.block_m; g1.e2m1 = e2m1;
-    g1.epi = Epi::kSiluHalf; g1.out = h; g1.out_top_k = top_k; g1.x_fp8 = xq; g1.act_scales = s1;
-    g1.act_group_sums = pf1 ? gs1 : nullptr;
-    int rc;
-    if (!mfma) rc = launch_grouped_scalar(g1, s);
-    else if (pl.decode && !e2m1 && gemv_supported(H, group_size)) rc = launch_grouped_gemv(g1, s);
-    else if (pf1) rc = launch_grouped_prefill(g1, s);
-    else rc = launch_grouped_mfma(g1, s);
-    if (rc) return rc;
-    stage_mark(4, s);
-    // act-quant of h over real rows only, once per row (quantising inside the decode GEMV
-    // would repeat it for every work-group that reads the row)
-    const bool gemv2 = pl.decode && !e2m1 && gemv_supported(inter, group_size);
-    if ((rc = launch_act_quant(h, false, pl.P, inter, hq, s2, true, s, sti, ntp, numel,
-                               pf2 ? gs2 : nullptr)))
-        return rc;
-    stage_mark(5, s);
-    // gemm2 (identity gather) -> per-slot rows (decode) or scatter (prefill)
-    GroupedArgs g2{};
-    g2.x_rows = pl.P; g2.K = inter; g2.w = w2; g2.scales = static_cast<const uint16_t*>(w2_scales_f16);
-    g2.zeros = w2_zeros; g2.E = E; g2.N = H; g2.group_size = group_size;
-    g2.sorted_ids = sti; g2.P = pl.P; g2.expert_ids = eid; g2.ntp = ntp; g2.top_k = top_k;
-    g2.identity_gather = true; g2.num_valid = numel; g2.block_m = pl.block_m; g2.e2m1 = e2m1;
-    g2.epi = pl.decode ? Epi::kSlotF32 : Epi::kHalf; g2.out = pl.decode ? (void*)acc : (void*)y;
-    g2.topk_weights = topk_weights; g2.out_top_k = top_k;
-    g2.x = h; g2.x_bf16 = false;
-    g2.x_fp8 = hq;
-    g2.act_scales = s2;
-    g2.act_group_sums = pf2 ? gs2 : nullptr;
-    if (!mfma) rc = launch_grouped_scalar(g2, s);
-    else if (gemv2) rc = launch_grouped_gemv(g2, s);
-    else if (pf2) rc = launch_grouped_prefill(g2, s);
-    else rc = launch_grouped_mfma(g2, s);
-    if (rc) return rc;
-    stage_mark(6, s);
-    // slots whose expert is not local / out of range contribute nothing
-    if (pl.decode)
-        rc = launch_slot_reduce(acc, topk_weights, topk_ids, expert_map, E, T, H, top_k, out,
-                                bf16, s);
-    else
-        rc = launch_row_reduce(y, s2r, topk_weights, T, H, top_k, out, bf16, s);
-    stage_mark(7, s);
-    return rc;
+int w4a8_moe_apply_fragments(const void* x, int x_dtype, int64_t T, int64_t H, int64_t inter,
+                             int64_t E, int64_t top_k, int64_t group_size, const int32_t* w13_frag,
+                             const void* w13_scales_f16, const int32_t* w13_zeros,
+                             const int32_t* w2_frag, const void* w2_scales_f16,
+                             const int32_t* w2_zeros, const float* topk_weights,
+                             const int32_t* topk_ids, const int32_t* expert_map, void* out,
+                             void* workspace, size_t workspace_bytes, void* stream) {
+    clear_error();
+    return moe_apply_impl(x, x_dtype, T, H, inter, E, top_k, group_size, w13_frag,
+                          w13_scales_f16, w13_zeros, w2_frag, w2_scales_f16, w2_zeros,
+                          topk_weights, topk_ids, expert_map, 0, out, workspace, workspace_bytes,
+                          stream, true);
+}
+
+int w4a8_repack_int4_fragments(const int32_t* w_packed, int64_t E, int64_t N, int64_t K,
+                               int32_t* out, void* stream) {
+    clear_error();
+    W4A8_REQUIRE(E >= 0 && N >= 0 && K >= 0, "repack: invalid sizes");
+    W4A8_REQUIRE(N % 16 == 0 && K % 128 == 0, "repack: needs N % 16 == 0 and K % 128 == 0");
+    W4A8_REQUIRE(E * N * K == 0 || (w_packed && out), "repack: null pointer");
+    W4A8_REQUIRE(w_packed != out, "repack: out must not alias w_packed");
+    return launch_repack_fragments(w_packed, E, N, K, out, as_stream(stream));
 }
 
 }  // extern "C"

@@ -418,7 +418,9 @@ __device__ __forceinline__ float act_bits_to_f32(uint32_t bits, bool bf16) {
 // from a ballot, so the prologue has no work-group barrier.
 // AQ: x is fp16/bf16 and each pass quantises its rows in registers, bit-identical to
 // act_quant_kernel (the row absmax is combined across the KSPLIT waves through LDS).
-template <Epi EPI, int GPW, int KSPLIT, bool AQ>
+// FRAG: weights in the fragment layout (repack.hip): a fragment-group is one contiguous
+// kilobyte, lane l's 16 bytes at offset 16 l.
+template <Epi EPI, int GPW, int KSPLIT, bool AQ, bool FRAG>
 __global__ void __launch_bounds__(256, 2) grouped_gemv_kernel(Params p, int tpt) {
     using C = GemvCfg<EPI, GPW, KSPLIT>;
     extern __shared__ __attribute__((aligned(16))) uint8_t s_dyn[];   // KSPLIT > 1 partials
@@ -497,11 +499,15 @@ __global__ void __launch_bounds__(256, 2) grouped_gemv_kernel(Params p, int tpt)
 #pragma unroll
         for (int f = 0; f < C::FR; ++f) {
             const int n = live ? row_of(t, f) : 0;
-            const int32_t* wr = we + (live ? (int64_t)n * kw_row + g * (kGroup / 8) + q * 4 : 0);
+            // op layout: row n, words 16 (g + u) + 4 q; fragment layout: block (n / 16, g + u)
+            const int32_t* wr =
+                FRAG ? we + (live ? ((int64_t)(n >> 4) * p.G + g) * 256 + lane * 4 : 0)
+                     : we + (live ? (int64_t)n * kw_row + g * (kGroup / 8) + q * 4 : 0);
+            constexpr int ustep = FRAG ? 256 : kGroup / 8;
 #pragma unroll
             for (int u = 0; u < C::GC; ++u)
                 wv[b][u * C::FR + f] =
-                    *reinterpret_cast<const uint4*>(wr + (live ? u * (kGroup / 8) : 0));
+                    *reinterpret_cast<const uint4*>(wr + (live ? u * ustep : 0));
             if constexpr (!C::kStagedSZ) {
                 load_scales<C::GC>(se + (int64_t)n * p.G + g, sw[b][f]);
                 // symmetric weights load (and ignore) scale words instead: same load count
@@ -842,12 +848,12 @@ int gemv_default_tpt(const Params& p, int ntiles, int frag_bytes_per_tile_wave, 
     return tpt;
 }
 
-template <Epi EPI, int GPW, int KSPLIT, bool AQ>
+template <Epi EPI, int GPW, int KSPLIT, bool AQ, bool FRAG>
 int launch_gemv_a(const Params& p, int tpt, dim3 grid, size_t lds, hipStream_t s) {
     using C = GemvCfg<EPI, GPW, KSPLIT>;
     static bool attr_set = false;
     if (!attr_set) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&grouped_gemv_kernel<EPI, GPW, KSPLIT, AQ>),
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&grouped_gemv_kernel<EPI, GPW, KSPLIT, AQ, FRAG>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize,
                                 4 * kGemvMaxTiles * C::NF * 64 * (int)sizeof(v4f)) != hipSuccess) {
             set_error("grouped_gemv_kernel: cannot reserve dynamic LDS");
@@ -855,7 +861,7 @@ int launch_gemv_a(const Params& p, int tpt, dim3 grid, size_t lds, hipStream_t s
         }
         attr_set = true;
     }
-    grouped_gemv_kernel<EPI, GPW, KSPLIT, AQ><<<grid, 256, lds, s>>>(p, tpt);
+    grouped_gemv_kernel<EPI, GPW, KSPLIT, AQ, FRAG><<<grid, 256, lds, s>>>(p, tpt);
     return check_launch("grouped_gemv_kernel");
 }
 
@@ -869,8 +875,16 @@ int launch_gemv_t(const Params& p, int tpt, hipStream_t s) {
     const size_t lds = KSPLIT > 1 ? (size_t)4 * tpt * C::NF * 64 * sizeof(v4f) : 0;
     const dim3 grid((unsigned)((ntiles + C::TEAMS * tpt - 1) / (C::TEAMS * tpt)),
                     (unsigned)((p.P + p.block_m - 1) / p.block_m));
-    if (p.xq) return launch_gemv_a<EPI, GPW, KSPLIT, false>(p, tpt, grid, lds, s);
-    return launch_gemv_a<EPI, GPW, KSPLIT, true>(p, tpt, grid, lds, s);
+    if (p.w_frag) {
+        // fragment-layout weights come only with prequantised rows (the whole-layer path)
+        if (!p.xq) {
+            set_error("grouped GEMV: fragment-layout weights need prequantised activations");
+            return W4A8_ERR_INVALID;
+        }
+        return launch_gemv_a<EPI, GPW, KSPLIT, false, true>(p, tpt, grid, lds, s);
+    }
+    if (p.xq) return launch_gemv_a<EPI, GPW, KSPLIT, false, false>(p, tpt, grid, lds, s);
+    return launch_gemv_a<EPI, GPW, KSPLIT, true, false>(p, tpt, grid, lds, s);
 }
 
 template <Epi EPI>
@@ -902,6 +916,10 @@ bool mfma_supported(int64_t K, int64_t group_size) {
 int launch_grouped_scalar(const GroupedArgs& a, hipStream_t s) {
     const Params p = make_params(a);
     if (p.P == 0) return W4A8_OK;
+    if (a.w_frag) {
+        set_error("scalar grouped GEMM reads op-layout weights only");
+        return W4A8_ERR_INVALID;
+    }
     switch (a.epi) {
         case Epi::kHalf: return launch_scalar_t<Epi::kHalf>(p, s);
         case Epi::kSiluHalf: return launch_scalar_t<Epi::kSiluHalf>(p, s);
@@ -914,6 +932,10 @@ int launch_grouped_scalar(const GroupedArgs& a, hipStream_t s) {
 int launch_grouped_mfma(const GroupedArgs& a, hipStream_t s) {
     const Params p = make_params(a);
     if (p.P == 0) return W4A8_OK;
+    if (a.w_frag) {
+        set_error("mfma grouped GEMM reads op-layout weights only");
+        return W4A8_ERR_INVALID;
+    }
     switch (a.epi) {
         case Epi::kHalf: return launch_mfma_e<Epi::kHalf>(p, s);
         case Epi::kSiluHalf: return launch_mfma_e<Epi::kSiluHalf>(p, s);
@@ -936,6 +958,10 @@ int launch_grouped_gemv_tpt(const GroupedArgs& a, int tpt, hipStream_t s) {
     }
     if (a.e2m1) {
         set_error("gemv grouped GEMM: E2M1 weights run on the matrix-core tiles");
+        return W4A8_ERR_INVALID;
+    }
+    if (a.w_frag && (a.N % 16 != 0 || (a.epi == Epi::kSiluHalf && (a.N / 2) % 16 != 0))) {
+        set_error("gemv grouped GEMM: fragment-layout weights need 16-row aligned halves");
         return W4A8_ERR_INVALID;
     }
     switch (a.epi) {

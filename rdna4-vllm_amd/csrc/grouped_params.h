@@ -14,7 +14,7 @@ struct Params {
     const uint8_t* xq;          // (x_rows, K) e4m3, k8-interleaved
     const float* asc;           // (x_rows,)
     const void* xh;             // (x_rows, K) fp16/bf16 rows (fused quantisation path)
-    const int32_t* w;           // (E, N, K/8)
+    const int32_t* w;           // (E, N, K/8), or fragment layout when w_frag
     const __half* scales;       // (E, N, G)
     const int32_t* zeros;       // (E, N/8, G) or null
     const int32_t* sorted_ids;
@@ -29,6 +29,7 @@ struct Params {
     int identity;
     int e2m1;
     int xbf16;                  // xh holds bf16 (else fp16)
+    int w_frag;                 // w in fragment layout (16-row tile, group, lane)
     const float* asum;          // (x_rows, K/128) sums of the e4m3 values per group, or null
 };
 
@@ -68,6 +69,7 @@ inline Params make_params(const GroupedArgs& a) {
     p.e2m1 = a.e2m1 ? 1 : 0;
     p.xbf16 = a.x_bf16 ? 1 : 0;
     p.asum = a.act_group_sums;
+    p.w_frag = a.w_frag ? 1 : 0;
     return p;
 }
 

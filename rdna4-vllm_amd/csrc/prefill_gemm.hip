@@ -69,12 +69,17 @@ __device__ __forceinline__ void pf_store_a(const uint4 (&reg)[A_CHUNKS], uint8_t
 #pragma unroll
     for (int i = 0; i < A_CHUNKS; ++i) *reinterpret_cast<uint4*>(dst + off[i]) = reg[i];
 }
+// FRAG: fragment-layout weights (repack.hip), lane l's 16 bytes of block (row / 16, group)
+// at offset 16 l; otherwise op layout, row wrow, words 16 gg + 4 q.
+template <bool FRAG>
 __device__ __forceinline__ void pf_load_b(uint4 (&w)[kPfNT], uint32_t (&sc)[kPfNT],
                                           const int32_t* __restrict__ we, const uint16_t* __restrict__ se,
-                                          const int (&wrow)[kPfNT], int kw_row, int G, int gg, int q) {
+                                          const int (&wrow)[kPfNT], int kw_row, int G, int gg, int lane) {
 #pragma unroll
     for (int j = 0; j < kPfNT; ++j) {
-        w[j] = *reinterpret_cast<const uint4*>(we + (int64_t)wrow[j] * kw_row + gg * (kGroup / 8) + q * 4);
+        const int32_t* src = FRAG ? we + ((int64_t)(wrow[j] >> 4) * G + gg) * 256 + lane * 4
+                                  : we + (int64_t)wrow[j] * kw_row + gg * (kGroup / 8) + (lane >> 4) * 4;
+        w[j] = *reinterpret_cast<const uint4*>(src);
         sc[j] = se[(int64_t)wrow[j] * G + gg];
     }
 }
@@ -92,7 +97,7 @@ struct PfLds {
     }
 };
 
-template <Epi EPI, int MT>
+template <Epi EPI, int MT, bool FRAG>
 __global__ void __launch_bounds__(256, 1) prefill_mfma_kernel(Params p, int nblocks, int ntiles) {
     constexpr bool kSilu = EPI == Epi::kSiluHalf;
     constexpr int BM = 16 * MT;
@@ -256,8 +261,8 @@ __global__ void __launch_bounds__(256, 1) prefill_mfma_kernel(Params p, int nblo
     // B runs two groups ahead in two register sets (alternating with the group parity; the
     // loop is unrolled by 2); A runs one group ahead: A(g+1) is requested at the top of
     // group g and lands in the other LDS slot at its end.
-    pf_load_b(wv0, sv0, we, se16, wrow, kw_row, G, 0, q);
-    pf_load_b(wv1, sv1, we, se16, wrow, kw_row, G, min(1, Gl), q);
+    pf_load_b<FRAG>(wv0, sv0, we, se16, wrow, kw_row, G, 0, lane);
+    pf_load_b<FRAG>(wv1, sv1, we, se16, wrow, kw_row, G, min(1, Gl), lane);
     {
         uint4 a_reg[A_CHUNKS];
         pf_load_a(a_reg, p.xq, a_src, 0);
@@ -272,7 +277,7 @@ __global__ void __launch_bounds__(256, 1) prefill_mfma_kernel(Params p, int nblo
             float sc[kPfNT];
 #pragma unroll
             for (int j = 0; j < kPfNT; ++j) { bf[j] = spread_nibbles(wv0[j]); sc[j] = half_bits(sv0[j]); }
-            pf_load_b(wv0, sv0, we, se16, wrow, kw_row, G, min(g + 2, Gl), q);
+            pf_load_b<FRAG>(wv0, sv0, we, se16, wrow, kw_row, G, min(g + 2, Gl), lane);
             mma(bf, sc, g);
             pf_store_a(a_reg, slot(g + 1), a_dst);
             lds_barrier();
@@ -288,7 +293,7 @@ __global__ void __launch_bounds__(256, 1) prefill_mfma_kernel(Params p, int nblo
             float sc[kPfNT];
 #pragma unroll
             for (int j = 0; j < kPfNT; ++j) { bf[j] = spread_nibbles(wv1[j]); sc[j] = half_bits(sv1[j]) * live; }
-            pf_load_b(wv1, sv1, we, se16, wrow, kw_row, G, min(g + 3, Gl), q);
+            pf_load_b<FRAG>(wv1, sv1, we, se16, wrow, kw_row, G, min(g + 3, Gl), lane);
             mma(bf, sc, g + 1);
             pf_store_a(a_reg, slot(g + 2), a_dst);
             lds_barrier();
@@ -363,7 +368,7 @@ __global__ void __launch_bounds__(256, 1) prefill_mfma_kernel(Params p, int nblo
     }
 }
 
-template <Epi EPI, int MT>
+template <Epi EPI, int MT, bool FRAG>
 int launch_prefill_t(const Params& p, hipStream_t s) {
     constexpr bool kSilu = EPI == Epi::kSiluHalf;
     const int ncols = kSilu ? p.N / 2 : p.N;
@@ -374,7 +379,7 @@ int launch_prefill_t(const Params& p, hipStream_t s) {
     const PfLds L(16 * MT, (p.G + 15) / 16 * 16);
     static bool attr_set = false;
     if (!attr_set) {   // > 64 KB of dynamic LDS needs an explicit opt-in
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_mfma_kernel<EPI, MT>),
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_mfma_kernel<EPI, MT, FRAG>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize,
                                 PfLds(16 * MT, kPfMaxGroups).total) != hipSuccess) {
             set_error("prefill_mfma_kernel: cannot reserve dynamic LDS");
@@ -382,19 +387,23 @@ int launch_prefill_t(const Params& p, hipStream_t s) {
         }
         attr_set = true;
     }
-    prefill_mfma_kernel<EPI, MT><<<(unsigned)grid, 256, L.total, s>>>(p, nblocks, ntiles);
+    prefill_mfma_kernel<EPI, MT, FRAG><<<(unsigned)grid, 256, L.total, s>>>(p, nblocks, ntiles);
     return check_launch("prefill_mfma_kernel");
 }
 
-template <Epi EPI>
-int launch_prefill_e(const Params& p, hipStream_t s) {
+template <Epi EPI, bool FRAG>
+int launch_prefill_f(const Params& p, hipStream_t s) {
     // the tile height divides block_m so a tile never spans two experts
-    if (p.block_m % 128 == 0) return launch_prefill_t<EPI, 8>(p, s);
-    if (p.block_m % 64 == 0) return launch_prefill_t<EPI, 4>(p, s);
-    if (p.block_m % 32 == 0) return launch_prefill_t<EPI, 2>(p, s);
-    if (p.block_m % 16 == 0) return launch_prefill_t<EPI, 1>(p, s);
+    if (p.block_m % 128 == 0) return launch_prefill_t<EPI, 8, FRAG>(p, s);
+    if (p.block_m % 64 == 0) return launch_prefill_t<EPI, 4, FRAG>(p, s);
+    if (p.block_m % 32 == 0) return launch_prefill_t<EPI, 2, FRAG>(p, s);
+    if (p.block_m % 16 == 0) return launch_prefill_t<EPI, 1, FRAG>(p, s);
     set_error("prefill grouped GEMM: block_m must be a multiple of 16");
     return W4A8_ERR_INVALID;
+}
+template <Epi EPI>
+int launch_prefill_e(const Params& p, hipStream_t s) {
+    return p.w_frag ? launch_prefill_f<EPI, true>(p, s) : launch_prefill_f<EPI, false>(p, s);
 }
 
 }  // namespace
@@ -410,6 +419,10 @@ int launch_grouped_prefill(const GroupedArgs& a, hipStream_t s) {
         a.x_rows * a.K >= ((int64_t)1 << 31)) {
         set_error("prefill grouped GEMM: needs g128 int4 weights, K <= 4096, prequantised rows "
                   "(rows * K < 2^31) and their group sums");
+        return W4A8_ERR_INVALID;
+    }
+    if (a.w_frag && (a.N % 16 != 0 || (a.epi == Epi::kSiluHalf && (a.N / 2) % 16 != 0))) {
+        set_error("prefill grouped GEMM: fragment-layout weights need 16-row aligned halves");
         return W4A8_ERR_INVALID;
     }
     switch (a.epi) {

@@ -93,7 +93,8 @@ struct GroupedArgs {
     bool x_bf16;
     int64_t x_rows;         // rows of x
     int64_t K;
-    const int32_t* w;       // (E, N, K/8)
+    const int32_t* w;       // (E, N, K/8), or fragment layout when w_frag
+    bool w_frag;            // w repacked by launch_repack_fragments (decode GEMV / prefill only)
     const uint16_t* scales; // (E, N, G) fp16 bits
     const int32_t* zeros;   // (E, N/8, G) or null
     int64_t E, N, group_size;
@@ -119,6 +120,11 @@ struct GroupedArgs {
 int launch_grouped_scalar(const GroupedArgs& a, hipStream_t stream);
 int launch_grouped_mfma(const GroupedArgs& a, hipStream_t stream);   // prefill tiles
 int launch_grouped_gemv(const GroupedArgs& a, hipStream_t stream);   // decode GEMV
+// (E, N, K/8) int32 op layout -> fragment layout: per expert, 16-row tile t and 128-wide
+// group g, a 1 KB block whose 16-byte lane l holds row 16t + l % 16, k in
+// [128g + 32 (l / 16), +32) (the MFMA B operand of lane l). N % 16 == 0, K % 128 == 0.
+int launch_repack_fragments(const int32_t* w, int64_t E, int64_t N, int64_t K, int32_t* out,
+                            hipStream_t stream);
 // Prefill tiles with raw-nibble B in registers; needs x_fp8, act_scales and act_group_sums.
 int launch_grouped_prefill(const GroupedArgs& a, hipStream_t stream);
 bool prefill_supported(int64_t K, int64_t group_size, bool e2m1);   // g128, K <= 4096, no E2M1

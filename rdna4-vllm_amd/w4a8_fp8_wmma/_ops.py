@@ -345,21 +345,48 @@ def silu_and_mul(out: torch.Tensor, x: torch.Tensor) -> None:
     check(lib.w4a8_silu_and_mul(_ptr(x), R, I2 // 2, _ptr(out), _stream(x)), "silu_and_mul")
 
 
+def repack_fragments(w_packed: torch.Tensor) -> torch.Tensor:
+    """Op-layout int4 weights (E, N, K/8) int32 -> fragment layout (E, N/16, K/128, 64, 4)
+    int32: block (e, t, g) holds, in lane l's 16 bytes, row 16t + l % 16 and k in
+    [128g + 32 (l // 16), +32), the fp8 MFMA B operand of lane l. Run once at weight load
+    (the reference's process_weights_after_loading, moe_experts.py:1277-1306)."""
+    _check(w_packed.is_cuda and w_packed.dtype == torch.int32 and w_packed.dim() == 3,
+           "w_packed must be CUDA int32 (E, N, K/8)")
+    w = w_packed.contiguous()
+    E, N, K8 = w.shape
+    K = K8 * 8
+    _check(N % 16 == 0 and K % 128 == 0, "fragment layout needs N % 16 == 0 and K % 128 == 0")
+    out = torch.empty((E, N // 16, K // 128, 64, 4), dtype=torch.int32, device=w.device)
+    check(lib.w4a8_repack_int4_fragments(_ptr(w), E, N, K, _ptr(out), _stream(w)),
+          "repack_fragments")
+    return out
+
+
 def moe_apply(x, w13, w2, w13_s, w2_s, w13_z, w2_z, topk_weights, topk_ids, expert_map=None,
               weight_is_e2m1: bool = False) -> torch.Tensor:
     """Whole gated-SiLU MoE layer in one C-ABI call (the _run_grouped_moe composition,
-    moe_experts.py:493-665). x (T, H) fp16/bf16 -> (T, H) same dtype."""
+    moe_experts.py:493-665). x (T, H) fp16/bf16 -> (T, H) same dtype. w13 / w2 are op-layout
+    (E, N, K/8) int32, or both fragment layout from repack_fragments (5-d)."""
     _check(x.is_cuda and x.dtype in (torch.float16, torch.bfloat16) and x.dim() == 2,
            "x must be CUDA fp16/bf16 (T, H)")
     x = x.contiguous()
     T, H = x.shape
-    E, I2, _ = w13.shape
-    inter = I2 // 2
+    frag = w13.dim() == 5
+    _check(w2.dim() == w13.dim(), "w13 and w2 must share a layout")
+    if frag:
+        E, nt13, g13, _, _ = w13.shape
+        inter = nt13 * 16 // 2
+        _check(g13 * 128 == H, "w13 fragments must cover K = H")
+        _check(w2.shape[:3] == (E, H // 16, inter // 128), "w2 fragments must be (E, H/16, I/128, 64, 4)")
+        _check(not weight_is_e2m1, "fragment layout holds int4 weights only")
+    else:
+        E, I2, _ = w13.shape
+        inter = I2 // 2
+        _check(w2.shape == (E, H, inter // 8), f"w2 must be (E, H, inter/8)=({E},{H},{inter // 8})")
     top_k = topk_ids.shape[1]
     gs = H // w13_s.shape[2]
     _check(w13.dtype == torch.int32 and w2.dtype == torch.int32, "weights must be int32")
     _check(w13_s.dtype == torch.float16 and w2_s.dtype == torch.float16, "scales must be fp16")
-    _check(w2.shape == (E, H, inter // 8), f"w2 must be (E, H, inter/8)=({E},{H},{inter // 8})")
     _check(inter // w2_s.shape[2] == gs, "w13 and w2 must share the group size")
     for t in (w13, w2, w13_s, w2_s):
         _check(t.is_cuda and t.is_contiguous(), "weights/scales must be contiguous CUDA")
@@ -370,9 +397,15 @@ def moe_apply(x, w13, w2, w13_s, w2_s, w13_z, w2_z, topk_weights, topk_ids, expe
     emap = None if expert_map is None else expert_map.to(torch.int32).contiguous()
     out = torch.empty_like(x)
     ws = _workspace(lib.w4a8_moe_apply_workspace_size(T, H, inter, E, top_k), x.device)
-    check(lib.w4a8_moe_apply(
-        _ptr(x), 1 if x.dtype == torch.bfloat16 else 0, T, H, inter, E, top_k, gs,
-        _ptr(w13), _ptr(w13_s), _ptr(z13), _ptr(w2), _ptr(w2_s), _ptr(z2), _ptr(tw), _ptr(ids),
-        _ptr(emap), int(bool(weight_is_e2m1)), _ptr(out), ws.data_ptr(), ws.numel(),
-        _stream(x)), "moe_apply")
+    dt = 1 if x.dtype == torch.bfloat16 else 0
+    if frag:
+        check(lib.w4a8_moe_apply_fragments(
+            _ptr(x), dt, T, H, inter, E, top_k, gs, _ptr(w13), _ptr(w13_s), _ptr(z13), _ptr(w2),
+            _ptr(w2_s), _ptr(z2), _ptr(tw), _ptr(ids), _ptr(emap), _ptr(out), ws.data_ptr(),
+            ws.numel(), _stream(x)), "moe_apply")
+    else:
+        check(lib.w4a8_moe_apply(
+            _ptr(x), dt, T, H, inter, E, top_k, gs, _ptr(w13), _ptr(w13_s), _ptr(z13), _ptr(w2),
+            _ptr(w2_s), _ptr(z2), _ptr(tw), _ptr(ids), _ptr(emap), int(bool(weight_is_e2m1)),
+            _ptr(out), ws.data_ptr(), ws.numel(), _stream(x)), "moe_apply")
     return out

@@ -104,6 +104,33 @@ def test_baseline_configs_sampled_tokens(name):
     assert torch.isfinite(out.float()).all()
 
 
+@pytest.mark.parametrize("T,asym", [(1, True), (32, True), (32, False), (97, True), (300, False)])
+def test_fragment_layout_bit_identical(T, asym):
+    """Weights repacked into the fragment layout give the op-layout results bit for bit
+    (decode GEMV and prefill tiles), and the repack equals the oracle permutation."""
+    cfg, ws, x, tw, ids = small_layer(300 + T, T, 16, 512, 256, 4, asym=asym)
+    a = W.moe_apply(x, ws["w13"], ws["w2"], ws["s13"], ws["s2"], ws["z13"], ws["z2"], tw, ids)
+    f13, f2 = W.repack_fragments(ws["w13"]), W.repack_fragments(ws["w2"])
+    assert np.array_equal(f13.cpu().numpy(), O.repack_fragments(ws["w13"].cpu().numpy()))
+    assert np.array_equal(f2.cpu().numpy(), O.repack_fragments(ws["w2"].cpu().numpy()))
+    b = W.moe_apply(x, f13, f2, ws["s13"], ws["s2"], ws["z13"], ws["z2"], tw, ids)
+    assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("name,T", [("c3", None), ("c4", 512)])
+def test_fragment_layout_full_size(name, T):
+    cfg = dict(bench.CONFIGS[name])
+    if T is not None:
+        cfg["T"] = T
+    ws = bench.make_weights(cfg, 555, DEV)
+    x, logits = bench.make_inputs(cfg, 556, DEV)
+    tw, ids = W.fused_topk(None, logits, cfg["k"], True)
+    a = W.moe_apply(x, ws["w13"], ws["w2"], ws["s13"], ws["s2"], ws["z13"], ws["z2"], tw, ids)
+    b = W.moe_apply(x, W.repack_fragments(ws["w13"]), W.repack_fragments(ws["w2"]), ws["s13"],
+                    ws["s2"], ws["z13"], ws["z2"], tw, ids)
+    assert torch.equal(a, b)
+
+
 def test_decode_is_deterministic_and_token_local():
     """Decode schedule: bit-identical reruns; permuting tokens permutes outputs exactly."""
     cfg = dict(bench.CONFIGS["c3"])

@@ -157,3 +157,33 @@ def test_bf16_rounding(bits):
     x = np.array([bits], np.uint32).view(np.float32)
     ref = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
     assert np.array_equal(O.f32_to_bf16_bits(x), ref)
+
+
+@pytest.mark.parametrize("E,N,K", [(1, 16, 128), (2, 32, 256), (3, 48, 384)])
+def test_repack_fragments_bruteforce(E, N, K):
+    """Every nibble of row n, column k sits in block (n // 16, k // 128), lane
+    n % 16 + 16 * ((k % 128) // 32), nibble (k % 32) of that lane's 16 bytes (low nibble
+    first): the fp8 MFMA B operand layout (lane l -> column l % 16, k = 32 (l // 16) + i)."""
+    r = np.random.default_rng(E * 1000 + N + K)
+    nib = r.integers(0, 16, (E, N, K))
+    w = O.pack_nibbles(nib)
+    f = O.repack_fragments(w)
+    assert f.shape == (E, N // 16, K // 128, 64, 4) and f.dtype == np.int32
+    lane_nib = O.unpack_nibbles(f)            # (E, N/16, K/128, 64, 32)
+    for e in range(E):
+        for n in range(N):
+            for k in range(K):
+                lane = n % 16 + 16 * ((k % 128) // 32)
+                assert lane_nib[e, n // 16, k // 128, lane, k % 32] == nib[e, n, k]
+    assert np.array_equal(O.unrepack_fragments(f), w)
+
+
+def test_repack_fragments_is_a_permutation_of_words():
+    r = np.random.default_rng(7)
+    w = r.integers(-2**31, 2**31, (4, 64, 512 // 8), dtype=np.int64).astype(np.int32)
+    f = O.repack_fragments(w)
+    assert np.array_equal(np.sort(f.ravel()), np.sort(w.ravel()))
+    # a planted transposition of lane halves is caught by the inverse
+    bad = f.copy()
+    bad[..., [0, 16], :] = bad[..., [16, 0], :]
+    assert not np.array_equal(O.unrepack_fragments(bad), w)
