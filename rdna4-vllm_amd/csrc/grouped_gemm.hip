@@ -504,10 +504,14 @@ __global__ void __launch_bounds__(256, 2) grouped_gemv_kernel(Params p, int tpt)
                 FRAG ? we + (live ? ((int64_t)(n >> 4) * p.G + g) * 256 + lane * 4 : 0)
                      : we + (live ? (int64_t)n * kw_row + g * (kGroup / 8) + q * 4 : 0);
             constexpr int ustep = FRAG ? 256 : kGroup / 8;
+            // fragment layout: whole 128-byte lines per instruction, streamed (non-temporal,
+            // read once per launch); op layout: 64-byte row pieces whose second half the
+            // next instruction reads, so they stay cached
 #pragma unroll
             for (int u = 0; u < C::GC; ++u)
                 wv[b][u * C::FR + f] =
-                    *reinterpret_cast<const uint4*>(wr + (live ? u * ustep : 0));
+                    FRAG ? load_stream16(wr + (live ? u * ustep : 0))
+                         : *reinterpret_cast<const uint4*>(wr + (live ? u * ustep : 0));
             if constexpr (!C::kStagedSZ) {
                 load_scales<C::GC>(se + (int64_t)n * p.G + g, sw[b][f]);
                 // symmetric weights load (and ignore) scale words instead: same load count
