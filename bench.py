@@ -200,10 +200,10 @@ def main():
     torch.cuda.synchronize()
 
     def step(i):
+        # router (softmax / top-8 / renormalise) + the whole expert path, one C-ABI call
         ws = sets[i % R]
-        tw, ids = W.fused_topk(None, logits, k, True)
-        return W.moe_apply(x, ws["w13"], ws["w2"], ws["s13"], ws["s2"], ws["z13"], ws["z2"],
-                           tw, ids), tw, ids
+        return W.moe_forward(x, logits, k, ws["w13"], ws["w2"], ws["s13"], ws["s2"], ws["z13"],
+                             ws["z2"])
 
     out0, tw0, ids0 = step(0)
     for i in range(args.warmup):

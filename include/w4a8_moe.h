@@ -215,6 +215,26 @@ W4A8_API int w4a8_moe_apply_fragments(const void* x, int x_dtype, int64_t T, int
                                       const int32_t* expert_map, void* out, void* workspace,
                                       size_t workspace_bytes, void* stream);
 
+/* Weight layouts for w4a8_moe_forward. */
+#define W4A8_WEIGHTS_OP 0          /* (E, N, K/8) int32, the reference op layout */
+#define W4A8_WEIGHTS_FRAGMENTS 1   /* w4a8_repack_int4_fragments output */
+
+/* Router + expert path in one call: softmax / top-k / renormalise of router_logits (T, E)
+ * fp32 (the vLLM fused_topk the reference's caller runs before apply; ties go to the lower
+ * expert id), then w4a8_moe_apply (op layout) or w4a8_moe_apply_fragments on the result.
+ * topk_weights (T, top_k) fp32 and topk_ids (T, top_k) int32 are outputs. Same workspace
+ * size as w4a8_moe_apply. At decode sizes the router runs inside the first launch of the
+ * layer. No single reference counterpart (fused_topk is vLLM's, moe_experts.py:493-665 the
+ * rest). */
+W4A8_API int w4a8_moe_forward(const void* x, int x_dtype, int64_t T, int64_t H, int64_t inter,
+                              int64_t E, int64_t top_k, int64_t group_size,
+                              const float* router_logits, int renormalize, const int32_t* w13,
+                              const void* w13_scales_f16, const int32_t* w13_zeros,
+                              const int32_t* w2, const void* w2_scales_f16,
+                              const int32_t* w2_zeros, int weights_layout,
+                              const int32_t* expert_map, float* topk_weights, int32_t* topk_ids,
+                              void* out, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Optional per-stage timing of w4a8_moe_apply on the calling thread: when count == 8,
  * the next w4a8_moe_apply calls record events[0] before the first launch and events[i]
  * after stage i (1 align, 2 act-quant x, 3 reserved (empty), 4 gemm1+SiLU, 5 act-quant

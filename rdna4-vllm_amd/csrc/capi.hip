@@ -186,13 +186,16 @@ using namespace w4a8;
 namespace w4a8 {
 // frag: w13 / w2 in the fragment layout (launch_repack_fragments); only the GEMV and the
 // prefill tiles read it, so every other schedule is refused up front.
+// logits: when given, the router runs first and topk_weights / topk_ids are its outputs
+// (the decode schedule folds it into the prologue launch).
 int moe_apply_impl(const void* x, int x_dtype, int64_t T, int64_t H, int64_t inter, int64_t E,
                    int64_t top_k, int64_t group_size, const int32_t* w13,
                    const void* w13_scales_f16, const int32_t* w13_zeros, const int32_t* w2,
                    const void* w2_scales_f16, const int32_t* w2_zeros,
                    const float* topk_weights, const int32_t* topk_ids,
                    const int32_t* expert_map, int weight_is_e2m1, void* out, void* workspace,
-                   size_t workspace_bytes, void* stream, bool frag) {
+                   size_t workspace_bytes, void* stream, bool frag,
+                   const float* logits = nullptr, bool renormalize = true) {
     W4A8_REQUIRE(x_dtype == W4A8_DTYPE_F16 || x_dtype == W4A8_DTYPE_BF16, "x dtype must be fp16 or bf16");
     W4A8_REQUIRE(T >= 0 && H > 0 && inter > 0 && E > 0 && top_k > 0, "moe_apply: invalid sizes");
     W4A8_REQUIRE(group_size > 0 && H % group_size == 0 && inter % group_size == 0 &&
@@ -230,13 +233,27 @@ int moe_apply_impl(const void* x, int x_dtype, int64_t T, int64_t H, int64_t int
     const bool pf1 = !pl.decode && mfma && prefill_supported(H, group_size, e2m1);
     const bool pf2 = !pl.decode && mfma && prefill_supported(inter, group_size, e2m1);
     stage_mark(0, s);
-    if (pl.decode && numel <= kAlignSmallMax) {
+    if (logits != nullptr && pl.decode && numel <= kAlignSmallMax) {
+        // one launch: router and align in work-group 0, act-quant of x in the others
+        if (int rc = launch_route_align_quant(logits, T, E, top_k, renormalize,
+                                              const_cast<float*>(topk_weights),
+                                              const_cast<int32_t*>(topk_ids), pl.block_m,
+                                              expert_map, sti, pl.P, eid, ntp, x, bf16, H, xq,
+                                              s1, s))
+            return rc;
+        stage_mark(1, s);
+    } else if (pl.decode && numel <= kAlignSmallMax) {
         // one launch: align in work-group 0, act-quant of x in the others
         if (int rc = launch_align_quant(topk_ids, numel, E, pl.block_m, expert_map, sti, pl.P,
                                         eid, ntp, s2r, x, bf16, T, H, xq, s1, nullptr, s))
             return rc;
         stage_mark(1, s);
     } else {
+        if (logits != nullptr)
+            if (int rc = launch_topk_softmax(logits, T, E, top_k, renormalize,
+                                             const_cast<float*>(topk_weights),
+                                             const_cast<int32_t*>(topk_ids), s))
+                return rc;
         if (int rc = launch_align(topk_ids, numel, E, pl.block_m, expert_map, sti, pl.P, eid,
                                   ntp, aws, abytes, s, s2r))
             return rc;
@@ -566,6 +583,24 @@ int w4a8_moe_apply_fragments(const void* x, int x_dtype, int64_t T, int64_t H, i
                           w13_scales_f16, w13_zeros, w2_frag, w2_scales_f16, w2_zeros,
                           topk_weights, topk_ids, expert_map, 0, out, workspace, workspace_bytes,
                           stream, true);
+}
+
+int w4a8_moe_forward(const void* x, int x_dtype, int64_t T, int64_t H, int64_t inter, int64_t E,
+                     int64_t top_k, int64_t group_size, const float* router_logits,
+                     int renormalize, const int32_t* w13, const void* w13_scales_f16,
+                     const int32_t* w13_zeros, const int32_t* w2, const void* w2_scales_f16,
+                     const int32_t* w2_zeros, int weights_layout, const int32_t* expert_map,
+                     float* topk_weights, int32_t* topk_ids, void* out, void* workspace,
+                     size_t workspace_bytes, void* stream) {
+    clear_error();
+    W4A8_REQUIRE(weights_layout == W4A8_WEIGHTS_OP || weights_layout == W4A8_WEIGHTS_FRAGMENTS,
+                 "moe_forward: weights_layout must be W4A8_WEIGHTS_OP or W4A8_WEIGHTS_FRAGMENTS");
+    W4A8_REQUIRE(T == 0 || (router_logits && topk_weights && topk_ids), "moe_forward: null pointer");
+    return moe_apply_impl(x, x_dtype, T, H, inter, E, top_k, group_size, w13, w13_scales_f16,
+                          w13_zeros, w2, w2_scales_f16, w2_zeros, topk_weights, topk_ids,
+                          expert_map, 0, out, workspace, workspace_bytes, stream,
+                          weights_layout == W4A8_WEIGHTS_FRAGMENTS, router_logits,
+                          renormalize != 0);
 }
 
 int w4a8_repack_int4_fragments(const int32_t* w_packed, int64_t E, int64_t N, int64_t K,

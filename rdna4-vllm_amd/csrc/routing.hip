@@ -213,37 +213,93 @@ constexpr int kRouterMaxPerLane = 16;   // E <= 1024
 
 // NV = logits per lane (E <= 64 * NV). Loads are unconditional (clamped index, the
 // out-of-range entries masked to -inf afterwards) so they issue together.
-// (value desc, expert asc) maximum over the wave; every lane gets it.
-__device__ __forceinline__ void argmax_pick(float& bv, int& be, float ov, int oe) {
-    if (ov > bv || (ov == bv && oe < be)) {
-        bv = ov;
-        be = oe;
-    }
+// Selection key: a larger key is a larger logit, equal logits order by the lower expert id
+// (the router's tie-break). Entries past E get key 0, below every real entry.
+__device__ __forceinline__ uint64_t topk_key(float v, int e) {
+    uint32_t b = __float_as_uint(v);
+    b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);   // order-preserving float -> uint
+    return ((uint64_t)b << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)e);
+}
+__device__ __forceinline__ float topk_key_value(uint64_t key) {
+    uint32_t b = (uint32_t)(key >> 32);
+    b = (b & 0x80000000u) ? (b & 0x7FFFFFFFu) : ~b;
+    return __uint_as_float(b);
+}
+__device__ __forceinline__ int topk_key_expert(uint64_t key) {
+    return (int)(0xFFFFFFFFu - (uint32_t)key);
 }
 template <int S>
-__device__ __forceinline__ void argmax_dpp(float& bv, int& be) {
-    const float ov = __uint_as_float(dpp_step<S>(__float_as_uint(bv)));
-    const int oe = (int)dpp_step<S>((uint32_t)be);
-    argmax_pick(bv, be, ov, oe);
+__device__ __forceinline__ uint64_t key_max_dpp(uint64_t k) {
+    const uint32_t lo = dpp_step<S>((uint32_t)k), hi = dpp_step<S>((uint32_t)(k >> 32));
+    const uint64_t o = ((uint64_t)hi << 32) | lo;
+    return o > k ? o : k;
 }
-__device__ __forceinline__ void wave_argmax(float& bv, int& be) {
-    argmax_dpp<0>(bv, be);
-    argmax_dpp<1>(bv, be);
-    argmax_dpp<2>(bv, be);
-    argmax_dpp<3>(bv, be);
+// maximum key over the wave, every lane gets it (branch-free compare-selects)
+__device__ __forceinline__ uint64_t wave_max_key(uint64_t k) {
+    k = key_max_dpp<0>(k);
+    k = key_max_dpp<1>(k);
+    k = key_max_dpp<2>(k);
+    k = key_max_dpp<3>(k);
     {
-        const auto rv = __builtin_amdgcn_permlane16_swap(__float_as_uint(bv), __float_as_uint(bv), false, false);
-        const auto re = __builtin_amdgcn_permlane16_swap((uint32_t)be, (uint32_t)be, false, false);
-        bv = __uint_as_float(rv[0]);
-        be = (int)re[0];
-        argmax_pick(bv, be, __uint_as_float(rv[1]), (int)re[1]);
+        const auto lo = __builtin_amdgcn_permlane16_swap((uint32_t)k, (uint32_t)k, false, false);
+        const auto hi = __builtin_amdgcn_permlane16_swap((uint32_t)(k >> 32), (uint32_t)(k >> 32), false, false);
+        const uint64_t a = ((uint64_t)hi[0] << 32) | lo[0], b = ((uint64_t)hi[1] << 32) | lo[1];
+        k = a > b ? a : b;
     }
     {
-        const auto rv = __builtin_amdgcn_permlane32_swap(__float_as_uint(bv), __float_as_uint(bv), false, false);
-        const auto re = __builtin_amdgcn_permlane32_swap((uint32_t)be, (uint32_t)be, false, false);
-        bv = __uint_as_float(rv[0]);
-        be = (int)re[0];
-        argmax_pick(bv, be, __uint_as_float(rv[1]), (int)re[1]);
+        const auto lo = __builtin_amdgcn_permlane32_swap((uint32_t)k, (uint32_t)k, false, false);
+        const auto hi = __builtin_amdgcn_permlane32_swap((uint32_t)(k >> 32), (uint32_t)(k >> 32), false, false);
+        const uint64_t a = ((uint64_t)hi[0] << 32) | lo[0], b = ((uint64_t)hi[1] << 32) | lo[1];
+        k = a > b ? a : b;
+    }
+    return k;
+}
+
+// Softmax + top-k of one token's logits row l (E <= 64 * NV) by one wave: lane j < top_k
+// writes pick j (weight, expert) to tw[j] / ids[j] and, if ids_lds is given, the expert to
+// ids_lds[j] too. Picks are made on the logits (exact ids); the weights are
+// exp(l - max) / sum exp(l - max), renormalised over the picks in pick order.
+template <int NV>
+__device__ __forceinline__ void topk_one_token(const float* __restrict__ l, int E, int top_k,
+                                               bool renorm, float* __restrict__ tw,
+                                               int32_t* __restrict__ ids, int32_t* ids_lds,
+                                               int lane) {
+    float v[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) v[i] = l[min(lane + 64 * i, E - 1)];
+    float m = -INFINITY;
+    uint64_t key[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const bool in = lane + 64 * i < E;
+        if (!in) v[i] = -INFINITY;
+        m = fmaxf(m, v[i]);
+        key[i] = in ? topk_key(v[i], lane + 64 * i) : 0ull;
+    }
+    m = wave_max(m);
+    float ssum = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) ssum += lane + 64 * i < E ? expf(v[i] - m) : 0.f;
+    ssum = wave_sum(ssum);
+    uint64_t mine = 0;   // lane j < top_k: key of pick j
+    for (int j = 0; j < top_k; ++j) {
+        uint64_t best = 0;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) best = key[i] > best ? key[i] : best;
+        best = wave_max_key(best);
+#pragma unroll
+        for (int i = 0; i < NV; ++i) key[i] = key[i] == best ? 0ull : key[i];   // taken
+        mine = lane == j ? best : mine;
+    }
+    const float p = expf(topk_key_value(mine) - m) / ssum;
+    float sum_sel = 0.f;   // picks in order, as a sequential sum
+    for (int j = 0; j < top_k; ++j)
+        sum_sel += __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(p), j));
+    if (lane < top_k) {
+        const int e = topk_key_expert(mine);
+        tw[lane] = renorm ? p / sum_sel : p;
+        ids[lane] = e;
+        if (ids_lds != nullptr) ids_lds[lane] = e;
     }
 }
 
@@ -254,47 +310,8 @@ __global__ void __launch_bounds__(256) topk_softmax_kernel(
     const int lane = threadIdx.x & 63;
     const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (t >= T) return;
-    const float* l = logits + t * E;
-    float v[NV];
-#pragma unroll
-    for (int i = 0; i < NV; ++i) v[i] = l[min(lane + 64 * i, E - 1)];
-    float m = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < NV; ++i) {
-        if (lane + 64 * i >= E) v[i] = -INFINITY;
-        m = fmaxf(m, v[i]);
-    }
-    m = wave_max(m);
-    float ssum = 0.f;
-#pragma unroll
-    for (int i = 0; i < NV; ++i) ssum += lane + 64 * i < E ? expf(v[i] - m) : 0.f;
-    ssum = wave_sum(ssum);
-    uint32_t taken = 0;   // bit i: v[i] already selected
-    float wsel = 0.f;     // this lane's output weight (lane j < top_k holds pick j)
-    int isel = 0;
-    float sum_sel = 0.f;
-    for (int j = 0; j < top_k; ++j) {
-        // best (value desc, expert asc) among this lane's untaken entries
-        float bv = -INFINITY;
-        int be = 0x7FFFFFFF;
-#pragma unroll
-        for (int i = 0; i < NV; ++i) {
-            const int e = lane + 64 * i;
-            if (e < E && !(taken & (1u << i)) && (v[i] > bv || (v[i] == bv && e < be))) {
-                bv = v[i];
-                be = e;
-            }
-        }
-        wave_argmax(bv, be);
-        if ((be & 63) == lane) taken |= 1u << (be >> 6);
-        const float p = expf(bv - m) / ssum;
-        sum_sel += p;
-        if (lane == j) { wsel = p; isel = be; }
-    }
-    if (lane < top_k) {
-        tw[t * top_k + lane] = renorm ? wsel / sum_sel : wsel;
-        tids[t * top_k + lane] = isel;
-    }
+    topk_one_token<NV>(logits + t * E, E, top_k, renorm, tw + t * top_k, tids + t * top_k,
+                       nullptr, lane);
 }
 
 // Decode prologue in one launch: work-group 0 builds the align layout (numel <= kChunk),
@@ -313,6 +330,31 @@ __global__ void __launch_bounds__(kAlignThreads) align_quant_kernel(
     }
     align_small_body(ids, numel, E, block_m, emap, sorted_ids, sorted_len, expert_ids, ntp,
                      slot_to_row);
+}
+
+// Decode prologue with the router in one launch (T * top_k <= kChunk): work-group 0 runs
+// the softmax/top-k of every token (one wave per token, ids kept in LDS) and then the
+// single-work-group align on them; work-groups 1.. quantise 16 rows of x each.
+template <bool BF16, int NV>
+__global__ void __launch_bounds__(kAlignThreads) route_align_quant_kernel(
+    const float* __restrict__ logits, int64_t T, int E, int top_k, bool renorm,
+    float* __restrict__ tw, int32_t* __restrict__ tids, int64_t block_m,
+    const int32_t* __restrict__ emap, int32_t* __restrict__ sorted_ids, int64_t sorted_len,
+    int32_t* __restrict__ expert_ids, int32_t* __restrict__ ntp, const void* __restrict__ x,
+    int K, uint8_t* __restrict__ xq, float* __restrict__ xs) {
+    if (blockIdx.x > 0) {
+        const int64_t row = (int64_t)(blockIdx.x - 1) * (kAlignThreads / 64) + (threadIdx.x >> 6);
+        if (row < T) quantize_row<BF16>(x, row, K, xq, xs, true, nullptr, threadIdx.x & 63);
+        return;
+    }
+    __shared__ int32_t s_ids[kChunk];
+    const int lane = threadIdx.x & 63;
+    for (int64_t t = threadIdx.x >> 6; t < T; t += kAlignThreads / 64)
+        topk_one_token<NV>(logits + t * E, E, top_k, renorm, tw + t * top_k, tids + t * top_k,
+                           s_ids + t * top_k, lane);
+    __syncthreads();
+    align_small_body(s_ids, T * top_k, E, block_m, emap, sorted_ids, sorted_len, expert_ids, ntp,
+                     nullptr);
 }
 
 }  // namespace
@@ -375,6 +417,39 @@ int launch_topk_softmax(const float* logits, int64_t T, int64_t E, int64_t top_k
     else if (E <= 512) topk_softmax_kernel<8><<<grid, 256, 0, stream>>>(logits, T, (int)E, (int)top_k, renorm, w, ids);
     else topk_softmax_kernel<16><<<grid, 256, 0, stream>>>(logits, T, (int)E, (int)top_k, renorm, w, ids);
     return check_launch("topk_softmax_kernel");
+}
+
+int launch_route_align_quant(const float* logits, int64_t T, int64_t E, int64_t top_k,
+                             bool renorm, float* tw, int32_t* ids, int64_t block_m,
+                             const int32_t* emap, int32_t* sorted_ids, int64_t sorted_len,
+                             int32_t* expert_ids, int32_t* ntp, const void* x, bool x_bf16,
+                             int64_t K, uint8_t* xq, float* xs, hipStream_t stream) {
+    if (E > 64 * kRouterMaxPerLane || top_k > 64 || top_k > E || T * top_k > kChunk ||
+        E > kMaxExperts) {
+        set_error("route_align_quant: needs E <= 1024, top_k <= min(64, E), T * top_k <= 1024");
+        return W4A8_ERR_INVALID;
+    }
+    if (T == 0) return W4A8_OK;
+    const unsigned grid = 1u + (unsigned)((T + kAlignThreads / 64 - 1) / (kAlignThreads / 64));
+#define W4A8_RAQ(BF, NV)                                                                        \
+    route_align_quant_kernel<BF, NV><<<grid, kAlignThreads, 0, stream>>>(                       \
+        logits, T, (int)E, (int)top_k, renorm, tw, ids, block_m, emap, sorted_ids, sorted_len,  \
+        expert_ids, ntp, x, (int)K, xq, xs)
+    const int nv = E <= 64 ? 1 : E <= 128 ? 2 : E <= 256 ? 4 : E <= 512 ? 8 : 16;
+    switch (nv * 2 + (x_bf16 ? 1 : 0)) {
+        case 2: W4A8_RAQ(false, 1); break;
+        case 3: W4A8_RAQ(true, 1); break;
+        case 4: W4A8_RAQ(false, 2); break;
+        case 5: W4A8_RAQ(true, 2); break;
+        case 8: W4A8_RAQ(false, 4); break;
+        case 9: W4A8_RAQ(true, 4); break;
+        case 16: W4A8_RAQ(false, 8); break;
+        case 17: W4A8_RAQ(true, 8); break;
+        case 32: W4A8_RAQ(false, 16); break;
+        default: W4A8_RAQ(true, 16); break;
+    }
+#undef W4A8_RAQ
+    return check_launch("route_align_quant_kernel");
 }
 
 int launch_align_quant(const int32_t* ids, int64_t numel, int64_t E, int64_t block_m,

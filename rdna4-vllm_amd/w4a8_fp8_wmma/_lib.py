@@ -56,6 +56,10 @@ SIGNATURES = {
                               _c_void_p, _c_void_p, _int, _c_void_p, _c_void_p, _size,
                               _c_void_p]),
     "w4a8_repack_int4_fragments": (_int, [_c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p]),
+    "w4a8_moe_forward": (_int, [_c_void_p, _int, _i64, _i64, _i64, _i64, _i64, _i64, _c_void_p,
+                                _int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                _c_void_p, _int, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                _c_void_p, _size, _c_void_p]),
     "w4a8_moe_apply_fragments": (_int, [_c_void_p, _int, _i64, _i64, _i64, _i64, _i64, _i64,
                                         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,

@@ -362,14 +362,10 @@ def repack_fragments(w_packed: torch.Tensor) -> torch.Tensor:
     return out
 
 
-def moe_apply(x, w13, w2, w13_s, w2_s, w13_z, w2_z, topk_weights, topk_ids, expert_map=None,
-              weight_is_e2m1: bool = False) -> torch.Tensor:
-    """Whole gated-SiLU MoE layer in one C-ABI call (the _run_grouped_moe composition,
-    moe_experts.py:493-665). x (T, H) fp16/bf16 -> (T, H) same dtype. w13 / w2 are op-layout
-    (E, N, K/8) int32, or both fragment layout from repack_fragments (5-d)."""
+def _layer_args(x, w13, w2, w13_s, w2_s, w13_z, w2_z, top_k, weight_is_e2m1):
+    """Shared validation of the whole-layer entry points; returns the size and pointer pack."""
     _check(x.is_cuda and x.dtype in (torch.float16, torch.bfloat16) and x.dim() == 2,
            "x must be CUDA fp16/bf16 (T, H)")
-    x = x.contiguous()
     T, H = x.shape
     frag = w13.dim() == 5
     _check(w2.dim() == w13.dim(), "w13 and w2 must share a layout")
@@ -383,7 +379,6 @@ def moe_apply(x, w13, w2, w13_s, w2_s, w13_z, w2_z, topk_weights, topk_ids, expe
         E, I2, _ = w13.shape
         inter = I2 // 2
         _check(w2.shape == (E, H, inter // 8), f"w2 must be (E, H, inter/8)=({E},{H},{inter // 8})")
-    top_k = topk_ids.shape[1]
     gs = H // w13_s.shape[2]
     _check(w13.dtype == torch.int32 and w2.dtype == torch.int32, "weights must be int32")
     _check(w13_s.dtype == torch.float16 and w2_s.dtype == torch.float16, "scales must be fp16")
@@ -392,11 +387,23 @@ def moe_apply(x, w13, w2, w13_s, w2_s, w13_z, w2_z, topk_weights, topk_ids, expe
         _check(t.is_cuda and t.is_contiguous(), "weights/scales must be contiguous CUDA")
     z13 = None if w13_z is None or w13_z.numel() == 0 else w13_z.contiguous()
     z2 = None if w2_z is None or w2_z.numel() == 0 else w2_z.contiguous()
+    ws = _workspace(lib.w4a8_moe_apply_workspace_size(T, H, inter, E, top_k), x.device)
+    return T, H, inter, E, gs, frag, z13, z2, ws
+
+
+def moe_apply(x, w13, w2, w13_s, w2_s, w13_z, w2_z, topk_weights, topk_ids, expert_map=None,
+              weight_is_e2m1: bool = False) -> torch.Tensor:
+    """Whole gated-SiLU MoE layer in one C-ABI call (the _run_grouped_moe composition,
+    moe_experts.py:493-665). x (T, H) fp16/bf16 -> (T, H) same dtype. w13 / w2 are op-layout
+    (E, N, K/8) int32, or both fragment layout from repack_fragments (5-d)."""
+    x = x.contiguous()
+    top_k = topk_ids.shape[1]
+    T, H, inter, E, gs, frag, z13, z2, ws = _layer_args(x, w13, w2, w13_s, w2_s, w13_z, w2_z,
+                                                        top_k, weight_is_e2m1)
     tw = topk_weights.to(torch.float32).contiguous()
     ids = topk_ids.to(torch.int32).contiguous()
     emap = None if expert_map is None else expert_map.to(torch.int32).contiguous()
     out = torch.empty_like(x)
-    ws = _workspace(lib.w4a8_moe_apply_workspace_size(T, H, inter, E, top_k), x.device)
     dt = 1 if x.dtype == torch.bfloat16 else 0
     if frag:
         check(lib.w4a8_moe_apply_fragments(
@@ -409,3 +416,25 @@ def moe_apply(x, w13, w2, w13_s, w2_s, w13_z, w2_z, topk_weights, topk_ids, expe
             _ptr(w2_s), _ptr(z2), _ptr(tw), _ptr(ids), _ptr(emap), int(bool(weight_is_e2m1)),
             _ptr(out), ws.data_ptr(), ws.numel(), _stream(x)), "moe_apply")
     return out
+
+
+def moe_forward(x, router_logits, top_k: int, w13, w2, w13_s, w2_s, w13_z, w2_z,
+                renormalize: bool = True, expert_map=None):
+    """Router (softmax / top-k / renormalise, the vLLM fused_topk contract) plus the expert
+    path in one C-ABI call; at decode sizes the router shares the layer's first launch.
+    Returns (out (T, H) in x.dtype, topk_weights (T, k) fp32, topk_ids (T, k) int32)."""
+    x = x.contiguous()
+    T, H, inter, E, gs, frag, z13, z2, ws = _layer_args(x, w13, w2, w13_s, w2_s, w13_z, w2_z,
+                                                        top_k, False)
+    lg = router_logits.to(torch.float32).contiguous()
+    _check(lg.shape == (T, E), f"router_logits must be (T, E)=({T},{E})")
+    emap = None if expert_map is None else expert_map.to(torch.int32).contiguous()
+    out = torch.empty_like(x)
+    tw = torch.empty((T, top_k), dtype=torch.float32, device=x.device)
+    ids = torch.empty((T, top_k), dtype=torch.int32, device=x.device)
+    check(lib.w4a8_moe_forward(
+        _ptr(x), 1 if x.dtype == torch.bfloat16 else 0, T, H, inter, E, top_k, gs, _ptr(lg),
+        int(bool(renormalize)), _ptr(w13), _ptr(w13_s), _ptr(z13), _ptr(w2), _ptr(w2_s),
+        _ptr(z2), 1 if frag else 0, _ptr(emap), _ptr(tw), _ptr(ids), _ptr(out), ws.data_ptr(),
+        ws.numel(), _stream(x)), "moe_forward")
+    return out, tw, ids

@@ -131,6 +131,25 @@ def test_fragment_layout_full_size(name, T):
     assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("T,frag", [(1, True), (32, True), (32, False), (96, True), (300, True)])
+def test_moe_forward_equals_router_then_apply(T, frag):
+    """The router folded into the layer's first launch gives the fused_topk ids / weights
+    and the moe_apply output bit for bit."""
+    cfg = dict(T=T, H=512, E=64, k=8, I=256, g=128, routing="uniform")
+    ws = bench.make_weights(cfg, 700 + T, DEV)
+    x, logits = bench.make_inputs(cfg, 701 + T, DEV)
+    x = x.to(torch.bfloat16)
+    w13, w2 = ws["w13"], ws["w2"]
+    if frag:
+        w13, w2 = W.repack_fragments(w13), W.repack_fragments(w2)
+    tw, ids = W.fused_topk(None, logits, cfg["k"], True)
+    a = W.moe_apply(x, w13, w2, ws["s13"], ws["s2"], ws["z13"], ws["z2"], tw, ids)
+    b, tw2, ids2 = W.moe_forward(x, logits, cfg["k"], w13, w2, ws["s13"], ws["s2"], ws["z13"],
+                                 ws["z2"])
+    assert torch.equal(ids2, ids.to(torch.int32)) and torch.equal(tw2, tw)
+    assert torch.equal(a, b)
+
+
 def test_decode_is_deterministic_and_token_local():
     """Decode schedule: bit-identical reruns; permuting tokens permutes outputs exactly."""
     cfg = dict(bench.CONFIGS["c3"])
