@@ -223,8 +223,7 @@ W4A8_API int w4a8_moe_apply_fragments(const void* x, int x_dtype, int64_t T, int
  * fp32 (the vLLM fused_topk the reference's caller runs before apply; ties go to the lower
  * expert id), then w4a8_moe_apply (op layout) or w4a8_moe_apply_fragments on the result.
  * topk_weights (T, top_k) fp32 and topk_ids (T, top_k) int32 are outputs. Same workspace
- * size as w4a8_moe_apply. At decode sizes the router runs inside the first launch of the
- * layer. No single reference counterpart (fused_topk is vLLM's, moe_experts.py:493-665 the
+ * size as w4a8_moe_apply. No single reference counterpart (fused_topk is vLLM's, moe_experts.py:493-665 the
  * rest). */
 W4A8_API int w4a8_moe_forward(const void* x, int x_dtype, int64_t T, int64_t H, int64_t inter,
                               int64_t E, int64_t top_k, int64_t group_size,

@@ -232,28 +232,21 @@ int moe_apply_impl(const void* x, int x_dtype, int64_t T, int64_t H, int64_t int
     // prefill tiles need the per-group sums of the quantised rows (zero-point term)
     const bool pf1 = !pl.decode && mfma && prefill_supported(H, group_size, e2m1);
     const bool pf2 = !pl.decode && mfma && prefill_supported(inter, group_size, e2m1);
-    stage_mark(0, s);
-    if (logits != nullptr && pl.decode && numel <= kAlignSmallMax) {
-        // one launch: router and align in work-group 0, act-quant of x in the others
-        if (int rc = launch_route_align_quant(logits, T, E, top_k, renormalize,
-                                              const_cast<float*>(topk_weights),
-                                              const_cast<int32_t*>(topk_ids), pl.block_m,
-                                              expert_map, sti, pl.P, eid, ntp, x, bf16, H, xq,
-                                              s1, s))
+    // router: one wave per token over the whole grid (folding it into the align launch
+    // would serialise the tokens on the align work-group)
+    if (logits != nullptr)
+        if (int rc = launch_topk_softmax(logits, T, E, top_k, renormalize,
+                                         const_cast<float*>(topk_weights),
+                                         const_cast<int32_t*>(topk_ids), s))
             return rc;
-        stage_mark(1, s);
-    } else if (pl.decode && numel <= kAlignSmallMax) {
+    stage_mark(0, s);
+    if (pl.decode && numel <= kAlignSmallMax) {
         // one launch: align in work-group 0, act-quant of x in the others
         if (int rc = launch_align_quant(topk_ids, numel, E, pl.block_m, expert_map, sti, pl.P,
                                         eid, ntp, s2r, x, bf16, T, H, xq, s1, nullptr, s))
             return rc;
         stage_mark(1, s);
     } else {
-        if (logits != nullptr)
-            if (int rc = launch_topk_softmax(logits, T, E, top_k, renormalize,
-                                             const_cast<float*>(topk_weights),
-                                             const_cast<int32_t*>(topk_ids), s))
-                return rc;
         if (int rc = launch_align(topk_ids, numel, E, pl.block_m, expert_map, sti, pl.P, eid,
                                   ntp, aws, abytes, s, s2r))
             return rc;

@@ -332,30 +332,6 @@ __global__ void __launch_bounds__(kAlignThreads) align_quant_kernel(
                      slot_to_row);
 }
 
-// Decode prologue with the router in one launch (T * top_k <= kChunk): work-group 0 runs
-// the softmax/top-k of every token (one wave per token, ids kept in LDS) and then the
-// single-work-group align on them; work-groups 1.. quantise 16 rows of x each.
-template <bool BF16, int NV>
-__global__ void __launch_bounds__(kAlignThreads) route_align_quant_kernel(
-    const float* __restrict__ logits, int64_t T, int E, int top_k, bool renorm,
-    float* __restrict__ tw, int32_t* __restrict__ tids, int64_t block_m,
-    const int32_t* __restrict__ emap, int32_t* __restrict__ sorted_ids, int64_t sorted_len,
-    int32_t* __restrict__ expert_ids, int32_t* __restrict__ ntp, const void* __restrict__ x,
-    int K, uint8_t* __restrict__ xq, float* __restrict__ xs) {
-    if (blockIdx.x > 0) {
-        const int64_t row = (int64_t)(blockIdx.x - 1) * (kAlignThreads / 64) + (threadIdx.x >> 6);
-        if (row < T) quantize_row<BF16>(x, row, K, xq, xs, true, nullptr, threadIdx.x & 63);
-        return;
-    }
-    __shared__ int32_t s_ids[kChunk];
-    const int lane = threadIdx.x & 63;
-    for (int64_t t = threadIdx.x >> 6; t < T; t += kAlignThreads / 64)
-        topk_one_token<NV>(logits + t * E, E, top_k, renorm, tw + t * top_k, tids + t * top_k,
-                           s_ids + t * top_k, lane);
-    __syncthreads();
-    align_small_body(s_ids, T * top_k, E, block_m, emap, sorted_ids, sorted_len, expert_ids, ntp,
-                     nullptr);
-}
 
 }  // namespace
 
@@ -419,38 +395,6 @@ int launch_topk_softmax(const float* logits, int64_t T, int64_t E, int64_t top_k
     return check_launch("topk_softmax_kernel");
 }
 
-int launch_route_align_quant(const float* logits, int64_t T, int64_t E, int64_t top_k,
-                             bool renorm, float* tw, int32_t* ids, int64_t block_m,
-                             const int32_t* emap, int32_t* sorted_ids, int64_t sorted_len,
-                             int32_t* expert_ids, int32_t* ntp, const void* x, bool x_bf16,
-                             int64_t K, uint8_t* xq, float* xs, hipStream_t stream) {
-    if (E > 64 * kRouterMaxPerLane || top_k > 64 || top_k > E || T * top_k > kChunk ||
-        E > kMaxExperts) {
-        set_error("route_align_quant: needs E <= 1024, top_k <= min(64, E), T * top_k <= 1024");
-        return W4A8_ERR_INVALID;
-    }
-    if (T == 0) return W4A8_OK;
-    const unsigned grid = 1u + (unsigned)((T + kAlignThreads / 64 - 1) / (kAlignThreads / 64));
-#define W4A8_RAQ(BF, NV)                                                                        \
-    route_align_quant_kernel<BF, NV><<<grid, kAlignThreads, 0, stream>>>(                       \
-        logits, T, (int)E, (int)top_k, renorm, tw, ids, block_m, emap, sorted_ids, sorted_len,  \
-        expert_ids, ntp, x, (int)K, xq, xs)
-    const int nv = E <= 64 ? 1 : E <= 128 ? 2 : E <= 256 ? 4 : E <= 512 ? 8 : 16;
-    switch (nv * 2 + (x_bf16 ? 1 : 0)) {
-        case 2: W4A8_RAQ(false, 1); break;
-        case 3: W4A8_RAQ(true, 1); break;
-        case 4: W4A8_RAQ(false, 2); break;
-        case 5: W4A8_RAQ(true, 2); break;
-        case 8: W4A8_RAQ(false, 4); break;
-        case 9: W4A8_RAQ(true, 4); break;
-        case 16: W4A8_RAQ(false, 8); break;
-        case 17: W4A8_RAQ(true, 8); break;
-        case 32: W4A8_RAQ(false, 16); break;
-        default: W4A8_RAQ(true, 16); break;
-    }
-#undef W4A8_RAQ
-    return check_launch("route_align_quant_kernel");
-}
 
 int launch_align_quant(const int32_t* ids, int64_t numel, int64_t E, int64_t block_m,
                        const int32_t* emap, int32_t* sorted_ids, int64_t sorted_len,

@@ -54,13 +54,6 @@ int launch_silu_and_mul(const void* in, int64_t rows, int64_t inter, void* out,
 int launch_topk_softmax(const float* logits, int64_t T, int64_t E, int64_t top_k,
                         bool renorm, float* w, int32_t* ids, hipStream_t stream);
 size_t align_workspace_bytes(int64_t numel, int64_t num_experts);
-// Decode prologue with the router (T * top_k <= 1024): softmax/top-k of every token, the
-// single-work-group align on those ids, and per-row act-quant of x, in one launch.
-int launch_route_align_quant(const float* logits, int64_t T, int64_t E, int64_t top_k,
-                             bool renorm, float* tw, int32_t* ids, int64_t block_m,
-                             const int32_t* emap, int32_t* sorted_ids, int64_t sorted_len,
-                             int32_t* expert_ids, int32_t* ntp, const void* x, bool x_bf16,
-                             int64_t K, uint8_t* xq, float* xs, hipStream_t stream);
 // Decode prologue in one launch (numel <= 1024): the single-work-group align plus per-row
 // act-quant of x (k8-interleaved) with optional group sums.
 int launch_align_quant(const int32_t* ids, int64_t numel, int64_t E, int64_t block_m,

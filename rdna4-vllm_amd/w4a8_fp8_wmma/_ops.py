@@ -421,7 +421,7 @@ def moe_apply(x, w13, w2, w13_s, w2_s, w13_z, w2_z, topk_weights, topk_ids, expe
 def moe_forward(x, router_logits, top_k: int, w13, w2, w13_s, w2_s, w13_z, w2_z,
                 renormalize: bool = True, expert_map=None):
     """Router (softmax / top-k / renormalise, the vLLM fused_topk contract) plus the expert
-    path in one C-ABI call; at decode sizes the router shares the layer's first launch.
+    path in one C-ABI call.
     Returns (out (T, H) in x.dtype, topk_weights (T, k) fp32, topk_ids (T, k) int32)."""
     x = x.contiguous()
     T, H, inter, E, gs, frag, z13, z2, ws = _layer_args(x, w13, w2, w13_s, w2_s, w13_z, w2_z,

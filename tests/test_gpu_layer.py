@@ -133,8 +133,8 @@ def test_fragment_layout_full_size(name, T):
 
 @pytest.mark.parametrize("T,frag", [(1, True), (32, True), (32, False), (96, True), (300, True)])
 def test_moe_forward_equals_router_then_apply(T, frag):
-    """The router folded into the layer's first launch gives the fused_topk ids / weights
-    and the moe_apply output bit for bit."""
+    """moe_forward (router + expert path in one call) gives the fused_topk ids / weights and
+    the moe_apply output bit for bit."""
     cfg = dict(T=T, H=512, E=64, k=8, I=256, g=128, routing="uniform")
     ws = bench.make_weights(cfg, 700 + T, DEV)
     x, logits = bench.make_inputs(cfg, 701 + T, DEV)
