@@ -43,6 +43,7 @@ def hipcc() -> str:
 # every result once; from AGPRs each read would cost an extra v_accvgpr_read).
 EXTRA_FLAGS = {
     "prefill_gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+    "prefill_ares.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
 }
 
 

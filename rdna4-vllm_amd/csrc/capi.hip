@@ -270,6 +270,8 @@ int moe_apply_impl(const void* x, int x_dtype, int64_t T, int64_t H, int64_t int
     int rc;
     if (!mfma) rc = launch_grouped_scalar(g1, s);
     else if (pl.decode && !e2m1 && gemv_supported(H, group_size)) rc = launch_grouped_gemv(g1, s);
+    else if (pf1 && prefill_ares_supported(H, 2 * inter, group_size, e2m1, pl.block_m, Epi::kSiluHalf))
+        rc = launch_grouped_prefill_ares(g1, s);
     else if (pf1) rc = launch_grouped_prefill(g1, s);
     else rc = launch_grouped_mfma(g1, s);
     if (rc) return rc;
@@ -296,6 +298,8 @@ int moe_apply_impl(const void* x, int x_dtype, int64_t T, int64_t H, int64_t int
     g2.w_frag = frag;
     if (!mfma) rc = launch_grouped_scalar(g2, s);
     else if (gemv2) rc = launch_grouped_gemv(g2, s);
+    else if (pf2 && prefill_ares_supported(inter, H, group_size, e2m1, pl.block_m, Epi::kHalf))
+        rc = launch_grouped_prefill_ares(g2, s);
     else if (pf2) rc = launch_grouped_prefill(g2, s);
     else rc = launch_grouped_mfma(g2, s);
     if (rc) return rc;

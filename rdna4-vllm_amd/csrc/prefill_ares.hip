@@ -1,0 +1,452 @@
+// Prefill grouped W4A8 GEMM, activation-resident schedule (gfx950 fp8 MFMA).
+//
+// Replaces the reference's tiled WMMA grouped GEMM (moe_gemm_tiled.h:29-350, dispatched at
+// moe_kernel.hip:1110-1155) for the many-token regime when K <= 2048. Arithmetic contract as
+// in w4a8_common.h; the schedule is this file's own:
+//
+//   * a work-group owns 64 consecutive sorted rows (one expert) and ALL N columns: its e4m3
+//     activation tile (64 x K bytes) and the rows' per-group sums are loaded into LDS once,
+//     then the kernel streams the expert's int4 weights past them, 256 weight rows at a time
+//     (a "range": 4 waves x 4 16-column fragments; SiLU: 128 gate + the matching 128 up
+//     columns);
+//   * tiles are taken in an XCD-aware order: work-group b runs sorted tile
+//     (b % 8) * ceil(tiles / 8) + b / 8, so each XCD walks a contiguous run of tiles and the
+//     tiles of one expert share that XCD's L2 while they stream the same weights;
+//   * inside a range each wave keeps the next 4 (range, K group) steps' B fragments in flight
+//     (raw int4 words, 16 B per lane per fragment). Load addresses are a wave-uniform step
+//     offset plus a fixed per-lane offset, so they cost scalar instructions only; issues are
+//     unconditional (steps past the end reload the slab's start), so wait counts stay exact;
+//   * per step and live 16-row fragment: v_mfma_f32_16x16x128_f8f6f4 on the raw-nibble B
+//     (n * 2^-9, two ANDs and a shift), then the fp32 scale fold run += acc * scale[n, g]
+//     (moe_gemm_tiled.h:144-151) with the scale read from a per-wave LDS table;
+//   * the range's scales and zero-points are fetched one range ahead into registers; at a
+//     range boundary each wave writes the scale table and s*z (bf16 hi/lo) for its own 64
+//     columns, so no work-group barrier follows the prologue;
+//   * after the last group of a range the zero-point term sum_g sum_k a * z * s is formed by
+//     bf16 MFMAs over (row group sums) x (s*z), out = asc * (512 * run - term) is stored
+//     (fp16, or fp16 SiLU(gate) * up) and the accumulators restart;
+//   * the main loop is instantiated per live 16-row fragment count (1..4), so partial tiles
+//     run straight-line code without per-fragment branches.
+#include <algorithm>
+#include <type_traits>
+
+#include "grouped_params.h"
+
+namespace w4a8 {
+namespace {
+
+constexpr int kArBM = 64;                       // rows per work-group
+constexpr int kArWaves = 4;
+constexpr int kArNT = 4;                        // 16-column B fragments per wave and range
+constexpr int kArBN = kArWaves * kArNT * 16;    // 256 weight rows per range
+constexpr int kArD = 4;                         // B steps in flight per wave
+constexpr int kArMaxK = 2048;                   // activation tile must fit LDS
+constexpr int kArAPad = 16;                     // LDS row stride K + 16: conflict-free reads
+constexpr int kArGp = 16;                       // group slots of the per-range tables
+constexpr int kArXcds = 8;                      // work-groups go round-robin to 8 XCDs
+
+__host__ __device__ inline int ar_a_stride(int K) { return K + kArAPad; }
+// Dynamic LDS layout (bytes): activation tile; row group sums (hi/lo bf16); per range:
+// s*z (hi/lo bf16) of the 256 weight rows, scales [wave][group][column][fragment] (fp16)
+// and a staging area for the zero-point words
+struct ArLds {
+    int a, sah, sal, szh, szl, sc, zst, total;
+    __host__ __device__ explicit ArLds(int K) {
+        a = 0;
+        sah = kArBM * ar_a_stride(K);
+        sal = sah + kArBM * kArGp * 2;
+        szh = sal + kArBM * kArGp * 2;
+        szl = szh + kArBN * kArGp * 2;
+        sc = szl + kArBN * kArGp * 2;
+        zst = sc + kArBN * kArGp * 2;
+        total = zst + kArBN * 8;
+    }
+};
+__host__ inline size_t ar_lds_bytes(int K) { return (size_t)ArLds(K).total + kArBM * 4; }
+
+// Columns per range and the weight row of fragment j, column c of wave w in range r
+// (SiLU: fragments 0, 1 gate rows, 2, 3 the matching up rows ncols + col).
+template <bool kSilu>
+__host__ __device__ constexpr int ar_range_cols() { return kSilu ? kArBN / 2 : kArBN; }
+template <bool kSilu>
+__device__ __forceinline__ int ar_col(int r, int w, int j, int c) {
+    return kSilu ? r * (kArBN / 2) + w * 32 + 16 * (j & 1) + c : r * kArBN + w * 64 + 16 * j + c;
+}
+template <bool kSilu>
+__device__ __forceinline__ int ar_row(int r, int w, int j, int c, int ncols) {
+    return ar_col<kSilu>(r, w, j, c) + (kSilu && j >= 2 ? ncols : 0);
+}
+
+using bf16x8 = __bf16 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ v4f mfma_bf16_16x16x32(const bf16x8& a, const bf16x8& b, const v4f& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ bf16x8 lds_bf16x8(const __bf16* ptr) {
+    const uint4 v = *reinterpret_cast<const uint4*>(ptr);
+    bf16x8 r;
+    __builtin_memcpy(&r, &v, 16);
+    return r;
+}
+__device__ __forceinline__ uint32_t pack_bf16x2(__bf16 a, __bf16 b) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+}
+
+template <Epi EPI, bool FRAG>
+__global__ void __launch_bounds__(256, 1) prefill_ares_kernel(Params p) {
+    constexpr bool kSilu = EPI == Epi::kSiluHalf;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int q = lane >> 4;
+    const int c16 = lane & 15;
+    const int K = p.K;
+    const int G = p.G;
+    const int astride = ar_a_stride(K);
+    const ArLds L(K);
+    uint8_t* s_a = lds + L.a;                                         // [64][K + 16] e4m3
+    __bf16* s_sah = reinterpret_cast<__bf16*>(lds + L.sah);           // [64][16] row sums hi
+    __bf16* s_sal = reinterpret_cast<__bf16*>(lds + L.sal);           // ... lo
+    __bf16* s_szh = reinterpret_cast<__bf16*>(lds + L.szh);           // [256][16] s*z hi
+    __bf16* s_szl = reinterpret_cast<__bf16*>(lds + L.szl);           // ... lo
+    uint16_t* s_sc = reinterpret_cast<uint16_t*>(lds + L.sc);         // [4][16][16][4] fp16
+    uint2* s_zst = reinterpret_cast<uint2*>(lds + L.zst);             // [256] zero words
+    float* s_asc = reinterpret_cast<float*>(lds + L.total);           // [64]
+
+    // ---- tile of this work-group: XCD-aware order over the live tiles ----
+    const int ntp = p.ntp ? p.ntp[0] : (int)p.P;
+    const int64_t live_rows = std::min<int64_t>((int64_t)ntp, p.P);
+    const int ntiles = (int)((live_rows + kArBM - 1) / kArBM);
+    const int per_xcd = (ntiles + kArXcds - 1) / kArXcds;
+    const int b = blockIdx.x;
+    if (b / kArXcds >= per_xcd) return;
+    const int tile = (b % kArXcds) * per_xcd + b / kArXcds;
+    if (tile >= ntiles) return;
+    const int64_t row0 = (int64_t)tile * kArBM;
+    const int e = p.expert_ids ? p.expert_ids[row0 / p.block_m] : 0;
+    if (e < 0 || e >= p.E) return;
+    // lane l of every wave resolves row l; a real row's source is its activation row
+    int slot = -1;
+    const int src = resolve_row(p, row0 + lane, ntp, slot);
+    const uint64_t vmask = __ballot(src >= 0);
+    if (vmask == 0) return;
+    const int maxrow = 63 - __clzll(vmask);
+    const int nfl = maxrow / 16 + 1;                   // live 16-row fragments
+    const int fallback = __shfl(src, __ffsll((long long)vmask) - 1, 64);
+    // source row of tile row r (lane r of every wave resolved it); padding rows read a real
+    // row so every load stays in bounds. Every lane must take part (shuffle).
+    auto src_of = [&](int r) {
+        const int sr = __shfl(src, r, 64);
+        return sr >= 0 ? sr : fallback;
+    };
+
+    const int ncols = kSilu ? p.N / 2 : p.N;
+    const int nranges = ncols / ar_range_cols<kSilu>();
+    const uint32_t half_k = (uint32_t)K / 2;           // bytes per op-layout weight row
+    const uint8_t* we = reinterpret_cast<const uint8_t*>(p.w) + (int64_t)e * p.N * half_k;
+    const uint16_t* se = reinterpret_cast<const uint16_t*>(p.scales) + (int64_t)e * p.N * G;
+    const int32_t* ze = p.zeros ? p.zeros + (int64_t)e * (p.N / 8) * G : nullptr;
+
+    // ---- B ring. Byte offset of fragment j at step (range r, group g) =
+    //      step_off(r, g) + frag_off[j] (wave-uniform) + lane_off ----
+    //   fragment layout: 1 KB per (16-row block, group): ((row / 16) * G + g) * 1024 + lane * 16
+    //   op layout: row * K / 2 + g * 64 + q * 16 with row = first row + c16
+    const uint32_t g_step = FRAG ? 1024u : 64u;
+    const uint32_t r_step = FRAG ? (uint32_t)(ar_range_cols<kSilu>() / 16) * G * 1024u
+                                 : (uint32_t)ar_range_cols<kSilu>() * half_k;
+    const uint32_t lane_off = FRAG ? (uint32_t)lane * 16u : (uint32_t)c16 * half_k + q * 16u;
+    uint32_t frag_off[kArNT];
+#pragma unroll
+    for (int j = 0; j < kArNT; ++j) {
+        const uint32_t n0 = (uint32_t)ar_row<kSilu>(0, wave, j, 0, ncols);
+        frag_off[j] = FRAG ? (n0 / 16) * G * 1024u : n0 * half_k;
+    }
+    uint4 bw[kArD][kArNT];
+    uint32_t i_off = 0;          // step_off of the next issue
+    int i_g = 0, i_r = 0;        // its group and range
+    auto issue = [&](auto slotc) {
+        constexpr int sl = decltype(slotc)::value;
+        const uint8_t* base = we + i_off;
+#pragma unroll
+        for (int j = 0; j < kArNT; ++j) {
+            const uint8_t* ptr = base + frag_off[j] + lane_off;
+            bw[sl][j] = FRAG ? load_stream16(ptr) : *reinterpret_cast<const uint4*>(ptr);
+        }
+        // advance; past the last range the ring reloads range 0 (never consumed)
+        i_off += g_step;
+        if (++i_g == G) {
+            i_g = 0;
+            i_off += r_step - (uint32_t)G * g_step;
+            if (++i_r >= nranges) i_off = 0;
+        }
+    };
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    using S2 = std::integral_constant<int, 2>;
+    using S3 = std::integral_constant<int, 3>;
+
+    // ---- per-range tables. Lane l of wave w owns weight row lrow = 64 w + l, i.e. fragment
+    //      l / 16, column l % 16: its G scales (G / 4 8-byte loads) and two zero-point words of
+    //      its 8-row group (lanes 8k..8k+7 hold the group's 16 words between them) ----
+    const int tj = lane >> 4, tc = lane & 15;
+    uint2 pf_s[4];
+    uint2 pf_z;
+    auto prefetch = [&](int r) {
+        const int n = ar_row<kSilu>(std::min(r, nranges - 1), wave, tj, tc, ncols);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int uu = std::min(u, G / 4 - 1);
+            pf_s[u] = *reinterpret_cast<const uint2*>(se + (uint32_t)n * G + 4 * uu);
+        }
+        const int w0 = std::min(2 * (lane & 7), G - 2);
+        // symmetric weights read (and ignore) a scale pair instead: same load count
+        pf_z = ze ? *reinterpret_cast<const uint2*>(ze + (uint32_t)(n >> 3) * G + w0)
+                  : *reinterpret_cast<const uint2*>(se);
+    };
+    auto build = [&](int r) {
+        const int n = ar_row<kSilu>(r, wave, tj, tc, ncols);
+        s_zst[64 * wave + lane] = pf_z;
+        uint32_t zw[kArGp];
+        {
+            const uint4* zr = reinterpret_cast<const uint4*>(s_zst + 64 * wave + (lane & ~7));
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const uint4 v = zr[u];
+                zw[4 * u] = v.x;
+                zw[4 * u + 1] = v.y;
+                zw[4 * u + 2] = v.z;
+                zw[4 * u + 3] = v.w;
+            }
+        }
+        const int zsh = (n & 7) * 4;
+        uint32_t szh[kArGp / 2], szl[kArGp / 2];
+#pragma unroll
+        for (int g = 0; g < kArGp; g += 2) {
+            float sz[2];
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const uint2 sp = pf_s[(g + t) / 4];
+                const uint32_t w2 = ((g + t) & 2) ? sp.y : sp.x;
+                const uint16_t hb = ((g + t) & 1) ? (uint16_t)(w2 >> 16) : (uint16_t)(w2 & 0xFFFF);
+                const float sv = __half2float(__ushort_as_half(hb));
+                const float z = ze ? (float)((zw[g + t] >> zsh) & 0xF) : 8.0f;
+                sz[t] = g + t < G ? sv * z : 0.f;   // exact: fp16 scale x integer <= 15
+                s_sc[((wave * kArGp + g + t) * 16 + tc) * kArNT + tj] = hb;
+            }
+            const __bf16 h0 = (__bf16)sz[0], h1 = (__bf16)sz[1];
+            szh[g / 2] = pack_bf16x2(h0, h1);
+            szl[g / 2] = pack_bf16x2((__bf16)(sz[0] - (float)h0), (__bf16)(sz[1] - (float)h1));
+        }
+        uint4* dh = reinterpret_cast<uint4*>(s_szh + (64 * wave + lane) * kArGp);
+        uint4* dl = reinterpret_cast<uint4*>(s_szl + (64 * wave + lane) * kArGp);
+        dh[0] = make_uint4(szh[0], szh[1], szh[2], szh[3]);
+        dh[1] = make_uint4(szh[4], szh[5], szh[6], szh[7]);
+        dl[0] = make_uint4(szl[0], szl[1], szl[2], szl[3]);
+        dl[1] = make_uint4(szl[4], szl[5], szl[6], szl[7]);
+    };
+
+    // ---- prologue: range 0's tables, the activation tile, row group sums, the ring ----
+    prefetch(0);
+    {
+        // 16-byte chunk c of the tile: row c / (K / 16), bytes (c % (K / 16)) * 16
+        const int cpr = K / 16;                         // chunks per row
+        const int total = kArBM * cpr;                  // multiple of 256 (K % 64 == 0)
+        for (int c0 = 0; c0 < total; c0 += 256 * 8) {
+            uint4 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int c = min(c0 + u * 256 + tid, total - 1);
+                v[u] = *reinterpret_cast<const uint4*>(p.xq + (int64_t)src_of(c / cpr) * K + (c % cpr) * 16);
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int c = c0 + u * 256 + tid;
+                if (c < total)
+                    *reinterpret_cast<uint4*>(s_a + (c / cpr) * astride + (c % cpr) * 16) = v[u];
+            }
+        }
+        for (int i = tid; i < kArBM * kArGp; i += 256) {   // row sums; groups >= G are 0
+            const int r = i / kArGp, g = i % kArGp;
+            const int sr = src_of(r);
+            const float v = g < G ? p.asum[(int64_t)sr * G + g] : 0.f;
+            const __bf16 h = (__bf16)v;
+            s_sah[i] = h;
+            s_sal[i] = (__bf16)(v - (float)h);
+        }
+        if (wave == 0) s_asc[lane] = src >= 0 ? p.asc[src] : 0.f;
+    }
+    issue(S0{});
+    issue(S1{});
+    issue(S2{});
+    issue(S3{});
+    build(0);
+    prefetch(1);
+    lds_barrier();
+
+    // Range epilogue: zero-point term of every (row, column) as bf16 MFMAs over the groups
+    // (lane (q, c16), K slot 8q + t <-> group 8 (q & 1) + t: A = hi (q < 2) or lo (q >= 2)
+    // half of the row's group sum; B = hi, then lo, half of s*z with slots 16..31 repeating
+    // 0..15, so the two MFMAs add (sa_hi + sa_lo)(sz_hi + sz_lo)), then
+    // out = asc * (512 * run - zero term), stored.
+    auto main_loop = [&](auto nflc) {
+        constexpr int NF = decltype(nflc)::value;
+        v4f run[NF][kArNT];
+#pragma unroll
+        for (int i = 0; i < NF; ++i)
+#pragma unroll
+            for (int j = 0; j < kArNT; ++j) run[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+
+        auto consume = [&](int g, auto slotc) {
+            constexpr int sl = decltype(slotc)::value;
+            const uint2 sp = *reinterpret_cast<const uint2*>(s_sc + ((wave * kArGp + g) * 16 + c16) * kArNT);
+            float sc[kArNT];
+            sc[0] = __half2float(__ushort_as_half((uint16_t)(sp.x & 0xFFFF)));
+            sc[1] = __half2float(__ushort_as_half((uint16_t)(sp.x >> 16)));
+            sc[2] = __half2float(__ushort_as_half((uint16_t)(sp.y & 0xFFFF)));
+            sc[3] = __half2float(__ushort_as_half((uint16_t)(sp.y >> 16)));
+            v8i bf[kArNT];
+#pragma unroll
+            for (int j = 0; j < kArNT; ++j) bf[j] = spread_nibbles(bw[sl][j]);
+            const uint8_t* A = s_a + c16 * astride + g * kGroup + q * 32;
+#pragma unroll
+            for (int i = 0; i < NF; ++i) {
+                const uint4 lo = *reinterpret_cast<const uint4*>(A + i * 16 * astride);
+                const uint4 hi = *reinterpret_cast<const uint4*>(A + i * 16 * astride + 16);
+                const v8i af = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w,
+                                   (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+#pragma unroll
+                for (int j = 0; j < kArNT; ++j) {
+                    const v4f acc = mfma_16x16x128(af, bf[j], v4f{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+                    for (int rr = 0; rr < 4; ++rr) run[i][j][rr] = fmaf(acc[rr], sc[j], run[i][j][rr]);
+                }
+            }
+        };
+
+        auto epilogue = [&](int r) {
+            const __bf16* sa_tab = q < 2 ? s_sah : s_sal;
+            const int go = 8 * (q & 1);
+#pragma unroll
+            for (int jp = 0; jp < 2; ++jp) {
+                const int ja = kSilu ? jp : 2 * jp;
+                const int jb = kSilu ? jp + 2 : 2 * jp + 1;
+                const int lra = 64 * wave + 16 * ja + c16, lrb = 64 * wave + 16 * jb + c16;
+                const bf16x8 zah = lds_bf16x8(s_szh + lra * kArGp + go);
+                const bf16x8 zal = lds_bf16x8(s_szl + lra * kArGp + go);
+                const bf16x8 zbh = lds_bf16x8(s_szh + lrb * kArGp + go);
+                const bf16x8 zbl = lds_bf16x8(s_szl + lrb * kArGp + go);
+                const int cola = ar_col<kSilu>(r, wave, ja, c16);
+                const int colb = ar_col<kSilu>(r, wave, jb, c16);
+#pragma unroll
+                for (int i = 0; i < NF; ++i) {
+                    const bf16x8 sa = lds_bf16x8(sa_tab + (16 * i + c16) * kArGp + go);
+                    v4f za = mfma_bf16_16x16x32(sa, zah, v4f{0.f, 0.f, 0.f, 0.f});
+                    za = mfma_bf16_16x16x32(sa, zal, za);
+                    v4f zb = mfma_bf16_16x16x32(sa, zbh, v4f{0.f, 0.f, 0.f, 0.f});
+                    zb = mfma_bf16_16x16x32(sa, zbl, zb);
+#pragma unroll
+                    for (int rr = 0; rr < 4; ++rr) {
+                        const int m = 16 * i + 4 * q + rr;
+                        if (!((vmask >> m) & 1)) continue;
+                        const float a = s_asc[m];
+                        const float va = a * (kNibbleScale * run[i][ja][rr] - za[rr]);
+                        const float vb = a * (kNibbleScale * run[i][jb][rr] - zb[rr]);
+                        const int64_t row_pad = row0 + m;
+                        if constexpr (kSilu) {
+                            reinterpret_cast<__half*>(p.out)[row_pad * ncols + cola] =
+                                silu_mul_h(__float2half(va), __float2half(vb));
+                        } else {
+                            reinterpret_cast<__half*>(p.out)[row_pad * p.N + cola] = __float2half(va);
+                            reinterpret_cast<__half*>(p.out)[row_pad * p.N + colb] = __float2half(vb);
+                        }
+                    }
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < NF; ++i)
+#pragma unroll
+                for (int j = 0; j < kArNT; ++j) run[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+        };
+
+        for (int r = 0; r < nranges; ++r) {
+            // G % 4 == 0: the ring's four slots turn over once per iteration
+            int g = 0;
+            do {
+                consume(g, S0{});
+                issue(S0{});
+                consume(g + 1, S1{});
+                issue(S1{});
+                consume(g + 2, S2{});
+                issue(S2{});
+                consume(g + 3, S3{});
+                issue(S3{});
+                g += 4;
+            } while (g < G);
+            epilogue(r);
+            if (r + 1 < nranges) {
+                build(r + 1);
+                prefetch(r + 2);
+            }
+        }
+    };
+    switch (nfl) {
+        case 1: main_loop(std::integral_constant<int, 1>{}); break;
+        case 2: main_loop(std::integral_constant<int, 2>{}); break;
+        case 3: main_loop(std::integral_constant<int, 3>{}); break;
+        default: main_loop(std::integral_constant<int, 4>{}); break;
+    }
+}
+
+template <Epi EPI, bool FRAG>
+int launch_ares_t(const Params& p, hipStream_t s) {
+    const size_t lds = ar_lds_bytes(p.K);
+    static bool attr_set = false;
+    if (!attr_set) {   // > 64 KB of dynamic LDS needs an explicit opt-in
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_ares_kernel<EPI, FRAG>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)ar_lds_bytes(kArMaxK)) != hipSuccess) {
+            set_error("prefill_ares_kernel: cannot reserve dynamic LDS");
+            return W4A8_ERR_HIP;
+        }
+        attr_set = true;
+    }
+    // a multiple of 8 work-groups covers every tile under the XCD-aware order
+    const int64_t tiles = (p.P + kArBM - 1) / kArBM;
+    const unsigned grid = (unsigned)((tiles + kArXcds - 1) / kArXcds * kArXcds);
+    prefill_ares_kernel<EPI, FRAG><<<grid, 256, lds, s>>>(p);
+    return check_launch("prefill_ares_kernel");
+}
+
+}  // namespace
+
+bool prefill_ares_supported(int64_t K, int64_t N, int64_t group_size, bool e2m1, int64_t block_m,
+                            Epi epi) {
+    if (e2m1 || group_size != kGroup || K % (4 * kGroup) != 0 || K > kArMaxK || block_m % kArBM != 0)
+        return false;
+    if (epi == Epi::kSiluHalf) return N % (2 * ar_range_cols<true>()) == 0;
+    if (epi == Epi::kHalf) return N % ar_range_cols<false>() == 0;
+    return false;
+}
+
+int launch_grouped_prefill_ares(const GroupedArgs& a, hipStream_t s) {
+    const Params p = make_params(a);
+    if (p.P == 0) return W4A8_OK;
+    if (!prefill_ares_supported(a.K, a.N, a.group_size, a.e2m1, a.block_m, a.epi) || p.xq == nullptr ||
+        p.asum == nullptr || p.asc == nullptr || a.x_rows * a.K >= ((int64_t)1 << 31)) {
+        set_error("prefill (activation-resident): needs g128 int4 weights, K % 512 == 0 and "
+                  "K <= 2048, output columns in whole 256-row ranges, block_m % 64 == 0, "
+                  "prequantised rows with group sums, fp16 out");
+        return W4A8_ERR_INVALID;
+    }
+    if (a.w_frag && (a.N % 16 != 0 || (a.epi == Epi::kSiluHalf && (a.N / 2) % 16 != 0))) {
+        set_error("prefill (activation-resident): fragment-layout weights need 16-row aligned halves");
+        return W4A8_ERR_INVALID;
+    }
+    if (a.epi == Epi::kSiluHalf)
+        return a.w_frag ? launch_ares_t<Epi::kSiluHalf, true>(p, s) : launch_ares_t<Epi::kSiluHalf, false>(p, s);
+    return a.w_frag ? launch_ares_t<Epi::kHalf, true>(p, s) : launch_ares_t<Epi::kHalf, false>(p, s);
+}
+
+}  // namespace w4a8

@@ -120,6 +120,10 @@ struct GroupedArgs {
 int launch_grouped_scalar(const GroupedArgs& a, hipStream_t stream);
 int launch_grouped_mfma(const GroupedArgs& a, hipStream_t stream);   // prefill tiles
 int launch_grouped_gemv(const GroupedArgs& a, hipStream_t stream);   // decode GEMV
+// Prefill, activation-resident schedule (prefill_ares.hip): 64-row tiles, all N per tile.
+bool prefill_ares_supported(int64_t K, int64_t N, int64_t group_size, bool e2m1, int64_t block_m,
+                            Epi epi);
+int launch_grouped_prefill_ares(const GroupedArgs& a, hipStream_t stream);
 // (E, N, K/8) int32 op layout -> fragment layout: per expert, 16-row tile t and 128-wide
 // group g, a 1 KB block whose 16-byte lane l holds row 16t + l % 16, k in
 // [128g + 32 (l / 16), +32) (the MFMA B operand of lane l). N % 16 == 0, K % 128 == 0.
