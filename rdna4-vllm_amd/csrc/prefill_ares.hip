@@ -36,16 +36,23 @@ namespace w4a8 {
 namespace {
 
 constexpr int kArBM = 64;                       // rows per work-group
-constexpr int kArWaves = 4;
-constexpr int kArNT = 4;                        // 16-column B fragments per wave and range
+constexpr int kArWaves = 8;                     // two waves per SIMD
+constexpr int kArThreads = kArWaves * 64;
+constexpr int kArNT = 2;                        // 16-column B fragments per wave and range
 constexpr int kArBN = kArWaves * kArNT * 16;    // 256 weight rows per range
 constexpr int kArD = 4;                         // B steps in flight per wave
 constexpr int kArMaxK = 2048;                   // activation tile must fit LDS
-constexpr int kArAPad = 16;                     // LDS row stride K + 16: conflict-free reads
 constexpr int kArGp = 16;                       // group slots of the per-range tables
 constexpr int kArXcds = 8;                      // work-groups go round-robin to 8 XCDs
 
-__host__ __device__ inline int ar_a_stride(int K) { return K + kArAPad; }
+// Activation tile in LDS, group-major: K group g of row m is 128 bytes at g * 8 KB + m * 128,
+// its eight 16-byte chunks stored at chunk ^ (m & 7), so the eight rows a ds_read_b128
+// serves per cycle hit eight different bank quads, and the rows of fragment i sit at the
+// fixed offset i * 2 KB.
+__host__ __device__ constexpr int ar_a_group_bytes() { return kArBM * kGroup; }
+__device__ __forceinline__ int ar_a_off(int m, int g, int chunk) {
+    return g * ar_a_group_bytes() + m * kGroup + ((chunk ^ (m & 7)) << 4);
+}
 // Dynamic LDS layout (bytes): activation tile; row group sums (hi/lo bf16); per range:
 // s*z (hi/lo bf16) of the 256 weight rows, scales [wave][group][column][fragment] (fp16)
 // and a staging area for the zero-point words
@@ -53,7 +60,7 @@ struct ArLds {
     int a, sah, sal, szh, szl, sc, zst, total;
     __host__ __device__ explicit ArLds(int K) {
         a = 0;
-        sah = kArBM * ar_a_stride(K);
+        sah = (K / kGroup) * ar_a_group_bytes();
         sal = sah + kArBM * kArGp * 2;
         szh = sal + kArBM * kArGp * 2;
         szl = szh + kArBN * kArGp * 2;
@@ -64,17 +71,27 @@ struct ArLds {
 };
 __host__ inline size_t ar_lds_bytes(int K) { return (size_t)ArLds(K).total + kArBM * 4; }
 
-// Columns per range and the weight row of fragment j, column c of wave w in range r
-// (SiLU: fragments 0, 1 gate rows, 2, 3 the matching up rows ncols + col).
+// Output columns per range; output column and weight row of fragment j, column c of wave w
+// in range r (SiLU: fragment 0 holds gate rows col, fragment 1 the matching up rows
+// ncols + col; otherwise the wave's two fragments are 32 adjacent columns).
 template <bool kSilu>
 __host__ __device__ constexpr int ar_range_cols() { return kSilu ? kArBN / 2 : kArBN; }
 template <bool kSilu>
 __device__ __forceinline__ int ar_col(int r, int w, int j, int c) {
-    return kSilu ? r * (kArBN / 2) + w * 32 + 16 * (j & 1) + c : r * kArBN + w * 64 + 16 * j + c;
+    return kSilu ? r * (kArBN / 2) + w * 16 + c : r * kArBN + w * 32 + 16 * j + c;
 }
 template <bool kSilu>
 __device__ __forceinline__ int ar_row(int r, int w, int j, int c, int ncols) {
-    return ar_col<kSilu>(r, w, j, c) + (kSilu && j >= 2 ? ncols : 0);
+    return ar_col<kSilu>(r, w, j, c) + (kSilu && j == 1 ? ncols : 0);
+}
+
+// SiLU(gate) * up on the fp16 gate/up values (moe_kernel.hip:555-561), with the hardware
+// exp2 and reciprocal (1 ulp each) in place of the correctly rounded expf and division.
+__device__ __forceinline__ __half silu_mul_fast(float gate, float up) {
+    const float g = __half2float(__float2half(gate));
+    const float e = __builtin_amdgcn_exp2f(g * -1.44269504088896341f);
+    const __half silu_h = __float2half(g * __builtin_amdgcn_rcpf(1.0f + e));
+    return __hmul(silu_h, __float2half(up));
 }
 
 using bf16x8 = __bf16 __attribute__((ext_vector_type(8)));
@@ -93,7 +110,7 @@ __device__ __forceinline__ uint32_t pack_bf16x2(__bf16 a, __bf16 b) {
 }
 
 template <Epi EPI, bool FRAG>
-__global__ void __launch_bounds__(256, 1) prefill_ares_kernel(Params p) {
+__global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
     constexpr bool kSilu = EPI == Epi::kSiluHalf;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
 
@@ -104,15 +121,14 @@ __global__ void __launch_bounds__(256, 1) prefill_ares_kernel(Params p) {
     const int c16 = lane & 15;
     const int K = p.K;
     const int G = p.G;
-    const int astride = ar_a_stride(K);
     const ArLds L(K);
-    uint8_t* s_a = lds + L.a;                                         // [64][K + 16] e4m3
+    uint8_t* s_a = lds + L.a;                                         // [G][64][128] e4m3
     __bf16* s_sah = reinterpret_cast<__bf16*>(lds + L.sah);           // [64][16] row sums hi
     __bf16* s_sal = reinterpret_cast<__bf16*>(lds + L.sal);           // ... lo
     __bf16* s_szh = reinterpret_cast<__bf16*>(lds + L.szh);           // [256][16] s*z hi
     __bf16* s_szl = reinterpret_cast<__bf16*>(lds + L.szl);           // ... lo
-    uint16_t* s_sc = reinterpret_cast<uint16_t*>(lds + L.sc);         // [4][16][16][4] fp16
-    uint2* s_zst = reinterpret_cast<uint2*>(lds + L.zst);             // [256] zero words
+    uint16_t* s_sc = reinterpret_cast<uint16_t*>(lds + L.sc);         // [8][16][16][2] fp16
+    uint32_t* s_zst = reinterpret_cast<uint32_t*>(lds + L.zst);       // [8][64] zero words
     float* s_asc = reinterpret_cast<float*>(lds + L.total);           // [64]
 
     // ---- tile of this work-group: XCD-aware order over the live tiles ----
@@ -187,64 +203,61 @@ __global__ void __launch_bounds__(256, 1) prefill_ares_kernel(Params p) {
     using S2 = std::integral_constant<int, 2>;
     using S3 = std::integral_constant<int, 3>;
 
-    // ---- per-range tables. Lane l of wave w owns weight row lrow = 64 w + l, i.e. fragment
-    //      l / 16, column l % 16: its G scales (G / 4 8-byte loads) and two zero-point words of
-    //      its 8-row group (lanes 8k..8k+7 hold the group's 16 words between them) ----
-    const int tj = lane >> 4, tc = lane & 15;
-    uint2 pf_s[4];
-    uint2 pf_z;
+    // ---- per-range tables. Lane l of wave w owns weight row lrow = 32 w + (l & 31), i.e.
+    //      fragment (l >> 4) & 1, column l & 15, for groups 8 (l >> 5) .. + 7: two 8-byte
+    //      scale loads. Lane l also loads zero-point word l & 15 of the wave's 8-row group
+    //      l >> 4; a row's group then reads its 8 words from the staging area ----
+    const int trow = lane & 31, tj = trow >> 4, tc = trow & 15, th = lane >> 5;
+    const int lrow = 32 * wave + trow;
+    uint2 pf_s[2];
+    uint32_t pf_z;
     auto prefetch = [&](int r) {
-        const int n = ar_row<kSilu>(std::min(r, nranges - 1), wave, tj, tc, ncols);
+        const int rr = std::min(r, nranges - 1);
+        const int n = ar_row<kSilu>(rr, wave, tj, tc, ncols);
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int uu = std::min(u, G / 4 - 1);
-            pf_s[u] = *reinterpret_cast<const uint2*>(se + (uint32_t)n * G + 4 * uu);
+        for (int u = 0; u < 2; ++u) {
+            const int qd = std::min(2 * th + u, G / 4 - 1);
+            pf_s[u] = *reinterpret_cast<const uint2*>(se + (uint32_t)n * G + 4 * qd);
         }
-        const int w0 = std::min(2 * (lane & 7), G - 2);
-        // symmetric weights read (and ignore) a scale pair instead: same load count
-        pf_z = ze ? *reinterpret_cast<const uint2*>(ze + (uint32_t)(n >> 3) * G + w0)
-                  : *reinterpret_cast<const uint2*>(se);
+        const int rgl = lane >> 4;                     // the wave's 8-row groups: (fragment, half)
+        const int nz = ar_row<kSilu>(rr, wave, rgl >> 1, 8 * (rgl & 1), ncols);
+        const int wz = std::min(lane & 15, G - 1);
+        // symmetric weights read (and ignore) a scale word instead: same load count
+        pf_z = ze ? (uint32_t)ze[(uint32_t)(nz >> 3) * G + wz] : *reinterpret_cast<const uint32_t*>(se);
     };
     auto build = [&](int r) {
         const int n = ar_row<kSilu>(r, wave, tj, tc, ncols);
         s_zst[64 * wave + lane] = pf_z;
-        uint32_t zw[kArGp];
+        uint32_t zw[8];
         {
-            const uint4* zr = reinterpret_cast<const uint4*>(s_zst + 64 * wave + (lane & ~7));
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const uint4 v = zr[u];
-                zw[4 * u] = v.x;
-                zw[4 * u + 1] = v.y;
-                zw[4 * u + 2] = v.z;
-                zw[4 * u + 3] = v.w;
-            }
+            const int rgl = 2 * tj + (tc >> 3);
+            const uint4* zr = reinterpret_cast<const uint4*>(s_zst + 64 * wave + 16 * rgl + 8 * th);
+            const uint4 z0 = zr[0], z1 = zr[1];
+            zw[0] = z0.x; zw[1] = z0.y; zw[2] = z0.z; zw[3] = z0.w;
+            zw[4] = z1.x; zw[5] = z1.y; zw[6] = z1.z; zw[7] = z1.w;
         }
         const int zsh = (n & 7) * 4;
-        uint32_t szh[kArGp / 2], szl[kArGp / 2];
+        uint32_t szh[4], szl[4];
 #pragma unroll
-        for (int g = 0; g < kArGp; g += 2) {
+        for (int t = 0; t < 8; t += 2) {
             float sz[2];
 #pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                const uint2 sp = pf_s[(g + t) / 4];
-                const uint32_t w2 = ((g + t) & 2) ? sp.y : sp.x;
-                const uint16_t hb = ((g + t) & 1) ? (uint16_t)(w2 >> 16) : (uint16_t)(w2 & 0xFFFF);
+            for (int v = 0; v < 2; ++v) {
+                const int tt = t + v, g = 8 * th + tt;
+                const uint2 sp = pf_s[tt / 4];
+                const uint32_t w2 = (tt & 2) ? sp.y : sp.x;
+                const uint16_t hb = (tt & 1) ? (uint16_t)(w2 >> 16) : (uint16_t)(w2 & 0xFFFF);
                 const float sv = __half2float(__ushort_as_half(hb));
-                const float z = ze ? (float)((zw[g + t] >> zsh) & 0xF) : 8.0f;
-                sz[t] = g + t < G ? sv * z : 0.f;   // exact: fp16 scale x integer <= 15
-                s_sc[((wave * kArGp + g + t) * 16 + tc) * kArNT + tj] = hb;
+                const float z = ze ? (float)((zw[tt] >> zsh) & 0xF) : 8.0f;
+                sz[v] = g < G ? sv * z : 0.f;   // exact: fp16 scale x integer <= 15
+                s_sc[((wave * kArGp + g) * 16 + tc) * kArNT + tj] = hb;
             }
             const __bf16 h0 = (__bf16)sz[0], h1 = (__bf16)sz[1];
-            szh[g / 2] = pack_bf16x2(h0, h1);
-            szl[g / 2] = pack_bf16x2((__bf16)(sz[0] - (float)h0), (__bf16)(sz[1] - (float)h1));
+            szh[t / 2] = pack_bf16x2(h0, h1);
+            szl[t / 2] = pack_bf16x2((__bf16)(sz[0] - (float)h0), (__bf16)(sz[1] - (float)h1));
         }
-        uint4* dh = reinterpret_cast<uint4*>(s_szh + (64 * wave + lane) * kArGp);
-        uint4* dl = reinterpret_cast<uint4*>(s_szl + (64 * wave + lane) * kArGp);
-        dh[0] = make_uint4(szh[0], szh[1], szh[2], szh[3]);
-        dh[1] = make_uint4(szh[4], szh[5], szh[6], szh[7]);
-        dl[0] = make_uint4(szl[0], szl[1], szl[2], szl[3]);
-        dl[1] = make_uint4(szl[4], szl[5], szl[6], szl[7]);
+        *reinterpret_cast<uint4*>(s_szh + lrow * kArGp + 8 * th) = make_uint4(szh[0], szh[1], szh[2], szh[3]);
+        *reinterpret_cast<uint4*>(s_szl + lrow * kArGp + 8 * th) = make_uint4(szl[0], szl[1], szl[2], szl[3]);
     };
 
     // ---- prologue: range 0's tables, the activation tile, row group sums, the ring ----
@@ -252,22 +265,22 @@ __global__ void __launch_bounds__(256, 1) prefill_ares_kernel(Params p) {
     {
         // 16-byte chunk c of the tile: row c / (K / 16), bytes (c % (K / 16)) * 16
         const int cpr = K / 16;                         // chunks per row
-        const int total = kArBM * cpr;                  // multiple of 256 (K % 64 == 0)
-        for (int c0 = 0; c0 < total; c0 += 256 * 8) {
+        const int total = kArBM * cpr;                  // multiple of 512 (K % 128 == 0)
+        for (int c0 = 0; c0 < total; c0 += kArThreads * 8) {
             uint4 v[8];
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
-                const int c = min(c0 + u * 256 + tid, total - 1);
+                const int c = min(c0 + u * kArThreads + tid, total - 1);
                 v[u] = *reinterpret_cast<const uint4*>(p.xq + (int64_t)src_of(c / cpr) * K + (c % cpr) * 16);
             }
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
-                const int c = c0 + u * 256 + tid;
+                const int c = c0 + u * kArThreads + tid;
                 if (c < total)
-                    *reinterpret_cast<uint4*>(s_a + (c / cpr) * astride + (c % cpr) * 16) = v[u];
+                    *reinterpret_cast<uint4*>(s_a + ar_a_off(c / cpr, (c % cpr) >> 3, c & 7)) = v[u];
             }
         }
-        for (int i = tid; i < kArBM * kArGp; i += 256) {   // row sums; groups >= G are 0
+        for (int i = tid; i < kArBM * kArGp; i += kArThreads) {   // row sums; groups >= G are 0
             const int r = i / kArGp, g = i % kArGp;
             const int sr = src_of(r);
             const float v = g < G ? p.asum[(int64_t)sr * G + g] : 0.f;
@@ -285,11 +298,6 @@ __global__ void __launch_bounds__(256, 1) prefill_ares_kernel(Params p) {
     prefetch(1);
     lds_barrier();
 
-    // Range epilogue: zero-point term of every (row, column) as bf16 MFMAs over the groups
-    // (lane (q, c16), K slot 8q + t <-> group 8 (q & 1) + t: A = hi (q < 2) or lo (q >= 2)
-    // half of the row's group sum; B = hi, then lo, half of s*z with slots 16..31 repeating
-    // 0..15, so the two MFMAs add (sa_hi + sa_lo)(sz_hi + sz_lo)), then
-    // out = asc * (512 * run - zero term), stored.
     auto main_loop = [&](auto nflc) {
         constexpr int NF = decltype(nflc)::value;
         v4f run[NF][kArNT];
@@ -298,69 +306,91 @@ __global__ void __launch_bounds__(256, 1) prefill_ares_kernel(Params p) {
 #pragma unroll
             for (int j = 0; j < kArNT; ++j) run[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
+        // Software pipeline: a step first folds the previous step's MFMA results into the
+        // accumulators (run += acc * scale), then issues its own MFMAs into the same
+        // registers, so every result has a whole step to arrive before it is read.
+        v4f pend[NF][kArNT];
+        float psc[kArNT] = {0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < NF; ++i)
+#pragma unroll
+            for (int j = 0; j < kArNT; ++j) pend[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+        auto fold = [&]() {
+#pragma unroll
+            for (int i = 0; i < NF; ++i)
+#pragma unroll
+                for (int j = 0; j < kArNT; ++j)
+#pragma unroll
+                    for (int rr = 0; rr < 4; ++rr) run[i][j][rr] = fmaf(pend[i][j][rr], psc[j], run[i][j][rr]);
+        };
         auto consume = [&](int g, auto slotc) {
             constexpr int sl = decltype(slotc)::value;
-            const uint2 sp = *reinterpret_cast<const uint2*>(s_sc + ((wave * kArGp + g) * 16 + c16) * kArNT);
-            float sc[kArNT];
-            sc[0] = __half2float(__ushort_as_half((uint16_t)(sp.x & 0xFFFF)));
-            sc[1] = __half2float(__ushort_as_half((uint16_t)(sp.x >> 16)));
-            sc[2] = __half2float(__ushort_as_half((uint16_t)(sp.y & 0xFFFF)));
-            sc[3] = __half2float(__ushort_as_half((uint16_t)(sp.y >> 16)));
+            const uint32_t sp = *reinterpret_cast<const uint32_t*>(s_sc + ((wave * kArGp + g) * 16 + c16) * kArNT);
             v8i bf[kArNT];
 #pragma unroll
             for (int j = 0; j < kArNT; ++j) bf[j] = spread_nibbles(bw[sl][j]);
-            const uint8_t* A = s_a + c16 * astride + g * kGroup + q * 32;
+            // fragment i's rows are 16 i + c16: same swizzle as row c16, offset i * 2 KB
+            const uint8_t* A0 = s_a + ar_a_off(c16, g, 2 * q);
+            const uint8_t* A1 = s_a + ar_a_off(c16, g, 2 * q + 1);
+            const float sc0 = __half2float(__ushort_as_half((uint16_t)(sp & 0xFFFF)));
+            const float sc1 = __half2float(__ushort_as_half((uint16_t)(sp >> 16)));
 #pragma unroll
             for (int i = 0; i < NF; ++i) {
-                const uint4 lo = *reinterpret_cast<const uint4*>(A + i * 16 * astride);
-                const uint4 hi = *reinterpret_cast<const uint4*>(A + i * 16 * astride + 16);
+                const uint4 lo = *reinterpret_cast<const uint4*>(A0 + i * 16 * kGroup);
+                const uint4 hi = *reinterpret_cast<const uint4*>(A1 + i * 16 * kGroup);
                 const v8i af = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w,
                                    (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
 #pragma unroll
                 for (int j = 0; j < kArNT; ++j) {
-                    const v4f acc = mfma_16x16x128(af, bf[j], v4f{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
-                    for (int rr = 0; rr < 4; ++rr) run[i][j][rr] = fmaf(acc[rr], sc[j], run[i][j][rr]);
+                    for (int rr = 0; rr < 4; ++rr) run[i][j][rr] = fmaf(pend[i][j][rr], psc[j], run[i][j][rr]);
+                    pend[i][j] = mfma_16x16x128(af, bf[j], v4f{0.f, 0.f, 0.f, 0.f});
                 }
             }
+            psc[0] = sc0;
+            psc[1] = sc1;
         };
 
+        // Range epilogue: zero-point term of every (row, column) as bf16 MFMAs over the
+        // groups (lane (q, c16), K slot 8q + t <-> group 8 (q & 1) + t: A = hi (q < 2) or lo
+        // (q >= 2) half of the row's group sum; B = hi, then lo, half of s*z with slots
+        // 16..31 repeating 0..15, so the two MFMAs add (sa_hi + sa_lo)(sz_hi + sz_lo)), then
+        // out = asc * (512 * run - zero term), stored; the accumulators restart.
         auto epilogue = [&](int r) {
+            fold();
+#pragma unroll
+            for (int i = 0; i < NF; ++i)
+#pragma unroll
+                for (int j = 0; j < kArNT; ++j) pend[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
             const __bf16* sa_tab = q < 2 ? s_sah : s_sal;
             const int go = 8 * (q & 1);
+            const int lra = 32 * wave + c16, lrb = lra + 16;
+            const bf16x8 zah = lds_bf16x8(s_szh + lra * kArGp + go);
+            const bf16x8 zal = lds_bf16x8(s_szl + lra * kArGp + go);
+            const bf16x8 zbh = lds_bf16x8(s_szh + lrb * kArGp + go);
+            const bf16x8 zbl = lds_bf16x8(s_szl + lrb * kArGp + go);
+            const int cola = ar_col<kSilu>(r, wave, 0, c16);
+            const int colb = ar_col<kSilu>(r, wave, 1, c16);
 #pragma unroll
-            for (int jp = 0; jp < 2; ++jp) {
-                const int ja = kSilu ? jp : 2 * jp;
-                const int jb = kSilu ? jp + 2 : 2 * jp + 1;
-                const int lra = 64 * wave + 16 * ja + c16, lrb = 64 * wave + 16 * jb + c16;
-                const bf16x8 zah = lds_bf16x8(s_szh + lra * kArGp + go);
-                const bf16x8 zal = lds_bf16x8(s_szl + lra * kArGp + go);
-                const bf16x8 zbh = lds_bf16x8(s_szh + lrb * kArGp + go);
-                const bf16x8 zbl = lds_bf16x8(s_szl + lrb * kArGp + go);
-                const int cola = ar_col<kSilu>(r, wave, ja, c16);
-                const int colb = ar_col<kSilu>(r, wave, jb, c16);
+            for (int i = 0; i < NF; ++i) {
+                const bf16x8 sa = lds_bf16x8(sa_tab + (16 * i + c16) * kArGp + go);
+                v4f za = mfma_bf16_16x16x32(sa, zah, v4f{0.f, 0.f, 0.f, 0.f});
+                za = mfma_bf16_16x16x32(sa, zal, za);
+                v4f zb = mfma_bf16_16x16x32(sa, zbh, v4f{0.f, 0.f, 0.f, 0.f});
+                zb = mfma_bf16_16x16x32(sa, zbl, zb);
 #pragma unroll
-                for (int i = 0; i < NF; ++i) {
-                    const bf16x8 sa = lds_bf16x8(sa_tab + (16 * i + c16) * kArGp + go);
-                    v4f za = mfma_bf16_16x16x32(sa, zah, v4f{0.f, 0.f, 0.f, 0.f});
-                    za = mfma_bf16_16x16x32(sa, zal, za);
-                    v4f zb = mfma_bf16_16x16x32(sa, zbh, v4f{0.f, 0.f, 0.f, 0.f});
-                    zb = mfma_bf16_16x16x32(sa, zbl, zb);
-#pragma unroll
-                    for (int rr = 0; rr < 4; ++rr) {
-                        const int m = 16 * i + 4 * q + rr;
-                        if (!((vmask >> m) & 1)) continue;
-                        const float a = s_asc[m];
-                        const float va = a * (kNibbleScale * run[i][ja][rr] - za[rr]);
-                        const float vb = a * (kNibbleScale * run[i][jb][rr] - zb[rr]);
-                        const int64_t row_pad = row0 + m;
-                        if constexpr (kSilu) {
-                            reinterpret_cast<__half*>(p.out)[row_pad * ncols + cola] =
-                                silu_mul_h(__float2half(va), __float2half(vb));
-                        } else {
-                            reinterpret_cast<__half*>(p.out)[row_pad * p.N + cola] = __float2half(va);
-                            reinterpret_cast<__half*>(p.out)[row_pad * p.N + colb] = __float2half(vb);
-                        }
+                for (int rr = 0; rr < 4; ++rr) {
+                    const int m = 16 * i + 4 * q + rr;
+                    if (!((vmask >> m) & 1)) continue;
+                    const float a = s_asc[m];
+                    const float va = a * (kNibbleScale * run[i][0][rr] - za[rr]);
+                    const float vb = a * (kNibbleScale * run[i][1][rr] - zb[rr]);
+                    const int64_t row_pad = row0 + m;
+                    if constexpr (kSilu) {
+                        reinterpret_cast<__half*>(p.out)[row_pad * ncols + cola] = silu_mul_fast(va, vb);
+                    } else {
+                        reinterpret_cast<__half*>(p.out)[row_pad * p.N + cola] = __float2half(va);
+                        reinterpret_cast<__half*>(p.out)[row_pad * p.N + colb] = __float2half(vb);
                     }
                 }
             }
@@ -370,25 +400,31 @@ __global__ void __launch_bounds__(256, 1) prefill_ares_kernel(Params p) {
                 for (int j = 0; j < kArNT; ++j) run[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
         };
 
+        // Four steps per iteration (one pass of the ring; G % 4 == 0), so every iteration
+        // issues the same loads and the wait counts stay exact. The next range's tables are
+        // requested once per range, before its loop. The scheduling barriers keep each step's
+        // MFMAs next to the fold that frees their registers instead of hoisting later steps'
+        // MFMAs.
         for (int r = 0; r < nranges; ++r) {
-            // G % 4 == 0: the ring's four slots turn over once per iteration
+            if (r > 0) prefetch(r + 1);
             int g = 0;
             do {
                 consume(g, S0{});
                 issue(S0{});
+                __builtin_amdgcn_sched_barrier(0);
                 consume(g + 1, S1{});
                 issue(S1{});
+                __builtin_amdgcn_sched_barrier(0);
                 consume(g + 2, S2{});
                 issue(S2{});
+                __builtin_amdgcn_sched_barrier(0);
                 consume(g + 3, S3{});
                 issue(S3{});
+                __builtin_amdgcn_sched_barrier(0);
                 g += 4;
             } while (g < G);
             epilogue(r);
-            if (r + 1 < nranges) {
-                build(r + 1);
-                prefetch(r + 2);
-            }
+            if (r + 1 < nranges) build(r + 1);
         }
     };
     switch (nfl) {
@@ -415,7 +451,7 @@ int launch_ares_t(const Params& p, hipStream_t s) {
     // a multiple of 8 work-groups covers every tile under the XCD-aware order
     const int64_t tiles = (p.P + kArBM - 1) / kArBM;
     const unsigned grid = (unsigned)((tiles + kArXcds - 1) / kArXcds * kArXcds);
-    prefill_ares_kernel<EPI, FRAG><<<grid, 256, lds, s>>>(p);
+    prefill_ares_kernel<EPI, FRAG><<<grid, kArThreads, lds, s>>>(p);
     return check_launch("prefill_ares_kernel");
 }
 
