@@ -176,11 +176,19 @@ __global__ void __launch_bounds__(kAlignThreads) align_scan_kernel(
     __shared__ int warp_tot[kAlignThreads / 64];
     const int tid = threadIdx.x;
     if (tid < E) {
+        // exclusive prefix over the chunks, 16 chunk counts requested at a time
+        constexpr int kBatch = 16;
         int run = 0;
-        for (int c = 0; c < nchunks; ++c) {
-            const int v = counts[(int64_t)c * E + tid];
-            counts[(int64_t)c * E + tid] = run;
-            run += v;
+        for (int c0 = 0; c0 < nchunks; c0 += kBatch) {
+            int v[kBatch];
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u)
+                v[u] = c0 + u < nchunks ? counts[(int64_t)(c0 + u) * E + tid] : 0;
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u) {
+                if (c0 + u < nchunks) counts[(int64_t)(c0 + u) * E + tid] = run;
+                run += v[u];
+            }
         }
         cnt[tid] = run;
     }
