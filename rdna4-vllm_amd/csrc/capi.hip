@@ -277,10 +277,13 @@ int moe_apply_impl(const void* x, int x_dtype, int64_t T, int64_t H, int64_t int
     if (rc) return rc;
     stage_mark(4, s);
     // act-quant of h over real rows only, once per row (quantising inside the decode GEMV
-    // would repeat it for every work-group that reads the row)
+    // would repeat it for every work-group that reads the row); the activation-resident
+    // prefill tiles quantise their own rows instead (a tile is the only reader of its rows)
     const bool gemv2 = pl.decode && !e2m1 && gemv_supported(inter, group_size);
-    if ((rc = launch_act_quant(h, false, pl.P, inter, hq, s2, true, s, sti, ntp, numel,
-                               pf2 ? gs2 : nullptr)))
+    const bool ares2 = pf2 && prefill_ares_supported(inter, H, group_size, e2m1, pl.block_m, Epi::kHalf);
+    const bool ares2_quant = ares2 && prefill_ares_quantises_rows(inter, Epi::kHalf);
+    if (!ares2_quant && (rc = launch_act_quant(h, false, pl.P, inter, hq, s2, true, s, sti, ntp,
+                                               numel, pf2 ? gs2 : nullptr)))
         return rc;
     stage_mark(5, s);
     // gemm2 (identity gather) -> per-slot rows (decode) or scatter (prefill)
@@ -292,14 +295,13 @@ int moe_apply_impl(const void* x, int x_dtype, int64_t T, int64_t H, int64_t int
     g2.epi = pl.decode ? Epi::kSlotF32 : Epi::kHalf; g2.out = pl.decode ? (void*)acc : (void*)y;
     g2.topk_weights = topk_weights; g2.out_top_k = top_k;
     g2.x = h; g2.x_bf16 = false;
-    g2.x_fp8 = hq;
-    g2.act_scales = s2;
-    g2.act_group_sums = pf2 ? gs2 : nullptr;
+    g2.x_fp8 = ares2_quant ? nullptr : hq;
+    g2.act_scales = ares2_quant ? nullptr : s2;
+    g2.act_group_sums = pf2 && !ares2_quant ? gs2 : nullptr;
     g2.w_frag = frag;
     if (!mfma) rc = launch_grouped_scalar(g2, s);
     else if (gemv2) rc = launch_grouped_gemv(g2, s);
-    else if (pf2 && prefill_ares_supported(inter, H, group_size, e2m1, pl.block_m, Epi::kHalf))
-        rc = launch_grouped_prefill_ares(g2, s);
+    else if (ares2) rc = launch_grouped_prefill_ares(g2, s);
     else if (pf2) rc = launch_grouped_prefill(g2, s);
     else rc = launch_grouped_mfma(g2, s);
     if (rc) return rc;

@@ -42,6 +42,7 @@ constexpr int kArNT = 2;                        // 16-column B fragments per wav
 constexpr int kArBN = kArWaves * kArNT * 16;    // 256 weight rows per range
 constexpr int kArD = 4;                         // B steps in flight per wave
 constexpr int kArMaxK = 2048;                   // activation tile must fit LDS
+constexpr int kArMaxKAq = 1024;                 // fp16 rows quantised in the prologue
 constexpr int kArGp = 16;                       // group slots of the per-range tables
 constexpr int kArXcds = 8;                      // work-groups go round-robin to 8 XCDs
 
@@ -262,7 +263,77 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
 
     // ---- prologue: range 0's tables, the activation tile, row group sums, the ring ----
     prefetch(0);
-    {
+    bool quantised = false;
+    if constexpr (!kSilu) {
+        if (p.xq == nullptr) {
+            // fp16 rows in (the tile owns its rows: each is read by this work-group only):
+            // wave w quantises tile rows 8w .. 8w + 7 as act_quant_kernel does (s =
+            // max(absmax / 448, 1e-8), e4m3 RNE of x / s in k8-interleaved order, per-group
+            // sums of the e4m3 values by the same lane tree), straight into the LDS tile
+            quantised = true;
+            constexpr int kRowsPerWave = kArBM / kArWaves;
+            const int npass = K / 512;                     // 1 or 2 (K <= kArMaxKAq)
+            const __half* xh = reinterpret_cast<const __half*>(p.xh);
+            uint4 raw[kRowsPerWave][kArMaxKAq / 512];
+#pragma unroll
+            for (int u = 0; u < kRowsPerWave; ++u) {
+                const int sr = src_of(kRowsPerWave * wave + u);
+#pragma unroll
+                for (int ps = 0; ps < kArMaxKAq / 512; ++ps)
+                    raw[u][ps] = *reinterpret_cast<const uint4*>(
+                        xh + (int64_t)sr * K + std::min(ps, npass - 1) * 512 + lane * 8);
+            }
+#pragma unroll
+            for (int u = 0; u < kRowsPerWave; ++u) {
+                const int m = kRowsPerWave * wave + u;
+                auto val = [&](int ps, int j) {
+                    const uint4 w4 = raw[u][ps];
+                    const uint32_t wd = j < 2 ? w4.x : j < 4 ? w4.y : j < 6 ? w4.z : w4.w;
+                    return __half2float(__ushort_as_half((uint16_t)((j & 1) ? wd >> 16 : wd & 0xFFFF)));
+                };
+                float amax = 0.0f;
+#pragma unroll
+                for (int ps = 0; ps < kArMaxKAq / 512; ++ps) {
+                    if (ps >= npass) break;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(val(ps, j)));
+                }
+                amax = wave_max(amax);
+                const float sc = act_scale_from_absmax(amax);
+                if (lane == 0) s_asc[m] = sc;
+                const float inv = 1.0f / sc;
+#pragma unroll
+                for (int ps = 0; ps < kArMaxKAq / 512; ++ps) {
+                    if (ps >= npass) break;
+                    float v[8];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) v[j] = val(ps, j) * inv;
+                    const uint32_t lo = pack4_e4m3(v[0], v[2], v[4], v[6]);
+                    const uint32_t hi = pack4_e4m3(v[1], v[3], v[5], v[7]);
+                    const int k = ps * 512 + lane * 8;
+                    *reinterpret_cast<uint2*>(s_a + ar_a_off(m, k / kGroup, (k % kGroup) / 16) + 8 * (lane & 1)) =
+                        make_uint2(lo, hi);
+                    float t = 0.f;
+#pragma unroll
+                    for (int b = 0; b < 4; ++b)
+                        t += e4m3_to_f32((lo >> (8 * b)) & 0xFF) + e4m3_to_f32((hi >> (8 * b)) & 0xFF);
+                    t = lane_allreduce<4>(t, SumOp{});
+                    if ((lane & 15) == 0) {
+                        const __bf16 h = (__bf16)t;
+                        s_sah[m * kArGp + k / kGroup] = h;
+                        s_sal[m * kArGp + k / kGroup] = (__bf16)(t - (float)h);
+                    }
+                }
+            }
+            for (int i = tid; i < kArBM * kArGp; i += kArThreads) {   // groups >= G are 0
+                if (i % kArGp >= G) {
+                    s_sah[i] = (__bf16)0.f;
+                    s_sal[i] = (__bf16)0.f;
+                }
+            }
+        }
+    }
+    if (!quantised) {
         // 16-byte chunk c of the tile: row c / (K / 16), bytes (c % (K / 16)) * 16
         const int cpr = K / 16;                         // chunks per row
         const int total = kArBM * cpr;                  // multiple of 512 (K % 128 == 0)
@@ -466,14 +537,23 @@ bool prefill_ares_supported(int64_t K, int64_t N, int64_t group_size, bool e2m1,
     return false;
 }
 
+bool prefill_ares_quantises_rows(int64_t K, Epi epi) {
+    return epi == Epi::kHalf && K <= kArMaxKAq;
+}
+
 int launch_grouped_prefill_ares(const GroupedArgs& a, hipStream_t s) {
     const Params p = make_params(a);
     if (p.P == 0) return W4A8_OK;
-    if (!prefill_ares_supported(a.K, a.N, a.group_size, a.e2m1, a.block_m, a.epi) || p.xq == nullptr ||
-        p.asum == nullptr || p.asc == nullptr || a.x_rows * a.K >= ((int64_t)1 << 31)) {
+    // rows come prequantised (x_fp8 with scales and group sums), or, for fp16 output and
+    // K <= 1024, as fp16 rows the tile quantises itself
+    const bool prequant = p.xq != nullptr && p.asum != nullptr && p.asc != nullptr;
+    const bool self_quant = p.xq == nullptr && p.xh != nullptr && !a.x_bf16 &&
+                            a.epi == Epi::kHalf && a.K <= kArMaxKAq;
+    if (!prefill_ares_supported(a.K, a.N, a.group_size, a.e2m1, a.block_m, a.epi) ||
+        !(prequant || self_quant) || a.x_rows * a.K >= ((int64_t)1 << 31)) {
         set_error("prefill (activation-resident): needs g128 int4 weights, K % 512 == 0 and "
-                  "K <= 2048, output columns in whole 256-row ranges, block_m % 64 == 0, "
-                  "prequantised rows with group sums, fp16 out");
+                  "K <= 2048, output columns in whole 256-row ranges, block_m % 64 == 0, fp16 "
+                  "out, and prequantised rows with group sums (or fp16 rows, fp16 out, K <= 1024)");
         return W4A8_ERR_INVALID;
     }
     if (a.w_frag && (a.N % 16 != 0 || (a.epi == Epi::kSiluHalf && (a.N / 2) % 16 != 0))) {

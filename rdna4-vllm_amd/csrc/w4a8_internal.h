@@ -124,6 +124,9 @@ int launch_grouped_gemv(const GroupedArgs& a, hipStream_t stream);   // decode G
 bool prefill_ares_supported(int64_t K, int64_t N, int64_t group_size, bool e2m1, int64_t block_m,
                             Epi epi);
 int launch_grouped_prefill_ares(const GroupedArgs& a, hipStream_t stream);
+// The activation-resident tiles can take fp16 rows (x, no x_fp8) and quantise them in their
+// prologue, bit-identical to act_quant_kernel with group sums (each tile owns its rows).
+bool prefill_ares_quantises_rows(int64_t K, Epi epi);
 // (E, N, K/8) int32 op layout -> fragment layout: per expert, 16-row tile t and 128-wide
 // group g, a 1 KB block whose 16-byte lane l holds row 16t + l % 16, k in
 // [128g + 32 (l / 16), +32) (the MFMA B operand of lane l). N % 16 == 0, K % 128 == 0.
