@@ -234,10 +234,14 @@ int moe_apply_impl(const void* x, int x_dtype, int64_t T, int64_t H, int64_t int
     const bool pf2 = !pl.decode && mfma && prefill_supported(inter, group_size, e2m1);
     // router: one wave per token over the whole grid (folding it into the align launch
     // would serialise the tokens on the align work-group)
+    // many-token schedule: the routing waves also quantise x (one launch less)
+    const bool route_quant = logits != nullptr && !(pl.decode && numel <= kAlignSmallMax);
     if (logits != nullptr)
         if (int rc = launch_topk_softmax(logits, T, E, top_k, renormalize,
                                          const_cast<float*>(topk_weights),
-                                         const_cast<int32_t*>(topk_ids), s))
+                                         const_cast<int32_t*>(topk_ids), s,
+                                         route_quant ? x : nullptr, bf16, H, xq, s1,
+                                         pf1 ? gs1 : nullptr))
             return rc;
     stage_mark(0, s);
     if (pl.decode && numel <= kAlignSmallMax) {
@@ -251,9 +255,10 @@ int moe_apply_impl(const void* x, int x_dtype, int64_t T, int64_t H, int64_t int
                                   ntp, aws, abytes, s, s2r))
             return rc;
         stage_mark(1, s);
-        if (int rc = launch_act_quant(x, bf16, T, H, xq, s1, true, s, nullptr, nullptr, 0,
-                                      pf1 ? gs1 : nullptr))
-            return rc;
+        if (!route_quant)
+            if (int rc = launch_act_quant(x, bf16, T, H, xq, s1, true, s, nullptr, nullptr, 0,
+                                          pf1 ? gs1 : nullptr))
+                return rc;
     }
     stage_mark(2, s);
     stage_mark(3, s);

@@ -311,15 +311,29 @@ __device__ __forceinline__ void topk_one_token(const float* __restrict__ l, int 
     }
 }
 
+// RowQuant: optional act-quant of the token's activation row by the same wave, after its
+// routing (act_quant_kernel's arithmetic; saves a launch for the many-token schedule).
+struct RowQuant {
+    const void* x = nullptr;   // (T, K) fp16 / bf16, or null: no quantisation
+    bool bf16 = false;
+    int K = 0;
+    uint8_t* xq = nullptr;     // (T, K) k8-interleaved e4m3
+    float* xs = nullptr;       // (T,)
+    float* gsum = nullptr;     // (T, K / 128) or null
+};
+
 template <int NV>
 __global__ void __launch_bounds__(256) topk_softmax_kernel(
     const float* __restrict__ logits, int64_t T, int E, int top_k, bool renorm,
-    float* __restrict__ tw, int32_t* __restrict__ tids) {
+    float* __restrict__ tw, int32_t* __restrict__ tids, RowQuant rq) {
     const int lane = threadIdx.x & 63;
     const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (t >= T) return;
     topk_one_token<NV>(logits + t * E, E, top_k, renorm, tw + t * top_k, tids + t * top_k,
                        nullptr, lane);
+    if (rq.x == nullptr) return;
+    if (rq.bf16) quantize_row<true>(rq.x, t, rq.K, rq.xq, rq.xs, true, rq.gsum, lane);
+    else quantize_row<false>(rq.x, t, rq.K, rq.xq, rq.xs, true, rq.gsum, lane);
 }
 
 // Decode prologue in one launch: work-group 0 builds the align layout (numel <= kChunk),
@@ -388,18 +402,27 @@ int launch_align(const int32_t* ids, int64_t numel, int64_t E, int64_t block_m,
 }
 
 int launch_topk_softmax(const float* logits, int64_t T, int64_t E, int64_t top_k, bool renorm,
-                        float* w, int32_t* ids, hipStream_t stream) {
+                        float* w, int32_t* ids, hipStream_t stream, const void* x, bool x_bf16,
+                        int64_t K, uint8_t* xq, float* xs, float* gsum) {
     if (E > 64 * kRouterMaxPerLane || top_k > 64 || top_k > E) {
         set_error("topk_softmax: need E <= 1024 and top_k <= min(64, E)");
         return W4A8_ERR_INVALID;
     }
     if (T == 0) return W4A8_OK;
+    RowQuant rq;
+    if (x != nullptr) {
+        if (K <= 0 || K % 8 != 0 || xq == nullptr || xs == nullptr || (gsum && K % 128 != 0)) {
+            set_error("topk_softmax: row quantisation needs K % 8 == 0 (K % 128 with group sums)");
+            return W4A8_ERR_INVALID;
+        }
+        rq.x = x; rq.bf16 = x_bf16; rq.K = (int)K; rq.xq = xq; rq.xs = xs; rq.gsum = gsum;
+    }
     const dim3 grid((unsigned)((T + 3) / 4));
-    if (E <= 64) topk_softmax_kernel<1><<<grid, 256, 0, stream>>>(logits, T, (int)E, (int)top_k, renorm, w, ids);
-    else if (E <= 128) topk_softmax_kernel<2><<<grid, 256, 0, stream>>>(logits, T, (int)E, (int)top_k, renorm, w, ids);
-    else if (E <= 256) topk_softmax_kernel<4><<<grid, 256, 0, stream>>>(logits, T, (int)E, (int)top_k, renorm, w, ids);
-    else if (E <= 512) topk_softmax_kernel<8><<<grid, 256, 0, stream>>>(logits, T, (int)E, (int)top_k, renorm, w, ids);
-    else topk_softmax_kernel<16><<<grid, 256, 0, stream>>>(logits, T, (int)E, (int)top_k, renorm, w, ids);
+    if (E <= 64) topk_softmax_kernel<1><<<grid, 256, 0, stream>>>(logits, T, (int)E, (int)top_k, renorm, w, ids, rq);
+    else if (E <= 128) topk_softmax_kernel<2><<<grid, 256, 0, stream>>>(logits, T, (int)E, (int)top_k, renorm, w, ids, rq);
+    else if (E <= 256) topk_softmax_kernel<4><<<grid, 256, 0, stream>>>(logits, T, (int)E, (int)top_k, renorm, w, ids, rq);
+    else if (E <= 512) topk_softmax_kernel<8><<<grid, 256, 0, stream>>>(logits, T, (int)E, (int)top_k, renorm, w, ids, rq);
+    else topk_softmax_kernel<16><<<grid, 256, 0, stream>>>(logits, T, (int)E, (int)top_k, renorm, w, ids, rq);
     return check_launch("topk_softmax_kernel");
 }
 

@@ -51,8 +51,12 @@ int launch_dequant(const int32_t* w, const int32_t* z, int64_t E, int64_t N, int
                    int64_t gs, bool e2m1, uint8_t* out, hipStream_t stream);
 int launch_silu_and_mul(const void* in, int64_t rows, int64_t inter, void* out,
                         hipStream_t stream);
+// x non-null: the routing wave of token t also quantises row t of x (act_quant_kernel's
+// arithmetic, k8-interleaved, group sums when gsum is non-null).
 int launch_topk_softmax(const float* logits, int64_t T, int64_t E, int64_t top_k,
-                        bool renorm, float* w, int32_t* ids, hipStream_t stream);
+                        bool renorm, float* w, int32_t* ids, hipStream_t stream,
+                        const void* x = nullptr, bool x_bf16 = false, int64_t K = 0,
+                        uint8_t* xq = nullptr, float* xs = nullptr, float* gsum = nullptr);
 size_t align_workspace_bytes(int64_t numel, int64_t num_experts);
 // Decode prologue in one launch (numel <= 1024): the single-work-group align plus per-row
 // act-quant of x (k8-interleaved) with optional group sums.
