@@ -17,6 +17,37 @@ __device__ __forceinline__ float load_act(const void* x, int64_t i) {
     }
 }
 
+// Element j (0..7) of 8 consecutive fp16 / bf16 activations packed in a uint4, as
+// load_act would read it.
+template <bool BF16>
+__device__ __forceinline__ float act_from_u4(const uint4& v, int j) {
+    const uint32_t w = j < 2 ? v.x : j < 4 ? v.y : j < 6 ? v.z : v.w;
+    const uint16_t b = (j & 1) ? (uint16_t)(w >> 16) : (uint16_t)(w & 0xFFFF);
+    if constexpr (BF16) {
+        const float f = __uint_as_float((uint32_t)b << 16);
+        return __half2float(__float2half(f));
+    } else {
+        return __half2float(__ushort_as_half(b));
+    }
+}
+
+template <bool BF16>
+__device__ __forceinline__ void quantize_row_scalar(const void* __restrict__ x, int64_t row, int K,
+                                                    uint8_t* __restrict__ q,
+                                                    float* __restrict__ scales, bool k8,
+                                                    float* __restrict__ gsum, int lane);
+
+// Group sum of one 512-wide pass (lanes 16j..16j+15 hold group k/128): fixed-order tree.
+__device__ __forceinline__ void row_group_sum(uint32_t lo, uint32_t hi, int64_t row, int K, int k,
+                                              float* __restrict__ gsum, int lane) {
+    float t = 0.f;
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+        t += e4m3_to_f32((lo >> (8 * b)) & 0xFF) + e4m3_to_f32((hi >> (8 * b)) & 0xFF);
+    t = lane_allreduce<4>(t, SumOp{});
+    if ((lane & 15) == 0 && k < K) gsum[row * (K / 128) + k / 128] = t;
+}
+
 // One wave quantises row `row` (moe_kernel.hip:87-127): s = max(absmax/448, 1e-8),
 // q = e4m3_RNE(x * (1/s)). k8: bytes in the kernels' k8-interleaved order. gsum (optional,
 // K % 128 == 0): per 128-wide group, the sum of the e4m3 values.
@@ -24,6 +55,63 @@ template <bool BF16>
 __device__ __forceinline__ void quantize_row(const void* __restrict__ x, int64_t row, int K,
                                              uint8_t* __restrict__ q, float* __restrict__ scales,
                                              bool k8, float* __restrict__ gsum, int lane) {
+    // Rows of up to 4096 values with 16-byte aligned starts: one 16-byte load per lane and
+    // 512-wide pass, the row kept in registers between the absmax and the quantisation.
+    // Same arithmetic as the element-wise form below, so the same bytes.
+    constexpr int kMaxPass = 8;
+    const int npass = (K + 511) / 512;
+    const char* rowp = reinterpret_cast<const char*>(x) + row * K * 2;
+    if (npass > kMaxPass || (reinterpret_cast<uintptr_t>(rowp) & 15) != 0) {
+        quantize_row_scalar<BF16>(x, row, K, q, scales, k8, gsum, lane);
+        return;
+    }
+    uint4 v[kMaxPass];
+#pragma unroll
+    for (int ps = 0; ps < kMaxPass; ++ps) {
+        const int k = ps * 512 + lane * 8;
+        v[ps] = make_uint4(0, 0, 0, 0);
+        if (ps < npass && k < K) v[ps] = *reinterpret_cast<const uint4*>(rowp + k * 2);
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int ps = 0; ps < kMaxPass; ++ps) {
+        if (ps >= npass) break;
+        if (ps * 512 + lane * 8 >= K) continue;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(act_from_u4<BF16>(v[ps], j)));
+    }
+    amax = wave_max(amax);
+    const float s = act_scale_from_absmax(amax);
+    if (lane == 0) scales[row] = s;
+    const float inv = 1.0f / s;
+    const int64_t base = row * K;
+#pragma unroll
+    for (int ps = 0; ps < kMaxPass; ++ps) {
+        if (ps >= npass) break;
+        const int k = ps * 512 + lane * 8;
+        uint32_t lo = 0, hi = 0;
+        if (k < K) {
+            float f[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) f[j] = act_from_u4<BF16>(v[ps], j) * inv;
+            if (k8) {
+                lo = pack4_e4m3(f[0], f[2], f[4], f[6]);
+                hi = pack4_e4m3(f[1], f[3], f[5], f[7]);
+            } else {
+                lo = pack4_e4m3(f[0], f[1], f[2], f[3]);
+                hi = pack4_e4m3(f[4], f[5], f[6], f[7]);
+            }
+            *reinterpret_cast<uint2*>(q + base + k) = make_uint2(lo, hi);
+        }
+        if (gsum != nullptr) row_group_sum(lo, hi, row, K, k, gsum, lane);
+    }
+}
+
+template <bool BF16>
+__device__ __forceinline__ void quantize_row_scalar(const void* __restrict__ x, int64_t row, int K,
+                                                    uint8_t* __restrict__ q,
+                                                    float* __restrict__ scales, bool k8,
+                                                    float* __restrict__ gsum, int lane) {
     const int64_t base = row * K;
     float amax = 0.0f;
     for (int k = lane * 8; k < K; k += 64 * 8) {
@@ -52,15 +140,7 @@ __device__ __forceinline__ void quantize_row(const void* __restrict__ x, int64_t
             }
             *reinterpret_cast<uint2*>(q + base + k) = make_uint2(lo, hi);
         }
-        if (gsum != nullptr) {
-            // lanes 16j..16j+15 hold group k/128 of this pass: fixed-order tree sum
-            float t = 0.f;
-#pragma unroll
-            for (int b = 0; b < 4; ++b)
-                t += e4m3_to_f32((lo >> (8 * b)) & 0xFF) + e4m3_to_f32((hi >> (8 * b)) & 0xFF);
-            t = lane_allreduce<4>(t, SumOp{});
-            if ((lane & 15) == 0 && k < K) gsum[row * (K / 128) + k / 128] = t;
-        }
+        if (gsum != nullptr) row_group_sum(lo, hi, row, K, k, gsum, lane);
     }
 }
 

@@ -50,6 +50,21 @@ def test_act_quant_bit_exact(k8, K):
     assert np.array_equal(q.cpu().numpy(), qo)
 
 
+@pytest.mark.parametrize("K", [512, 2048])
+def test_act_quant_misaligned_rows_bit_exact(K):
+    """Rows whose start is not 16-byte aligned take the element-wise loads: same bytes."""
+    r = rng(K + 1)
+    x = (r.standard_normal((9, K)) * 3).astype(np.float16)
+    buf = torch.zeros(9 * K + 4, dtype=torch.float16, device=DEV)
+    buf[4:].copy_(torch.from_numpy(x.reshape(-1)).to(DEV))
+    xv = buf[4:].view(9, K)                     # data pointer 8 bytes past an aligned start
+    assert xv.data_ptr() % 16 == 8
+    q, s = W.act_quant_fp8(xv, k8_interleave=False)
+    qo, so = O.act_quant(x)
+    assert np.array_equal(s.cpu().numpy(), so)
+    assert np.array_equal(q.cpu().numpy(), qo)
+
+
 @pytest.mark.parametrize("asym", [True, False])
 def test_dequant_bit_exact_all_zero_points(asym):
     r = rng(5)
