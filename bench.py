@@ -286,8 +286,16 @@ def main():
         achieved = g1_flops / (g1_ms * 1e-3) / 1e12
         roof = dict(bound="mfma", achieved=round(achieved, 1), peak=FP8_PEAK_TFLOPS,
                     unit="TFLOP/s", frac=round(achieved / FP8_PEAK_TFLOPS, 4), traffic=None,
-                    kernel="prefill_mfma_kernel<kSiluHalf, 4> (gemm1+SiLU)",
+                    kernel="prefill_ares_kernel<kSiluHalf> (gemm1+SiLU)",
                     algorithmic_flops=g1_flops, avg_ms=round(g1_ms, 5))
+    # HBM bytes per launch of that kernel, measured with rocprofv3 --pmc on this workload and
+    # weight layout (profiles/roofline_traffic.json); null for other configurations
+    tr_file = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "roofline_traffic.json")
+    if os.path.exists(tr_file) and args.layout == "fragments":
+        tr = json.load(open(tr_file)).get(args.config)
+        if tr is not None:
+            roof["traffic"] = tr["traffic_bytes"]
+            roof["traffic_source"] = "profiles/roofline_traffic.json (" + tr["kernel"] + ")"
     layer_s = ms_per_step * 1e-3
     value = T / layer_s
 
