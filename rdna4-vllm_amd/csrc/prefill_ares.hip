@@ -261,110 +261,120 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
         *reinterpret_cast<uint4*>(s_szl + lrow * kArGp + 8 * th) = make_uint4(szl[0], szl[1], szl[2], szl[3]);
     };
 
-    // ---- prologue: range 0's tables, the activation tile, row group sums, the ring ----
+    // ---- prologue. Loads first, in this order: range 0's tables, the activation rows (and
+    //      their scales and group sums), the first four weight steps; waiting for the rows
+    //      then leaves the weights in flight behind the LDS writes and the table build ----
     prefetch(0);
-    bool quantised = false;
-    if constexpr (!kSilu) {
-        if (p.xq == nullptr) {
-            // fp16 rows in (the tile owns its rows: each is read by this work-group only):
-            // wave w quantises tile rows 8w .. 8w + 7 as act_quant_kernel does (s =
-            // max(absmax / 448, 1e-8), e4m3 RNE of x / s in k8-interleaved order, per-group
-            // sums of the e4m3 values by the same lane tree), straight into the LDS tile
-            quantised = true;
-            constexpr int kRowsPerWave = kArBM / kArWaves;
-            const int npass = K / 512;                     // 1 or 2 (K <= kArMaxKAq)
-            const __half* xh = reinterpret_cast<const __half*>(p.xh);
-            uint4 raw[kRowsPerWave][kArMaxKAq / 512];
+    constexpr int kRowsPerWave = kArBM / kArWaves;
+    constexpr int kAqPass = kArMaxKAq / 512;
+    constexpr int kMaxChunks = kArMaxK / 16 * kArBM / kArThreads;   // 16-byte chunks per thread
+    const bool self_quant = !kSilu && p.xq == nullptr;
+    const int cpr = K / 16;                             // chunks per row
+    const int total = kArBM * cpr;                      // multiple of 512 (K % 128 == 0)
+    uint4 raw[kRowsPerWave][kAqPass];                   // fp16 rows (self-quantising tiles)
+    uint4 va[kMaxChunks];                               // e4m3 tile chunks (prequantised rows)
+    float asv[kArBM * kArGp / kArThreads];              // row group sums
+    float ascv = 0.f;
+    if (self_quant) {
+        // fp16 rows in (the tile owns its rows: each is read by this work-group only);
+        // wave w quantises tile rows 8w .. 8w + 7 below
+        const int npass = K / 512;                      // 1 or 2 (K <= kArMaxKAq)
+        const __half* xh = reinterpret_cast<const __half*>(p.xh);
 #pragma unroll
-            for (int u = 0; u < kRowsPerWave; ++u) {
-                const int sr = src_of(kRowsPerWave * wave + u);
+        for (int u = 0; u < kRowsPerWave; ++u) {
+            const int sr = src_of(kRowsPerWave * wave + u);
 #pragma unroll
-                for (int ps = 0; ps < kArMaxKAq / 512; ++ps)
-                    raw[u][ps] = *reinterpret_cast<const uint4*>(
-                        xh + (int64_t)sr * K + std::min(ps, npass - 1) * 512 + lane * 8);
-            }
-#pragma unroll
-            for (int u = 0; u < kRowsPerWave; ++u) {
-                const int m = kRowsPerWave * wave + u;
-                auto val = [&](int ps, int j) {
-                    const uint4 w4 = raw[u][ps];
-                    const uint32_t wd = j < 2 ? w4.x : j < 4 ? w4.y : j < 6 ? w4.z : w4.w;
-                    return __half2float(__ushort_as_half((uint16_t)((j & 1) ? wd >> 16 : wd & 0xFFFF)));
-                };
-                float amax = 0.0f;
-#pragma unroll
-                for (int ps = 0; ps < kArMaxKAq / 512; ++ps) {
-                    if (ps >= npass) break;
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(val(ps, j)));
-                }
-                amax = wave_max(amax);
-                const float sc = act_scale_from_absmax(amax);
-                if (lane == 0) s_asc[m] = sc;
-                const float inv = 1.0f / sc;
-#pragma unroll
-                for (int ps = 0; ps < kArMaxKAq / 512; ++ps) {
-                    if (ps >= npass) break;
-                    float v[8];
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) v[j] = val(ps, j) * inv;
-                    const uint32_t lo = pack4_e4m3(v[0], v[2], v[4], v[6]);
-                    const uint32_t hi = pack4_e4m3(v[1], v[3], v[5], v[7]);
-                    const int k = ps * 512 + lane * 8;
-                    *reinterpret_cast<uint2*>(s_a + ar_a_off(m, k / kGroup, (k % kGroup) / 16) + 8 * (lane & 1)) =
-                        make_uint2(lo, hi);
-                    float t = 0.f;
-#pragma unroll
-                    for (int b = 0; b < 4; ++b)
-                        t += e4m3_to_f32((lo >> (8 * b)) & 0xFF) + e4m3_to_f32((hi >> (8 * b)) & 0xFF);
-                    t = lane_allreduce<4>(t, SumOp{});
-                    if ((lane & 15) == 0) {
-                        const __bf16 h = (__bf16)t;
-                        s_sah[m * kArGp + k / kGroup] = h;
-                        s_sal[m * kArGp + k / kGroup] = (__bf16)(t - (float)h);
-                    }
-                }
-            }
-            for (int i = tid; i < kArBM * kArGp; i += kArThreads) {   // groups >= G are 0
-                if (i % kArGp >= G) {
-                    s_sah[i] = (__bf16)0.f;
-                    s_sal[i] = (__bf16)0.f;
-                }
-            }
+            for (int ps = 0; ps < kAqPass; ++ps)
+                raw[u][ps] = *reinterpret_cast<const uint4*>(
+                    xh + (int64_t)sr * K + std::min(ps, npass - 1) * 512 + lane * 8);
         }
-    }
-    if (!quantised) {
-        // 16-byte chunk c of the tile: row c / (K / 16), bytes (c % (K / 16)) * 16
-        const int cpr = K / 16;                         // chunks per row
-        const int total = kArBM * cpr;                  // multiple of 512 (K % 128 == 0)
-        for (int c0 = 0; c0 < total; c0 += kArThreads * 8) {
-            uint4 v[8];
+    } else {
+        // chunk c: row c / cpr, bytes (c % cpr) * 16; chunks past the tile repeat the last
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const int c = min(c0 + u * kArThreads + tid, total - 1);
-                v[u] = *reinterpret_cast<const uint4*>(p.xq + (int64_t)src_of(c / cpr) * K + (c % cpr) * 16);
-            }
+        for (int u = 0; u < kMaxChunks; ++u) {
+            const int c = min(u * kArThreads + tid, total - 1);
+            va[u] = *reinterpret_cast<const uint4*>(p.xq + (int64_t)src_of(c / cpr) * K + (c % cpr) * 16);
+        }
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const int c = c0 + u * kArThreads + tid;
-                if (c < total)
-                    *reinterpret_cast<uint4*>(s_a + ar_a_off(c / cpr, (c % cpr) >> 3, c & 7)) = v[u];
-            }
+        for (int j = 0; j < kArBM * kArGp / kArThreads; ++j) {   // row sums; groups >= G are 0
+            const int i = j * kArThreads + tid;
+            const int sr = src_of(i / kArGp);
+            asv[j] = i % kArGp < G ? p.asum[(int64_t)sr * G + i % kArGp] : 0.f;
         }
-        for (int i = tid; i < kArBM * kArGp; i += kArThreads) {   // row sums; groups >= G are 0
-            const int r = i / kArGp, g = i % kArGp;
-            const int sr = src_of(r);
-            const float v = g < G ? p.asum[(int64_t)sr * G + g] : 0.f;
-            const __bf16 h = (__bf16)v;
-            s_sah[i] = h;
-            s_sal[i] = (__bf16)(v - (float)h);
-        }
-        if (wave == 0) s_asc[lane] = src >= 0 ? p.asc[src] : 0.f;
+        if (wave == 0 && src >= 0) ascv = p.asc[src];
     }
     issue(S0{});
     issue(S1{});
     issue(S2{});
     issue(S3{});
+    if (self_quant) {
+        // as act_quant_kernel: s = max(absmax / 448, 1e-8), e4m3 RNE of x / s in k8-interleaved
+        // order, per-group sums of the e4m3 values by the same lane tree; straight into LDS
+        const int npass = K / 512;
+#pragma unroll
+        for (int u = 0; u < kRowsPerWave; ++u) {
+            const int m = kRowsPerWave * wave + u;
+            auto val = [&](int ps, int j) {
+                const uint4 w4 = raw[u][ps];
+                const uint32_t wd = j < 2 ? w4.x : j < 4 ? w4.y : j < 6 ? w4.z : w4.w;
+                return __half2float(__ushort_as_half((uint16_t)((j & 1) ? wd >> 16 : wd & 0xFFFF)));
+            };
+            float amax = 0.0f;
+#pragma unroll
+            for (int ps = 0; ps < kAqPass; ++ps) {
+                if (ps >= npass) break;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(val(ps, j)));
+            }
+            amax = wave_max(amax);
+            const float sc = act_scale_from_absmax(amax);
+            if (lane == 0) s_asc[m] = sc;
+            const float inv = 1.0f / sc;
+#pragma unroll
+            for (int ps = 0; ps < kAqPass; ++ps) {
+                if (ps >= npass) break;
+                float v[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) v[j] = val(ps, j) * inv;
+                const uint32_t lo = pack4_e4m3(v[0], v[2], v[4], v[6]);
+                const uint32_t hi = pack4_e4m3(v[1], v[3], v[5], v[7]);
+                const int k = ps * 512 + lane * 8;
+                *reinterpret_cast<uint2*>(s_a + ar_a_off(m, k / kGroup, (k % kGroup) / 16) + 8 * (lane & 1)) =
+                    make_uint2(lo, hi);
+                float t = 0.f;
+#pragma unroll
+                for (int b = 0; b < 4; ++b)
+                    t += e4m3_to_f32((lo >> (8 * b)) & 0xFF) + e4m3_to_f32((hi >> (8 * b)) & 0xFF);
+                t = lane_allreduce<4>(t, SumOp{});
+                if ((lane & 15) == 0) {
+                    const __bf16 h = (__bf16)t;
+                    s_sah[m * kArGp + k / kGroup] = h;
+                    s_sal[m * kArGp + k / kGroup] = (__bf16)(t - (float)h);
+                }
+            }
+        }
+        for (int i = tid; i < kArBM * kArGp; i += kArThreads) {   // groups >= G are 0
+            if (i % kArGp >= G) {
+                s_sah[i] = (__bf16)0.f;
+                s_sal[i] = (__bf16)0.f;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int u = 0; u < kMaxChunks; ++u) {
+            const int c = u * kArThreads + tid;
+            if (c < total)
+                *reinterpret_cast<uint4*>(s_a + ar_a_off(c / cpr, (c % cpr) >> 3, c & 7)) = va[u];
+        }
+#pragma unroll
+        for (int j = 0; j < kArBM * kArGp / kArThreads; ++j) {
+            const int i = j * kArThreads + tid;
+            const __bf16 h = (__bf16)asv[j];
+            s_sah[i] = h;
+            s_sal[i] = (__bf16)(asv[j] - (float)h);
+        }
+        if (wave == 0) s_asc[lane] = ascv;
+    }
     build(0);
     prefetch(1);
     lds_barrier();
