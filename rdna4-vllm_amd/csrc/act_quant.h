@@ -37,6 +37,20 @@ __device__ __forceinline__ void quantize_row_scalar(const void* __restrict__ x, 
                                                     float* __restrict__ scales, bool k8,
                                                     float* __restrict__ gsum, int lane);
 
+// A row of up to 4096 fp16 / bf16 values held by one wave: 16 bytes per lane and
+// 512-wide pass.
+struct RowRegs {
+    static constexpr int kMaxPass = 8;
+    uint4 v[kMaxPass];
+};
+__device__ __forceinline__ bool row_load(const void* __restrict__ x, int64_t row, int K, int lane,
+                                         RowRegs& rr);
+template <bool BF16>
+__device__ __forceinline__ void quantize_row_regs(const RowRegs& rr, int64_t row, int K,
+                                                  uint8_t* __restrict__ q,
+                                                  float* __restrict__ scales, bool k8,
+                                                  float* __restrict__ gsum, int lane);
+
 // Group sum of one 512-wide pass (lanes 16j..16j+15 hold group k/128): fixed-order tree.
 __device__ __forceinline__ void row_group_sum(uint32_t lo, uint32_t hi, int64_t row, int K, int k,
                                               float* __restrict__ gsum, int lane) {
@@ -58,20 +72,39 @@ __device__ __forceinline__ void quantize_row(const void* __restrict__ x, int64_t
     // Rows of up to 4096 values with 16-byte aligned starts: one 16-byte load per lane and
     // 512-wide pass, the row kept in registers between the absmax and the quantisation.
     // Same arithmetic as the element-wise form below, so the same bytes.
-    constexpr int kMaxPass = 8;
-    const int npass = (K + 511) / 512;
-    const char* rowp = reinterpret_cast<const char*>(x) + row * K * 2;
-    if (npass > kMaxPass || (reinterpret_cast<uintptr_t>(rowp) & 15) != 0) {
+    RowRegs rr;
+    if (!row_load(x, row, K, lane, rr)) {
         quantize_row_scalar<BF16>(x, row, K, q, scales, k8, gsum, lane);
         return;
     }
-    uint4 v[kMaxPass];
+    quantize_row_regs<BF16>(rr, row, K, q, scales, k8, gsum, lane);
+}
+
+// The 16-byte loads of quantize_row: false (nothing loaded) when the row is longer than
+// 4096 values or its start is not 16-byte aligned.
+__device__ __forceinline__ bool row_load(const void* __restrict__ x, int64_t row, int K, int lane,
+                                         RowRegs& rr) {
+    const int npass = (K + 511) / 512;
+    const char* rowp = reinterpret_cast<const char*>(x) + row * K * 2;
+    if (npass > RowRegs::kMaxPass || (reinterpret_cast<uintptr_t>(rowp) & 15) != 0) return false;
 #pragma unroll
-    for (int ps = 0; ps < kMaxPass; ++ps) {
+    for (int ps = 0; ps < RowRegs::kMaxPass; ++ps) {
         const int k = ps * 512 + lane * 8;
-        v[ps] = make_uint4(0, 0, 0, 0);
-        if (ps < npass && k < K) v[ps] = *reinterpret_cast<const uint4*>(rowp + k * 2);
+        rr.v[ps] = make_uint4(0, 0, 0, 0);
+        if (ps < npass && k < K) rr.v[ps] = *reinterpret_cast<const uint4*>(rowp + k * 2);
     }
+    return true;
+}
+
+// quantize_row on a row already in registers (row_load).
+template <bool BF16>
+__device__ __forceinline__ void quantize_row_regs(const RowRegs& rr, int64_t row, int K,
+                                                  uint8_t* __restrict__ q,
+                                                  float* __restrict__ scales, bool k8,
+                                                  float* __restrict__ gsum, int lane) {
+    constexpr int kMaxPass = RowRegs::kMaxPass;
+    const int npass = (K + 511) / 512;
+    const uint4* v = rr.v;
     float amax = 0.0f;
 #pragma unroll
     for (int ps = 0; ps < kMaxPass; ++ps) {

@@ -201,6 +201,61 @@ __global__ void __launch_bounds__(kAlignThreads) align_scan_kernel(
     write_layout(cnt, eoff, E, block_m, numel, total, sorted_ids, sorted_len, expert_ids, ntp);
 }
 
+// Multi-chunk phases 2 + 3 in one launch when the chunk histograms fit LDS: every
+// work-group reads all of them (one batch of loads), derives the per-expert totals, padded
+// expert offsets and its own chunk's bases, and places its chunk; work-group 0 also writes
+// the layout (sentinels, expert_ids, ntp).
+constexpr int kScanPlaceMaxCounts = 16384;   // nchunks * E held in LDS
+__global__ void __launch_bounds__(kAlignThreads) align_scan_place_kernel(
+    const int32_t* __restrict__ ids, int64_t numel, int E, int64_t block_m,
+    const int32_t* __restrict__ emap, const int32_t* __restrict__ counts, int nchunks,
+    int32_t* __restrict__ sorted_ids, int64_t sorted_len, int32_t* __restrict__ expert_ids,
+    int32_t* __restrict__ ntp, int32_t* __restrict__ slot_to_row) {
+    __shared__ ChunkScratch s;
+    __shared__ int lc[kScanPlaceMaxCounts];
+    __shared__ int cnt[kMaxExperts];
+    __shared__ int eoff[kMaxExperts];
+    __shared__ int base[kMaxExperts];
+    const int tid = threadIdx.x;
+    const int b = blockIdx.x;
+    const int ncount = nchunks * E;
+    constexpr int kPer = kScanPlaceMaxCounts / kAlignThreads;
+    int v[kPer];
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+        const int i = u * kAlignThreads + tid;
+        v[u] = i < ncount ? counts[i] : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+        const int i = u * kAlignThreads + tid;
+        if (i < ncount) lc[i] = v[u];
+    }
+    int rank;
+    const int e = chunk_rank(ids, numel, (int64_t)b * kChunk, emap, E, s, rank);   // syncs
+    for (int x = tid; x < E; x += kAlignThreads) {
+        int run = 0, mine = 0;
+        for (int c = 0; c < nchunks; ++c) {
+            if (c == b) mine = run;
+            run += lc[c * E + x];
+        }
+        cnt[x] = run;
+        base[x] = mine;
+    }
+    __syncthreads();
+    int total;
+    const int padded = (tid < E) ? (int)((cnt[tid] + block_m - 1) / block_m * block_m) : 0;
+    const int off = block_exclusive_scan(padded, s.warp_tot, total);
+    if (tid < E) eoff[tid] = off;
+    __syncthreads();
+    const int64_t slot = (int64_t)b * kChunk + tid;
+    const int row = e >= 0 ? eoff[e] + base[e] + rank : -1;
+    if (e >= 0) sorted_ids[row] = (int32_t)slot;
+    if (slot_to_row != nullptr && slot < numel) slot_to_row[slot] = row;
+    if (b == 0)
+        write_layout(cnt, eoff, E, block_m, numel, total, sorted_ids, sorted_len, expert_ids, ntp);
+}
+
 // Multi-chunk phase 3: stable placement.
 __global__ void __launch_bounds__(kAlignThreads) align_place_kernel(
     const int32_t* __restrict__ ids, int64_t numel, int E, const int32_t* __restrict__ emap,
@@ -268,13 +323,16 @@ __device__ __forceinline__ uint64_t wave_max_key(uint64_t k) {
 // ids_lds[j] too. Picks are made on the logits (exact ids); the weights are
 // exp(l - max) / sum exp(l - max), renormalised over the picks in pick order.
 template <int NV>
-__device__ __forceinline__ void topk_one_token(const float* __restrict__ l, int E, int top_k,
-                                               bool renorm, float* __restrict__ tw,
-                                               int32_t* __restrict__ ids, int32_t* ids_lds,
-                                               int lane) {
-    float v[NV];
+__device__ __forceinline__ void topk_load(const float* __restrict__ l, int E, int lane, float (&v)[NV]) {
 #pragma unroll
     for (int i = 0; i < NV; ++i) v[i] = l[min(lane + 64 * i, E - 1)];
+}
+
+// Selection of one token from its logits v (lane l holds entries l + 64 i).
+template <int NV>
+__device__ __forceinline__ void topk_select(float (&v)[NV], int E, int top_k, bool renorm,
+                                            float* __restrict__ tw, int32_t* __restrict__ ids,
+                                            int32_t* ids_lds, int lane) {
     float m = -INFINITY;
     uint64_t key[NV];
 #pragma unroll
@@ -311,6 +369,16 @@ __device__ __forceinline__ void topk_one_token(const float* __restrict__ l, int 
     }
 }
 
+template <int NV>
+__device__ __forceinline__ void topk_one_token(const float* __restrict__ l, int E, int top_k,
+                                               bool renorm, float* __restrict__ tw,
+                                               int32_t* __restrict__ ids, int32_t* ids_lds,
+                                               int lane) {
+    float v[NV];
+    topk_load<NV>(l, E, lane, v);
+    topk_select<NV>(v, E, top_k, renorm, tw, ids, ids_lds, lane);
+}
+
 // RowQuant: optional act-quant of the token's activation row by the same wave, after its
 // routing (act_quant_kernel's arithmetic; saves a launch for the many-token schedule).
 struct RowQuant {
@@ -329,11 +397,24 @@ __global__ void __launch_bounds__(256) topk_softmax_kernel(
     const int lane = threadIdx.x & 63;
     const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (t >= T) return;
-    topk_one_token<NV>(logits + t * E, E, top_k, renorm, tw + t * top_k, tids + t * top_k,
-                       nullptr, lane);
-    if (rq.x == nullptr) return;
-    if (rq.bf16) quantize_row<true>(rq.x, t, rq.K, rq.xq, rq.xs, true, rq.gsum, lane);
-    else quantize_row<false>(rq.x, t, rq.K, rq.xq, rq.xs, true, rq.gsum, lane);
+    float v[NV];
+    topk_load<NV>(logits + t * E, E, lane, v);
+    if (rq.x == nullptr) {
+        topk_select<NV>(v, E, top_k, renorm, tw + t * top_k, tids + t * top_k, nullptr, lane);
+        return;
+    }
+    // the row's loads go out behind the logits, so the selection runs while they arrive
+    RowRegs rr;
+    const bool in_regs = row_load(rq.x, t, rq.K, lane, rr);
+    topk_select<NV>(v, E, top_k, renorm, tw + t * top_k, tids + t * top_k, nullptr, lane);
+    if (!in_regs) {
+        if (rq.bf16) quantize_row<true>(rq.x, t, rq.K, rq.xq, rq.xs, true, rq.gsum, lane);
+        else quantize_row<false>(rq.x, t, rq.K, rq.xq, rq.xs, true, rq.gsum, lane);
+    } else if (rq.bf16) {
+        quantize_row_regs<true>(rr, t, rq.K, rq.xq, rq.xs, true, rq.gsum, lane);
+    } else {
+        quantize_row_regs<false>(rr, t, rq.K, rq.xq, rq.xs, true, rq.gsum, lane);
+    }
 }
 
 // Decode prologue in one launch: work-group 0 builds the align layout (numel <= kChunk),
@@ -391,6 +472,12 @@ int launch_align(const int32_t* ids, int64_t numel, int64_t E, int64_t block_m,
     align_count_kernel<<<(unsigned)nchunks, kAlignThreads, 0, stream>>>(ids, numel, (int)E, emap,
                                                                         counts);
     if (int rc = check_launch("align_count_kernel")) return rc;
+    if (nchunks * E <= kScanPlaceMaxCounts) {
+        align_scan_place_kernel<<<(unsigned)nchunks, kAlignThreads, 0, stream>>>(
+            ids, numel, (int)E, block_m, emap, counts, (int)nchunks, sorted_ids, sorted_len,
+            expert_ids, ntp, slot_to_row);
+        return check_launch("align_scan_place_kernel");
+    }
     align_scan_kernel<<<1, kAlignThreads, 0, stream>>>(counts, (int)nchunks, (int)E, block_m,
                                                        numel, eoff, sorted_ids, sorted_len,
                                                        expert_ids, ntp);

@@ -116,7 +116,8 @@ def test_topk_softmax(T, E, k):
 
 @pytest.mark.parametrize("T,k,E,bm", [(1, 8, 256, 16), (32, 8, 256, 16), (32, 8, 256, 8),
                                       (128, 8, 256, 64), (4096, 8, 256, 64), (2048, 8, 128, 64),
-                                      (200, 4, 1024, 32), (1, 1, 1, 1)])
+                                      (200, 4, 1024, 32), (1, 1, 1, 1),
+                                      (4096, 8, 1024, 64)])   # chunk counts beyond one LDS
 def test_align_bit_exact(T, k, E, bm):
     r = rng(T * 7 + E)
     ids = np.stack([r.permutation(E)[:k] for _ in range(T)]).astype(np.int32)
