@@ -450,8 +450,30 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
             const bf16x8 zal = lds_bf16x8(s_szl + lra * kArGp + go);
             const bf16x8 zbh = lds_bf16x8(s_szh + lrb * kArGp + go);
             const bf16x8 zbl = lds_bf16x8(s_szl + lrb * kArGp + go);
-            const int cola = ar_col<kSilu>(r, wave, 0, c16);
-            const int colb = ar_col<kSilu>(r, wave, 1, c16);
+            // A 16x16 fp16 block leaves in 8-byte row pieces: lane (q, 4a + b) holds rows
+            // 4q..4q+3 of column 4a + b; two DPP exchanges inside each quad of lanes (with
+            // lane b ^ 2 for 32-bit pairs, then lane b ^ 1 for halves) leave it row 4q + b,
+            // columns 4a..4a+3.
+            const int qb = c16 & 3;
+            const int64_t ldo = kSilu ? ncols : p.N;
+            auto store_block = [&](int i, const __half (&h)[4], int colbase) {
+                uint32_t p0 = (uint32_t)__half_as_ushort(h[0]) | ((uint32_t)__half_as_ushort(h[1]) << 16);
+                uint32_t p1 = (uint32_t)__half_as_ushort(h[2]) | ((uint32_t)__half_as_ushort(h[3]) << 16);
+                const uint32_t x = qb < 2 ? p1 : p0;
+                const uint32_t y = dpp_step<1>(x);
+                if (qb < 2) p1 = y; else p0 = y;
+                const uint32_t r0 = dpp_step<0>(p0), r1 = dpp_step<0>(p1);
+                const bool odd = qb & 1;
+                const uint32_t w0 = odd ? __builtin_amdgcn_perm(p0, r0, 0x07060302u)
+                                        : __builtin_amdgcn_perm(r0, p0, 0x05040100u);
+                const uint32_t w1 = odd ? __builtin_amdgcn_perm(p1, r1, 0x07060302u)
+                                        : __builtin_amdgcn_perm(r1, p1, 0x05040100u);
+                const int m = 16 * i + 4 * q + qb;
+                if ((vmask >> m) & 1)
+                    *reinterpret_cast<uint2*>(reinterpret_cast<__half*>(p.out) + (row0 + m) * ldo +
+                                              colbase + 4 * (c16 >> 2)) = make_uint2(w0, w1);
+            };
+            const int col0 = ar_col<kSilu>(r, wave, 0, 0);
 #pragma unroll
             for (int i = 0; i < NF; ++i) {
                 const bf16x8 sa = lds_bf16x8(sa_tab + (16 * i + c16) * kArGp + go);
@@ -459,21 +481,22 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
                 za = mfma_bf16_16x16x32(sa, zal, za);
                 v4f zb = mfma_bf16_16x16x32(sa, zbh, v4f{0.f, 0.f, 0.f, 0.f});
                 zb = mfma_bf16_16x16x32(sa, zbl, zb);
+                const float4 a4 = *reinterpret_cast<const float4*>(s_asc + 16 * i + 4 * q);
+                const float av[4] = {a4.x, a4.y, a4.z, a4.w};
+                __half ha[4], hb[4];
 #pragma unroll
                 for (int rr = 0; rr < 4; ++rr) {
-                    const int m = 16 * i + 4 * q + rr;
-                    if (!((vmask >> m) & 1)) continue;
-                    const float a = s_asc[m];
-                    const float va = a * (kNibbleScale * run[i][0][rr] - za[rr]);
-                    const float vb = a * (kNibbleScale * run[i][1][rr] - zb[rr]);
-                    const int64_t row_pad = row0 + m;
+                    const float va = av[rr] * (kNibbleScale * run[i][0][rr] - za[rr]);
+                    const float vb = av[rr] * (kNibbleScale * run[i][1][rr] - zb[rr]);
                     if constexpr (kSilu) {
-                        reinterpret_cast<__half*>(p.out)[row_pad * ncols + cola] = silu_mul_fast(va, vb);
+                        ha[rr] = silu_mul_fast(va, vb);
                     } else {
-                        reinterpret_cast<__half*>(p.out)[row_pad * p.N + cola] = __float2half(va);
-                        reinterpret_cast<__half*>(p.out)[row_pad * p.N + colb] = __float2half(vb);
+                        ha[rr] = __float2half(va);
+                        hb[rr] = __float2half(vb);
                     }
                 }
+                store_block(i, ha, col0);
+                if constexpr (!kSilu) store_block(i, hb, col0 + 16);
             }
 #pragma unroll
             for (int i = 0; i < NF; ++i)
