@@ -55,8 +55,9 @@ __device__ __forceinline__ int ar_a_off(int m, int g, int chunk) {
     return g * ar_a_group_bytes() + m * kGroup + ((chunk ^ (m & 7)) << 4);
 }
 // Dynamic LDS layout (bytes): activation tile; row group sums (hi/lo bf16); per range:
-// s*z (hi/lo bf16) of the 256 weight rows, scales [wave][group][column][fragment] (fp16)
-// and a staging area for the zero-point words
+// s*z (hi/lo bf16) of the 256 weight rows, scales [wave][group][column / 4][fragment]
+// [column % 4] (fp16, the 16 bytes lanes (q, *) read per step) and a staging area for the
+// zero-point words
 struct ArLds {
     int a, sah, sal, szh, szl, sc, zst, total;
     __host__ __device__ explicit ArLds(int K) {
@@ -128,7 +129,7 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
     __bf16* s_sal = reinterpret_cast<__bf16*>(lds + L.sal);           // ... lo
     __bf16* s_szh = reinterpret_cast<__bf16*>(lds + L.szh);           // [256][16] s*z hi
     __bf16* s_szl = reinterpret_cast<__bf16*>(lds + L.szl);           // ... lo
-    uint16_t* s_sc = reinterpret_cast<uint16_t*>(lds + L.sc);         // [8][16][16][2] fp16
+    uint16_t* s_sc = reinterpret_cast<uint16_t*>(lds + L.sc);         // [8][16][4][2][4] fp16
     uint32_t* s_zst = reinterpret_cast<uint32_t*>(lds + L.zst);       // [8][64] zero words
     float* s_asc = reinterpret_cast<float*>(lds + L.total);           // [64]
 
@@ -183,6 +184,10 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
     uint4 bw[kArD][kArNT];
     uint32_t i_off = 0;          // step_off of the next issue
     int i_g = 0, i_r = 0;        // its group and range
+    // Steps past the last range (at most the ring's four, never consumed) reload the last
+    // range's final four groups, which this wave requested just before and are still in L2:
+    // a work-group cannot retire before its loads return, so these must not go to HBM.
+    const uint32_t tail_off = (uint32_t)(nranges - 1) * r_step + (uint32_t)(G - kArD) * g_step;
     auto issue = [&](auto slotc) {
         constexpr int sl = decltype(slotc)::value;
         const uint8_t* base = we + i_off;
@@ -191,12 +196,11 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
             const uint8_t* ptr = base + frag_off[j] + lane_off;
             bw[sl][j] = FRAG ? load_stream16(ptr) : *reinterpret_cast<const uint4*>(ptr);
         }
-        // advance; past the last range the ring reloads range 0 (never consumed)
         i_off += g_step;
         if (++i_g == G) {
             i_g = 0;
             i_off += r_step - (uint32_t)G * g_step;
-            if (++i_r >= nranges) i_off = 0;
+            if (++i_r >= nranges) i_off = tail_off;
         }
     };
     using S0 = std::integral_constant<int, 0>;
@@ -251,7 +255,7 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
                 const float sv = __half2float(__ushort_as_half(hb));
                 const float z = ze ? (float)((zw[tt] >> zsh) & 0xF) : 8.0f;
                 sz[v] = g < G ? sv * z : 0.f;   // exact: fp16 scale x integer <= 15
-                s_sc[((wave * kArGp + g) * 16 + tc) * kArNT + tj] = hb;
+                s_sc[((wave * kArGp + g) * 4 + (tc >> 2)) * 8 + tj * 4 + (tc & 3)] = hb;
             }
             const __bf16 h0 = (__bf16)sz[0], h1 = (__bf16)sz[1];
             szh[t / 2] = pack_bf16x2(h0, h1);
@@ -376,45 +380,48 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
         if (wave == 0) s_asc[lane] = ascv;
     }
     build(0);
-    prefetch(1);
+    if (nranges > 1) prefetch(1);
     lds_barrier();
 
     auto main_loop = [&](auto nflc) {
         constexpr int NF = decltype(nflc)::value;
+        // Operands go in swapped (weights first), so the MFMAs produce the transposed block:
+        // lane (q, c16) of fragment (i, j) holds tile row 16 i + c16, columns 4 q .. 4 q + 3
+        // of fragment j; its four values leave as one 8-byte piece of an output row.
         v4f run[NF][kArNT];
-#pragma unroll
-        for (int i = 0; i < NF; ++i)
-#pragma unroll
-            for (int j = 0; j < kArNT; ++j) run[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
-
         // Software pipeline: a step first folds the previous step's MFMA results into the
-        // accumulators (run += acc * scale), then issues its own MFMAs into the same
-        // registers, so every result has a whole step to arrive before it is read.
+        // accumulators (run += acc * scale, the scale of each of the lane's four columns,
+        // read from the table at the step's start), then issues its own MFMAs into the same
+        // registers, so every result has a whole step to arrive before it is read. A range's
+        // first step has nothing to fold and its second starts the accumulators
+        // (run = acc * scale).
         v4f pend[NF][kArNT];
-        float psc[kArNT] = {0.f, 0.f};
-#pragma unroll
-        for (int i = 0; i < NF; ++i)
-#pragma unroll
-            for (int j = 0; j < kArNT; ++j) pend[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
-        auto fold = [&]() {
-#pragma unroll
-            for (int i = 0; i < NF; ++i)
-#pragma unroll
-                for (int j = 0; j < kArNT; ++j)
-#pragma unroll
-                    for (int rr = 0; rr < 4; ++rr) run[i][j][rr] = fmaf(pend[i][j][rr], psc[j], run[i][j][rr]);
+        auto scales_of = [&](int g) {      // fp16 scales [fragment][column 0..3] of group g
+            return *reinterpret_cast<const uint4*>(s_sc + ((wave * kArGp + g) * 4 + q) * 8);
         };
-        auto consume = [&](int g, auto slotc) {
+        auto fold_one = [&](int i, int j, const uint4& sc, auto modec) {
+            constexpr int mode = decltype(modec)::value;
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                const uint32_t w = j == 0 ? (rr < 2 ? sc.x : sc.y) : (rr < 2 ? sc.z : sc.w);
+                const float f = __half2float(__ushort_as_half((uint16_t)((rr & 1) ? w >> 16 : w & 0xFFFF)));
+                if constexpr (mode == 1) run[i][j][rr] = pend[i][j][rr] * f;
+                if constexpr (mode == 2) run[i][j][rr] = fmaf(pend[i][j][rr], f, run[i][j][rr]);
+            }
+        };
+        using M0 = std::integral_constant<int, 0>;
+        using M1 = std::integral_constant<int, 1>;
+        using M2 = std::integral_constant<int, 2>;
+        auto consume = [&](int g, auto slotc, auto modec) {
             constexpr int sl = decltype(slotc)::value;
-            const uint32_t sp = *reinterpret_cast<const uint32_t*>(s_sc + ((wave * kArGp + g) * 16 + c16) * kArNT);
+            constexpr int mode = decltype(modec)::value;
+            const uint4 sc = mode ? scales_of(g - 1) : make_uint4(0u, 0u, 0u, 0u);
             v8i bf[kArNT];
 #pragma unroll
             for (int j = 0; j < kArNT; ++j) bf[j] = spread_nibbles(bw[sl][j]);
             // fragment i's rows are 16 i + c16: same swizzle as row c16, offset i * 2 KB
             const uint8_t* A0 = s_a + ar_a_off(c16, g, 2 * q);
             const uint8_t* A1 = s_a + ar_a_off(c16, g, 2 * q + 1);
-            const float sc0 = __half2float(__ushort_as_half((uint16_t)(sp & 0xFFFF)));
-            const float sc1 = __half2float(__ushort_as_half((uint16_t)(sp >> 16)));
 #pragma unroll
             for (int i = 0; i < NF; ++i) {
                 const uint4 lo = *reinterpret_cast<const uint4*>(A0 + i * 16 * kGroup);
@@ -423,26 +430,24 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
                                    (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
 #pragma unroll
                 for (int j = 0; j < kArNT; ++j) {
-#pragma unroll
-                    for (int rr = 0; rr < 4; ++rr) run[i][j][rr] = fmaf(pend[i][j][rr], psc[j], run[i][j][rr]);
-                    pend[i][j] = mfma_16x16x128(af, bf[j], v4f{0.f, 0.f, 0.f, 0.f});
+                    fold_one(i, j, sc, modec);
+                    pend[i][j] = mfma_16x16x128(bf[j], af, v4f{0.f, 0.f, 0.f, 0.f});
                 }
             }
-            psc[0] = sc0;
-            psc[1] = sc1;
         };
 
         // Range epilogue: zero-point term of every (row, column) as bf16 MFMAs over the
-        // groups (lane (q, c16), K slot 8q + t <-> group 8 (q & 1) + t: A = hi (q < 2) or lo
-        // (q >= 2) half of the row's group sum; B = hi, then lo, half of s*z with slots
-        // 16..31 repeating 0..15, so the two MFMAs add (sa_hi + sa_lo)(sz_hi + sz_lo)), then
-        // out = asc * (512 * run - zero term), stored; the accumulators restart.
+        // groups (lane (q, c16), K slot 8q + t <-> group 8 (q & 1) + t: the row operand is
+        // the hi (q < 2) or lo (q >= 2) half of the row's group sum; the column operand the
+        // hi, then lo, half of s*z with slots 16..31 repeating 0..15, so the two MFMAs add
+        // (sa_hi + sa_lo)(sz_hi + sz_lo)); operands swapped as in the main MFMAs), then
+        // out = asc * (512 * run - zero term), stored.
         auto epilogue = [&](int r) {
-            fold();
+            const uint4 sc = scales_of(G - 1);
 #pragma unroll
             for (int i = 0; i < NF; ++i)
 #pragma unroll
-                for (int j = 0; j < kArNT; ++j) pend[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+                for (int j = 0; j < kArNT; ++j) fold_one(i, j, sc, M2{});
             const __bf16* sa_tab = q < 2 ? s_sah : s_sal;
             const int go = 8 * (q & 1);
             const int lra = 32 * wave + c16, lrb = lra + 16;
@@ -450,83 +455,82 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
             const bf16x8 zal = lds_bf16x8(s_szl + lra * kArGp + go);
             const bf16x8 zbh = lds_bf16x8(s_szh + lrb * kArGp + go);
             const bf16x8 zbl = lds_bf16x8(s_szl + lrb * kArGp + go);
-            // A 16x16 fp16 block leaves in 8-byte row pieces: lane (q, 4a + b) holds rows
-            // 4q..4q+3 of column 4a + b; two DPP exchanges inside each quad of lanes (with
-            // lane b ^ 2 for 32-bit pairs, then lane b ^ 1 for halves) leave it row 4q + b,
-            // columns 4a..4a+3.
-            const int qb = c16 & 3;
             const int64_t ldo = kSilu ? ncols : p.N;
-            auto store_block = [&](int i, const __half (&h)[4], int colbase) {
-                uint32_t p0 = (uint32_t)__half_as_ushort(h[0]) | ((uint32_t)__half_as_ushort(h[1]) << 16);
-                uint32_t p1 = (uint32_t)__half_as_ushort(h[2]) | ((uint32_t)__half_as_ushort(h[3]) << 16);
-                const uint32_t x = qb < 2 ? p1 : p0;
-                const uint32_t y = dpp_step<1>(x);
-                if (qb < 2) p1 = y; else p0 = y;
-                const uint32_t r0 = dpp_step<0>(p0), r1 = dpp_step<0>(p1);
-                const bool odd = qb & 1;
-                const uint32_t w0 = odd ? __builtin_amdgcn_perm(p0, r0, 0x07060302u)
-                                        : __builtin_amdgcn_perm(r0, p0, 0x05040100u);
-                const uint32_t w1 = odd ? __builtin_amdgcn_perm(p1, r1, 0x07060302u)
-                                        : __builtin_amdgcn_perm(r1, p1, 0x05040100u);
-                const int m = 16 * i + 4 * q + qb;
-                if ((vmask >> m) & 1)
-                    *reinterpret_cast<uint2*>(reinterpret_cast<__half*>(p.out) + (row0 + m) * ldo +
-                                              colbase + 4 * (c16 >> 2)) = make_uint2(w0, w1);
-            };
-            const int col0 = ar_col<kSilu>(r, wave, 0, 0);
+            __half* outp = reinterpret_cast<__half*>(p.out) + ar_col<kSilu>(r, wave, 0, 0) + 4 * q;
 #pragma unroll
             for (int i = 0; i < NF; ++i) {
-                const bf16x8 sa = lds_bf16x8(sa_tab + (16 * i + c16) * kArGp + go);
-                v4f za = mfma_bf16_16x16x32(sa, zah, v4f{0.f, 0.f, 0.f, 0.f});
-                za = mfma_bf16_16x16x32(sa, zal, za);
-                v4f zb = mfma_bf16_16x16x32(sa, zbh, v4f{0.f, 0.f, 0.f, 0.f});
-                zb = mfma_bf16_16x16x32(sa, zbl, zb);
-                const float4 a4 = *reinterpret_cast<const float4*>(s_asc + 16 * i + 4 * q);
-                const float av[4] = {a4.x, a4.y, a4.z, a4.w};
-                __half ha[4], hb[4];
+                const int m = 16 * i + c16;
+                const bf16x8 sa = lds_bf16x8(sa_tab + m * kArGp + go);
+                v4f za = mfma_bf16_16x16x32(zah, sa, v4f{0.f, 0.f, 0.f, 0.f});
+                za = mfma_bf16_16x16x32(zal, sa, za);
+                v4f zb = mfma_bf16_16x16x32(zbh, sa, v4f{0.f, 0.f, 0.f, 0.f});
+                zb = mfma_bf16_16x16x32(zbl, sa, zb);
+                const float av = s_asc[m];
+                float va[4], vb[4];
 #pragma unroll
                 for (int rr = 0; rr < 4; ++rr) {
-                    const float va = av[rr] * (kNibbleScale * run[i][0][rr] - za[rr]);
-                    const float vb = av[rr] * (kNibbleScale * run[i][1][rr] - zb[rr]);
-                    if constexpr (kSilu) {
-                        ha[rr] = silu_mul_fast(va, vb);
-                    } else {
-                        ha[rr] = __float2half(va);
-                        hb[rr] = __float2half(vb);
+                    va[rr] = av * (kNibbleScale * run[i][0][rr] - za[rr]);
+                    vb[rr] = av * (kNibbleScale * run[i][1][rr] - zb[rr]);
+                }
+                __half* rowp = outp + (row0 + m) * ldo;
+                const bool live = (vmask >> m) & 1;
+                if constexpr (kSilu) {
+                    const __half2 h01 = __halves2half2(silu_mul_fast(va[0], vb[0]), silu_mul_fast(va[1], vb[1]));
+                    const __half2 h23 = __halves2half2(silu_mul_fast(va[2], vb[2]), silu_mul_fast(va[3], vb[3]));
+                    if (live)
+                        *reinterpret_cast<uint2*>(rowp) = make_uint2(__builtin_bit_cast(uint32_t, h01),
+                                                                     __builtin_bit_cast(uint32_t, h23));
+                } else {
+                    const __half2 a01 = __floats2half2_rn(va[0], va[1]), a23 = __floats2half2_rn(va[2], va[3]);
+                    const __half2 b01 = __floats2half2_rn(vb[0], vb[1]), b23 = __floats2half2_rn(vb[2], vb[3]);
+                    if (live) {
+                        *reinterpret_cast<uint2*>(rowp) = make_uint2(__builtin_bit_cast(uint32_t, a01),
+                                                                     __builtin_bit_cast(uint32_t, a23));
+                        *reinterpret_cast<uint2*>(rowp + 16) = make_uint2(__builtin_bit_cast(uint32_t, b01),
+                                                                          __builtin_bit_cast(uint32_t, b23));
                     }
                 }
-                store_block(i, ha, col0);
-                if constexpr (!kSilu) store_block(i, hb, col0 + 16);
             }
-#pragma unroll
-            for (int i = 0; i < NF; ++i)
-#pragma unroll
-                for (int j = 0; j < kArNT; ++j) run[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
         };
 
-        // Four steps per iteration (one pass of the ring; G % 4 == 0), so every iteration
-        // issues the same loads and the wait counts stay exact. The next range's tables are
-        // requested once per range, before its loop. The scheduling barriers keep each step's
-        // MFMAs next to the fold that frees their registers instead of hoisting later steps'
-        // MFMAs.
+        // Four steps per pass of the ring (G % 4 == 0), so every pass issues the same loads
+        // and the wait counts stay exact; a range's first pass is written out on its own (its
+        // first two steps fold differently). The next range's tables are requested once per
+        // range, before its loop. The scheduling barriers keep each step's MFMAs next to the
+        // fold that frees their registers instead of hoisting later steps' MFMAs.
         for (int r = 0; r < nranges; ++r) {
-            if (r > 0) prefetch(r + 1);
-            int g = 0;
-            do {
-                consume(g, S0{});
+            // Waves w and w + 4 share a SIMD and the issue arbiter favours one of them; the
+            // higher priority alternates between the two every range, so neither falls a
+            // whole tile behind (the work-group ends with its slowest wave).
+            if (((wave >> 2) ^ r) & 1) __builtin_amdgcn_s_setprio(1);
+            else __builtin_amdgcn_s_setprio(0);
+            if (r > 0 && r + 1 < nranges) prefetch(r + 1);
+            consume(0, S0{}, M0{});
+            issue(S0{});
+            __builtin_amdgcn_sched_barrier(0);
+            consume(1, S1{}, M1{});
+            issue(S1{});
+            __builtin_amdgcn_sched_barrier(0);
+            consume(2, S2{}, M2{});
+            issue(S2{});
+            __builtin_amdgcn_sched_barrier(0);
+            consume(3, S3{}, M2{});
+            issue(S3{});
+            __builtin_amdgcn_sched_barrier(0);
+            for (int g = 4; g < G; g += 4) {
+                consume(g, S0{}, M2{});
                 issue(S0{});
                 __builtin_amdgcn_sched_barrier(0);
-                consume(g + 1, S1{});
+                consume(g + 1, S1{}, M2{});
                 issue(S1{});
                 __builtin_amdgcn_sched_barrier(0);
-                consume(g + 2, S2{});
+                consume(g + 2, S2{}, M2{});
                 issue(S2{});
                 __builtin_amdgcn_sched_barrier(0);
-                consume(g + 3, S3{});
+                consume(g + 3, S3{}, M2{});
                 issue(S3{});
                 __builtin_amdgcn_sched_barrier(0);
-                g += 4;
-            } while (g < G);
+            }
             epilogue(r);
             if (r + 1 < nranges) build(r + 1);
         }
