@@ -7,10 +7,13 @@
 // ntp keep the sentinel and expert id -1.
 //
 // Schedule: slots are cut into chunks of kChunk. Per chunk, a work-group builds a
-// per-expert histogram and the stable in-chunk rank of every slot (bucket the slots with
-// LDS atomics, then rank each slot by counting smaller slot ids in its bucket, so the
-// result never depends on atomic order). A single work-group scans the chunk histograms
-// into expert offsets. Small inputs (one chunk) run all three phases in one launch.
+// per-expert histogram and the stable in-chunk rank of every slot: each wave finds, with
+// one ballot per expert-id bit, the lanes that share a lane's expert (its rank in the wave
+// is the count of those below it), and an exclusive prefix of the per-wave counts over the
+// chunk's waves adds the slots of earlier waves. No atomics, so the result is the same
+// every run, and a popular expert costs no more than a rare one. The chunk histograms are
+// then scanned into expert offsets and every slot is placed. Small inputs (one chunk) run
+// all phases in one launch.
 #include "w4a8_common.h"
 #include "w4a8_internal.h"
 #include "act_quant.h"
@@ -23,10 +26,8 @@ constexpr int kAlignThreads = 1024;
 constexpr int kMaxExperts = 1024;  // experts handled by the align kernels
 
 struct ChunkScratch {
-    int hist[kMaxExperts];
-    int boff[kMaxExperts];    // bucket start (exclusive scan of hist)
-    int fill[kMaxExperts];
-    int16_t bucket[kChunk];   // in-chunk slot indices grouped by expert
+    int hist[kMaxExperts];                             // slots of the chunk per expert
+    int16_t wpre[kAlignThreads / 64][kMaxExperts];     // per wave: slots, then exclusive prefix
     int warp_tot[kAlignThreads / 64];
 };
 
@@ -64,34 +65,45 @@ __device__ int block_exclusive_scan(int v, int* warp_tot, int& total) {
     return before + x - v;
 }
 
-// Phase A for one chunk: histogram, buckets and the stable rank of this thread's slot.
-// Returns the expert (or -1) of slot `base + threadIdx.x`, writes its rank.
+// Lanes of the wave whose expert equals this lane's (valid lanes only; e < 2^nbits).
+__device__ __forceinline__ uint64_t same_expert_lanes(int e, int nbits) {
+    uint64_t m = __ballot(e >= 0);
+    for (int b = 0; b < nbits; ++b) {
+        const bool bit = (e >> b) & 1;
+        const uint64_t bb = __ballot(bit);
+        m &= bit ? bb : ~bb;
+    }
+    return m;
+}
+
+// Phase A for one chunk: histogram (s.hist) and the stable rank of this thread's slot among
+// the chunk's slots of its expert. Returns the expert (or -1) of slot `base + threadIdx.x`.
 __device__ int chunk_rank(const int32_t* __restrict__ ids, int64_t numel, int64_t base,
                           const int32_t* __restrict__ emap, int E, ChunkScratch& s,
                           int& rank) {
-    const int tid = threadIdx.x;
-    for (int e = tid; e < E; e += kAlignThreads) { s.hist[e] = 0; s.fill[e] = 0; }
-    __syncthreads();
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int64_t i = base + tid;
     const int e = (i < numel) ? map_expert(ids, i, emap, E) : -1;
-    if (e >= 0) atomicAdd(&s.hist[e], 1);
+    int* z = reinterpret_cast<int*>(&s.wpre[0][0]);
+    for (int k = tid; k < (kAlignThreads / 64) * kMaxExperts / 2; k += kAlignThreads) z[k] = 0;
     __syncthreads();
-    // bucket offsets: scan hist over experts (E <= 1024 -> one element per thread)
-    int total;
-    const int h = (tid < E) ? s.hist[tid] : 0;
-    const int off = block_exclusive_scan(h, s.warp_tot, total);
-    if (tid < E) s.boff[tid] = off;
+    const int nbits = 32 - __clz(E > 1 ? E - 1 : 1);
+    const uint64_t same = same_expert_lanes(e, nbits);
+    const int rw = __popcll(same & ((1ull << lane) - 1ull));
+    if (e >= 0 && rw == 0) s.wpre[w][e] = (int16_t)__popcll(same);
     __syncthreads();
-    if (e >= 0) {
-        const int p = atomicAdd(&s.fill[e], 1);
-        s.bucket[s.boff[e] + p] = (int16_t)tid;
+    for (int x = tid; x < E; x += kAlignThreads) {
+        int run = 0;
+#pragma unroll
+        for (int ww = 0; ww < kAlignThreads / 64; ++ww) {
+            const int c = s.wpre[ww][x];
+            s.wpre[ww][x] = (int16_t)run;
+            run += c;
+        }
+        s.hist[x] = run;
     }
     __syncthreads();
-    rank = 0;
-    if (e >= 0) {
-        const int b0 = s.boff[e], n = s.hist[e];
-        for (int q = 0; q < n; ++q) rank += (s.bucket[b0 + q] < tid) ? 1 : 0;
-    }
+    rank = e >= 0 ? s.wpre[w][e] + rw : 0;
     return e;
 }
 
@@ -150,19 +162,18 @@ __global__ void __launch_bounds__(kAlignThreads) align_small_kernel(
                      slot_to_row);
 }
 
-// Multi-chunk phase 1: per-chunk histograms -> counts[chunk][E].
+// Multi-chunk phase 1: per-chunk histograms -> counts[chunk][E], and every slot's expert
+// and in-chunk rank as one word: rank << 10 | expert (-1: no expert).
+__device__ __forceinline__ int slot_key_pack(int e, int rank) { return e >= 0 ? (rank << 10) | e : -1; }
 __global__ void __launch_bounds__(kAlignThreads) align_count_kernel(
     const int32_t* __restrict__ ids, int64_t numel, int E, const int32_t* __restrict__ emap,
-    int32_t* __restrict__ counts) {
-    __shared__ int hist[kMaxExperts];
-    const int tid = threadIdx.x;
-    for (int e = tid; e < E; e += kAlignThreads) hist[e] = 0;
-    __syncthreads();
-    const int64_t i = (int64_t)blockIdx.x * kChunk + tid;
-    const int e = (i < numel) ? map_expert(ids, i, emap, E) : -1;
-    if (e >= 0) atomicAdd(&hist[e], 1);
-    __syncthreads();
-    for (int x = tid; x < E; x += kAlignThreads) counts[(int64_t)blockIdx.x * E + x] = hist[x];
+    int32_t* __restrict__ counts, int32_t* __restrict__ slot_key) {
+    __shared__ ChunkScratch s;
+    int rank;
+    const int64_t base = (int64_t)blockIdx.x * kChunk;
+    const int e = chunk_rank(ids, numel, base, emap, E, s, rank);
+    if (base + threadIdx.x < numel) slot_key[base + threadIdx.x] = slot_key_pack(e, rank);
+    for (int x = threadIdx.x; x < E; x += kAlignThreads) counts[(int64_t)blockIdx.x * E + x] = s.hist[x];
 }
 
 // Multi-chunk phase 2 (one work-group): counts -> per-chunk expert bases (in place),
@@ -202,23 +213,25 @@ __global__ void __launch_bounds__(kAlignThreads) align_scan_kernel(
 }
 
 // Multi-chunk phases 2 + 3 in one launch when the chunk histograms fit LDS: every
-// work-group reads all of them (one batch of loads), derives the per-expert totals, padded
-// expert offsets and its own chunk's bases, and places its chunk; work-group 0 also writes
-// the layout (sentinels, expert_ids, ntp).
+// work-group reads all of them together with its chunk's slot keys (one batch of loads),
+// derives the per-expert totals, padded expert offsets and its own chunk's bases, and
+// places its chunk; work-group 0 also writes the layout (sentinels, expert_ids, ntp).
 constexpr int kScanPlaceMaxCounts = 16384;   // nchunks * E held in LDS
 __global__ void __launch_bounds__(kAlignThreads) align_scan_place_kernel(
-    const int32_t* __restrict__ ids, int64_t numel, int E, int64_t block_m,
-    const int32_t* __restrict__ emap, const int32_t* __restrict__ counts, int nchunks,
-    int32_t* __restrict__ sorted_ids, int64_t sorted_len, int32_t* __restrict__ expert_ids,
-    int32_t* __restrict__ ntp, int32_t* __restrict__ slot_to_row) {
-    __shared__ ChunkScratch s;
+    const int32_t* __restrict__ slot_key, int64_t numel, int E, int64_t block_m,
+    const int32_t* __restrict__ counts, int nchunks, int32_t* __restrict__ sorted_ids,
+    int64_t sorted_len, int32_t* __restrict__ expert_ids, int32_t* __restrict__ ntp,
+    int32_t* __restrict__ slot_to_row) {
     __shared__ int lc[kScanPlaceMaxCounts];
     __shared__ int cnt[kMaxExperts];
     __shared__ int eoff[kMaxExperts];
     __shared__ int base[kMaxExperts];
+    __shared__ int warp_tot[kAlignThreads / 64];
     const int tid = threadIdx.x;
     const int b = blockIdx.x;
     const int ncount = nchunks * E;
+    const int64_t slot = (int64_t)b * kChunk + tid;
+    const int key = slot < numel ? slot_key[slot] : -1;
     constexpr int kPer = kScanPlaceMaxCounts / kAlignThreads;
     int v[kPer];
 #pragma unroll
@@ -231,8 +244,7 @@ __global__ void __launch_bounds__(kAlignThreads) align_scan_place_kernel(
         const int i = u * kAlignThreads + tid;
         if (i < ncount) lc[i] = v[u];
     }
-    int rank;
-    const int e = chunk_rank(ids, numel, (int64_t)b * kChunk, emap, E, s, rank);   // syncs
+    __syncthreads();
     for (int x = tid; x < E; x += kAlignThreads) {
         int run = 0, mine = 0;
         for (int c = 0; c < nchunks; ++c) {
@@ -245,11 +257,11 @@ __global__ void __launch_bounds__(kAlignThreads) align_scan_place_kernel(
     __syncthreads();
     int total;
     const int padded = (tid < E) ? (int)((cnt[tid] + block_m - 1) / block_m * block_m) : 0;
-    const int off = block_exclusive_scan(padded, s.warp_tot, total);
+    const int off = block_exclusive_scan(padded, warp_tot, total);
     if (tid < E) eoff[tid] = off;
     __syncthreads();
-    const int64_t slot = (int64_t)b * kChunk + tid;
-    const int row = e >= 0 ? eoff[e] + base[e] + rank : -1;
+    const int e = key >= 0 ? (key & 1023) : -1;
+    const int row = e >= 0 ? eoff[e] + base[e] + (key >> 10) : -1;
     if (e >= 0) sorted_ids[row] = (int32_t)slot;
     if (slot_to_row != nullptr && slot < numel) slot_to_row[slot] = row;
     if (b == 0)
@@ -258,15 +270,13 @@ __global__ void __launch_bounds__(kAlignThreads) align_scan_place_kernel(
 
 // Multi-chunk phase 3: stable placement.
 __global__ void __launch_bounds__(kAlignThreads) align_place_kernel(
-    const int32_t* __restrict__ ids, int64_t numel, int E, const int32_t* __restrict__ emap,
+    const int32_t* __restrict__ slot_key, int64_t numel, int E,
     const int32_t* __restrict__ chunk_base, const int32_t* __restrict__ eoff,
     int32_t* __restrict__ sorted_ids, int32_t* __restrict__ slot_to_row) {
-    __shared__ ChunkScratch s;
-    int rank;
-    const int64_t base = (int64_t)blockIdx.x * kChunk;
-    const int e = chunk_rank(ids, numel, base, emap, E, s, rank);
-    const int64_t slot = base + threadIdx.x;
-    const int row = e >= 0 ? eoff[e] + chunk_base[(int64_t)blockIdx.x * E + e] + rank : -1;
+    const int64_t slot = (int64_t)blockIdx.x * kChunk + threadIdx.x;
+    const int key = slot < numel ? slot_key[slot] : -1;
+    const int e = key >= 0 ? (key & 1023) : -1;
+    const int row = e >= 0 ? eoff[e] + chunk_base[(int64_t)blockIdx.x * E + e] + (key >> 10) : -1;
     if (e >= 0) sorted_ids[row] = (int32_t)slot;
     if (slot_to_row != nullptr && slot < numel) slot_to_row[slot] = row;
 }
@@ -276,47 +286,23 @@ constexpr int kRouterMaxPerLane = 16;   // E <= 1024
 
 // NV = logits per lane (E <= 64 * NV). Loads are unconditional (clamped index, the
 // out-of-range entries masked to -inf afterwards) so they issue together.
-// Selection key: a larger key is a larger logit, equal logits order by the lower expert id
-// (the router's tie-break). Entries past E get key 0, below every real entry.
-__device__ __forceinline__ uint64_t topk_key(float v, int e) {
+// Selection key: the logit's bits mapped to an unsigned order (a larger key is a larger
+// logit), at least 1; entries past E and entries already picked hold 0. Equal keys go to
+// the lower expert id (the router's tie-break).
+__device__ __forceinline__ uint32_t topk_key(float v) {
     uint32_t b = __float_as_uint(v);
     b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);   // order-preserving float -> uint
-    return ((uint64_t)b << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)e);
+    return b > 1u ? b : 1u;
 }
-__device__ __forceinline__ float topk_key_value(uint64_t key) {
-    uint32_t b = (uint32_t)(key >> 32);
-    b = (b & 0x80000000u) ? (b & 0x7FFFFFFFu) : ~b;
+__device__ __forceinline__ float topk_key_value(uint32_t key) {
+    const uint32_t b = (key & 0x80000000u) ? (key & 0x7FFFFFFFu) : ~key;
     return __uint_as_float(b);
 }
-__device__ __forceinline__ int topk_key_expert(uint64_t key) {
-    return (int)(0xFFFFFFFFu - (uint32_t)key);
-}
-template <int S>
-__device__ __forceinline__ uint64_t key_max_dpp(uint64_t k) {
-    const uint32_t lo = dpp_step<S>((uint32_t)k), hi = dpp_step<S>((uint32_t)(k >> 32));
-    const uint64_t o = ((uint64_t)hi << 32) | lo;
-    return o > k ? o : k;
-}
-// maximum key over the wave, every lane gets it (branch-free compare-selects)
-__device__ __forceinline__ uint64_t wave_max_key(uint64_t k) {
-    k = key_max_dpp<0>(k);
-    k = key_max_dpp<1>(k);
-    k = key_max_dpp<2>(k);
-    k = key_max_dpp<3>(k);
-    {
-        const auto lo = __builtin_amdgcn_permlane16_swap((uint32_t)k, (uint32_t)k, false, false);
-        const auto hi = __builtin_amdgcn_permlane16_swap((uint32_t)(k >> 32), (uint32_t)(k >> 32), false, false);
-        const uint64_t a = ((uint64_t)hi[0] << 32) | lo[0], b = ((uint64_t)hi[1] << 32) | lo[1];
-        k = a > b ? a : b;
+struct MaxU32Op {   // unsigned maximum of two words carried in float registers
+    __device__ float operator()(float a, float b) const {
+        return __uint_as_float(max(__float_as_uint(a), __float_as_uint(b)));
     }
-    {
-        const auto lo = __builtin_amdgcn_permlane32_swap((uint32_t)k, (uint32_t)k, false, false);
-        const auto hi = __builtin_amdgcn_permlane32_swap((uint32_t)(k >> 32), (uint32_t)(k >> 32), false, false);
-        const uint64_t a = ((uint64_t)hi[0] << 32) | lo[0], b = ((uint64_t)hi[1] << 32) | lo[1];
-        k = a > b ? a : b;
-    }
-    return k;
-}
+};
 
 // Softmax + top-k of one token's logits row l (E <= 64 * NV) by one wave: lane j < top_k
 // writes pick j (weight, expert) to tw[j] / ids[j] and, if ids_lds is given, the expert to
@@ -334,38 +320,46 @@ __device__ __forceinline__ void topk_select(float (&v)[NV], int E, int top_k, bo
                                             float* __restrict__ tw, int32_t* __restrict__ ids,
                                             int32_t* ids_lds, int lane) {
     float m = -INFINITY;
-    uint64_t key[NV];
+    uint32_t key[NV];
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
         const bool in = lane + 64 * i < E;
         if (!in) v[i] = -INFINITY;
         m = fmaxf(m, v[i]);
-        key[i] = in ? topk_key(v[i], lane + 64 * i) : 0ull;
+        key[i] = in ? topk_key(v[i]) : 0u;
     }
     m = wave_max(m);
     float ssum = 0.f;
 #pragma unroll
     for (int i = 0; i < NV; ++i) ssum += lane + 64 * i < E ? expf(v[i] - m) : 0.f;
     ssum = wave_sum(ssum);
-    uint64_t mine = 0;   // lane j < top_k: key of pick j
+    uint32_t mine_key = 0;   // lane j < top_k: pick j
+    int mine_e = 0;
     for (int j = 0; j < top_k; ++j) {
-        uint64_t best = 0;
+        uint32_t best = 0;
 #pragma unroll
-        for (int i = 0; i < NV; ++i) best = key[i] > best ? key[i] : best;
-        best = wave_max_key(best);
+        for (int i = 0; i < NV; ++i) best = max(best, key[i]);
+        best = __float_as_uint(lane_allreduce<6>(__uint_as_float(best), MaxU32Op{}));
+        // the lowest expert holding it: lowest entry index i with a holder, lowest lane there
+        int pick = 0;
 #pragma unroll
-        for (int i = 0; i < NV; ++i) key[i] = key[i] == best ? 0ull : key[i];   // taken
-        mine = lane == j ? best : mine;
+        for (int i = NV - 1; i >= 0; --i) {
+            const uint64_t h = __ballot(key[i] == best);
+            if (h != 0) pick = (int)__builtin_ctzll(h) + 64 * i;
+        }
+#pragma unroll
+        for (int i = 0; i < NV; ++i) key[i] = (lane + 64 * i == pick) ? 0u : key[i];   // taken
+        mine_key = lane == j ? best : mine_key;
+        mine_e = lane == j ? pick : mine_e;
     }
-    const float p = expf(topk_key_value(mine) - m) / ssum;
+    const float p = expf(topk_key_value(mine_key) - m) / ssum;
     float sum_sel = 0.f;   // picks in order, as a sequential sum
     for (int j = 0; j < top_k; ++j)
         sum_sel += __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(p), j));
     if (lane < top_k) {
-        const int e = topk_key_expert(mine);
         tw[lane] = renorm ? p / sum_sel : p;
-        ids[lane] = e;
-        if (ids_lds != nullptr) ids_lds[lane] = e;
+        ids[lane] = mine_e;
+        if (ids_lds != nullptr) ids_lds[lane] = mine_e;
     }
 }
 
@@ -444,6 +438,7 @@ size_t align_workspace_bytes(int64_t numel, int64_t num_experts) {
     WorkspaceSize s;
     s.take<int32_t>((size_t)(nchunks * num_experts));
     s.take<int32_t>((size_t)num_experts);
+    s.take<int32_t>((size_t)numel);
     return s.used;
 }
 
@@ -465,16 +460,17 @@ int launch_align(const int32_t* ids, int64_t numel, int64_t E, int64_t block_m,
     Workspace w(ws, ws_bytes);
     int32_t* counts = w.take<int32_t>((size_t)(nchunks * E));
     int32_t* eoff = w.take<int32_t>((size_t)E);
+    int32_t* slot_key = w.take<int32_t>((size_t)numel);
     if (ws == nullptr || !w.ok()) {
         set_error("moe_align: workspace too small");
         return W4A8_ERR_WORKSPACE;
     }
     align_count_kernel<<<(unsigned)nchunks, kAlignThreads, 0, stream>>>(ids, numel, (int)E, emap,
-                                                                        counts);
+                                                                        counts, slot_key);
     if (int rc = check_launch("align_count_kernel")) return rc;
     if (nchunks * E <= kScanPlaceMaxCounts) {
         align_scan_place_kernel<<<(unsigned)nchunks, kAlignThreads, 0, stream>>>(
-            ids, numel, (int)E, block_m, emap, counts, (int)nchunks, sorted_ids, sorted_len,
+            slot_key, numel, (int)E, block_m, counts, (int)nchunks, sorted_ids, sorted_len,
             expert_ids, ntp, slot_to_row);
         return check_launch("align_scan_place_kernel");
     }
@@ -482,7 +478,7 @@ int launch_align(const int32_t* ids, int64_t numel, int64_t E, int64_t block_m,
                                                        numel, eoff, sorted_ids, sorted_len,
                                                        expert_ids, ntp);
     if (int rc = check_launch("align_scan_kernel")) return rc;
-    align_place_kernel<<<(unsigned)nchunks, kAlignThreads, 0, stream>>>(ids, numel, (int)E, emap,
+    align_place_kernel<<<(unsigned)nchunks, kAlignThreads, 0, stream>>>(slot_key, numel, (int)E,
                                                                         counts, eoff,
                                                                         sorted_ids, slot_to_row);
     return check_launch("align_place_kernel");
