@@ -117,8 +117,10 @@ __global__ void slot_reduce_kernel(const float* __restrict__ y, const float* __r
 }
 
 // Prefill combine (moe_kernel.hip:1241-1258 with the inverse map built by the align):
-// eight columns per thread, fp32 accumulation over j ascending.
-template <bool BF16>
+// eight columns per thread, fp32 accumulation over j ascending. KMAX > 0: the token's rows
+// and weights (top_k <= KMAX) are read first and all its row loads go out together;
+// KMAX == 0: any top_k, one row at a time.
+template <bool BF16, int KMAX>
 __global__ void row_reduce_kernel(const __half* __restrict__ y, const int32_t* __restrict__ s2r,
                                   const float* __restrict__ tw, int64_t T, int N, int top_k,
                                   void* __restrict__ out) {
@@ -126,16 +128,34 @@ __global__ void row_reduce_kernel(const __half* __restrict__ y, const int32_t* _
     const int n = (blockIdx.x * blockDim.x + threadIdx.x) * 8;
     if (n >= N || t >= T) return;
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int j = 0; j < top_k; ++j) {
-        const int32_t r = s2r[t * top_k + j];
-        if (r < 0) continue;
-        const float w = tw[t * top_k + j];
-        const uint4 v = *reinterpret_cast<const uint4*>(y + (int64_t)r * N + n);
+    auto add_row = [&](float w, const uint4& v) {
         const uint32_t u[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             acc[2 * i] = fmaf(w, __half2float(__ushort_as_half((unsigned short)(u[i] & 0xFFFFu))), acc[2 * i]);
             acc[2 * i + 1] = fmaf(w, __half2float(__ushort_as_half((unsigned short)(u[i] >> 16))), acc[2 * i + 1]);
+        }
+    };
+    if constexpr (KMAX > 0) {
+        int32_t r[KMAX];
+        float w[KMAX];
+#pragma unroll
+        for (int j = 0; j < KMAX; ++j) {
+            r[j] = j < top_k ? s2r[t * top_k + j] : -1;
+            w[j] = j < top_k ? tw[t * top_k + j] : 0.f;
+        }
+        uint4 v[KMAX];
+#pragma unroll
+        for (int j = 0; j < KMAX; ++j)
+            v[j] = r[j] >= 0 ? *reinterpret_cast<const uint4*>(y + (int64_t)r[j] * N + n) : make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+        for (int j = 0; j < KMAX; ++j)
+            if (r[j] >= 0) add_row(w[j], v[j]);
+    } else {
+        for (int j = 0; j < top_k; ++j) {
+            const int32_t r = s2r[t * top_k + j];
+            if (r < 0) continue;
+            add_row(tw[t * top_k + j], *reinterpret_cast<const uint4*>(y + (int64_t)r * N + n));
         }
     }
     uint32_t o[4];
@@ -256,10 +276,16 @@ int launch_row_reduce(const void* y, const int32_t* s2r, const float* tw, int64_
     }
     dim3 grid(blocks_for(N / 8, 256), (unsigned)T);
     const __half* yh = static_cast<const __half*>(y);
-    if (out_bf16)
-        row_reduce_kernel<true><<<grid, 256, 0, stream>>>(yh, s2r, tw, T, (int)N, (int)top_k, out);
-    else
-        row_reduce_kernel<false><<<grid, 256, 0, stream>>>(yh, s2r, tw, T, (int)N, (int)top_k, out);
+    if (top_k <= 8) {
+        if (out_bf16)
+            row_reduce_kernel<true, 8><<<grid, 256, 0, stream>>>(yh, s2r, tw, T, (int)N, (int)top_k, out);
+        else
+            row_reduce_kernel<false, 8><<<grid, 256, 0, stream>>>(yh, s2r, tw, T, (int)N, (int)top_k, out);
+    } else if (out_bf16) {
+        row_reduce_kernel<true, 0><<<grid, 256, 0, stream>>>(yh, s2r, tw, T, (int)N, (int)top_k, out);
+    } else {
+        row_reduce_kernel<false, 0><<<grid, 256, 0, stream>>>(yh, s2r, tw, T, (int)N, (int)top_k, out);
+    }
     return check_launch("row_reduce_kernel");
 }
 

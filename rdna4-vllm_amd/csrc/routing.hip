@@ -108,13 +108,15 @@ __device__ int chunk_rank(const int32_t* __restrict__ ids, int64_t numel, int64_
 }
 
 // Writes expert_ids, the padding sentinels and ntp from per-expert totals `cnt` and
-// padded offsets `eoff` (both in LDS). One thread per expert.
+// padded offsets `eoff` (both in LDS). One thread per expert; with nwg > 1 work-groups
+// sharing the job, work-group wg takes experts wg, wg + nwg, ... and every nwg-th
+// stretch of the tail.
 __device__ void write_layout(const int* cnt, const int* eoff, int E, int64_t block_m,
                              int64_t numel, int total_padded, int32_t* __restrict__ sorted_ids,
                              int64_t sorted_len, int32_t* __restrict__ expert_ids,
-                             int32_t* __restrict__ ntp) {
+                             int32_t* __restrict__ ntp, int wg = 0, int nwg = 1) {
     const int tid = threadIdx.x;
-    for (int e = tid; e < E; e += kAlignThreads) {
+    for (int e = wg + nwg * tid; e < E; e += nwg * kAlignThreads) {
         const int c = cnt[e];
         if (c == 0) continue;
         const int o = eoff[e];
@@ -123,11 +125,12 @@ __device__ void write_layout(const int* cnt, const int* eoff, int E, int64_t blo
         for (int b = (int)(o / block_m); b < (int)((o + padded) / block_m); ++b)
             expert_ids[b] = e;
     }
-    for (int64_t r = total_padded + tid; r < sorted_len; r += kAlignThreads)
+    const int64_t step = (int64_t)nwg * kAlignThreads;
+    for (int64_t r = total_padded + (int64_t)wg * kAlignThreads + tid; r < sorted_len; r += step)
         sorted_ids[r] = (int32_t)numel;
-    for (int64_t b = total_padded / block_m + tid; b < sorted_len / block_m; b += kAlignThreads)
+    for (int64_t b = total_padded / block_m + (int64_t)wg * kAlignThreads + tid; b < sorted_len / block_m; b += step)
         expert_ids[b] = -1;
-    if (tid == 0) ntp[0] = total_padded;
+    if (wg == 0 && tid == 0) ntp[0] = total_padded;
 }
 
 // Single launch for numel <= kChunk.
@@ -247,9 +250,15 @@ __global__ void __launch_bounds__(kAlignThreads) align_scan_place_kernel(
     __syncthreads();
     for (int x = tid; x < E; x += kAlignThreads) {
         int run = 0, mine = 0;
-        for (int c = 0; c < nchunks; ++c) {
-            if (c == b) mine = run;
-            run += lc[c * E + x];
+        for (int c0 = 0; c0 < nchunks; c0 += 8) {   // eight independent reads per pass
+            int cv[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) cv[u] = c0 + u < nchunks ? lc[(c0 + u) * E + x] : 0;
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                if (c0 + u == b) mine = run;
+                run += cv[u];
+            }
         }
         cnt[x] = run;
         base[x] = mine;
@@ -264,8 +273,8 @@ __global__ void __launch_bounds__(kAlignThreads) align_scan_place_kernel(
     const int row = e >= 0 ? eoff[e] + base[e] + (key >> 10) : -1;
     if (e >= 0) sorted_ids[row] = (int32_t)slot;
     if (slot_to_row != nullptr && slot < numel) slot_to_row[slot] = row;
-    if (b == 0)
-        write_layout(cnt, eoff, E, block_m, numel, total, sorted_ids, sorted_len, expert_ids, ntp);
+    write_layout(cnt, eoff, E, block_m, numel, total, sorted_ids, sorted_len, expert_ids, ntp, b,
+                 nchunks);
 }
 
 // Multi-chunk phase 3: stable placement.
