@@ -143,6 +143,25 @@ def test_align_zipf_skew_and_expert_map():
         assert np.array_equal(sti.cpu().numpy(), so) and np.array_equal(eid.cpu().numpy(), eo)
 
 
+@pytest.mark.parametrize("numel", [512, 1024, 32768, 65536 + 37])
+def test_align_degenerate_ids(numel):
+    """Every slot on one expert (one wave holds 64 equal ids), repeated ids inside a token,
+    and ids outside [0, E) (dropped): the per-wave ballot ranks against the oracle."""
+    r = rng(numel)
+    E, k, bm = 256, 8, 64
+    cases = [np.full(numel, 17, np.int32),
+             r.integers(0, 3, numel).astype(np.int32),
+             np.where(r.random(numel) < 0.1, -1,
+                      np.where(r.random(numel) < 0.05, E + 5, r.integers(0, E, numel))).astype(np.int32)]
+    for ids in cases:
+        ids2 = ids.reshape(-1, 1) if numel % k else ids.reshape(-1, k)
+        sti, eid, ntp = W.moe_align_block_size(torch.from_numpy(ids2).to(DEV), bm, E)
+        so, eo, no = O.moe_align(ids2, bm, E)
+        assert int(ntp.item()) == int(no[0])
+        assert np.array_equal(sti.cpu().numpy(), so)
+        assert np.array_equal(eid.cpu().numpy(), eo)
+
+
 # --------------------------------------------------------------------------- #
 # grouped GEMMs
 # --------------------------------------------------------------------------- #
