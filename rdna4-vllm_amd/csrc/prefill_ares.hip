@@ -7,24 +7,28 @@
 //   * a work-group owns 64 consecutive sorted rows (one expert) and ALL N columns: its e4m3
 //     activation tile (64 x K bytes) and the rows' per-group sums are loaded into LDS once,
 //     then the kernel streams the expert's int4 weights past them, 256 weight rows at a time
-//     (a "range": 4 waves x 4 16-column fragments; SiLU: 128 gate + the matching 128 up
-//     columns);
+//     (a "range": 8 waves, two per SIMD, x 2 16-column fragments; SiLU: 128 gate + the
+//     matching 128 up columns);
 //   * tiles are taken in an XCD-aware order: work-group b runs sorted tile
 //     (b % 8) * ceil(tiles / 8) + b / 8, so each XCD walks a contiguous run of tiles and the
 //     tiles of one expert share that XCD's L2 while they stream the same weights;
 //   * inside a range each wave keeps the next 4 (range, K group) steps' B fragments in flight
 //     (raw int4 words, 16 B per lane per fragment). Load addresses are a wave-uniform step
 //     offset plus a fixed per-lane offset, so they cost scalar instructions only; issues are
-//     unconditional (steps past the end reload the slab's start), so wait counts stay exact;
+//     unconditional (steps past the end reload the last range's final groups), so wait
+//     counts stay exact;
 //   * per step and live 16-row fragment: v_mfma_f32_16x16x128_f8f6f4 on the raw-nibble B
-//     (n * 2^-9, two ANDs and a shift), then the fp32 scale fold run += acc * scale[n, g]
-//     (moe_gemm_tiled.h:144-151) with the scale read from a per-wave LDS table;
+//     (n * 2^-9, two ANDs and a shift) with the operands swapped, so lane (q, c16) holds
+//     tile row c16, columns 4q..4q+3; then the fp32 scale fold run += acc * scale[n, g]
+//     (moe_gemm_tiled.h:144-151) with the lane's four scales read from a per-wave LDS table;
 //   * the range's scales and zero-points are fetched one range ahead into registers; at a
-//     range boundary each wave writes the scale table and s*z (bf16 hi/lo) for its own 64
-//     columns, so no work-group barrier follows the prologue;
+//     range boundary each wave writes the scale table and s*z (bf16 hi/lo) for its own 32
+//     weight rows, so no work-group barrier follows the prologue;
 //   * after the last group of a range the zero-point term sum_g sum_k a * z * s is formed by
-//     bf16 MFMAs over (row group sums) x (s*z), out = asc * (512 * run - term) is stored
-//     (fp16, or fp16 SiLU(gate) * up) and the accumulators restart;
+//     bf16 MFMAs over (row group sums) x (s*z), out = asc * (512 * run - term) is stored as
+//     8-byte row pieces (fp16, or fp16 SiLU(gate) * up) and the accumulators restart;
+//   * the two waves of a SIMD take turns at the higher issue priority, one range each, so
+//     neither ends a tile far behind the other;
 //   * the main loop is instantiated per live 16-row fragment count (1..4), so partial tiles
 //     run straight-line code without per-fragment branches.
 #include <algorithm>
