@@ -54,10 +54,7 @@ __device__ __forceinline__ void quantize_row_regs(const RowRegs& rr, int64_t row
 // Group sum of one 512-wide pass (lanes 16j..16j+15 hold group k/128): fixed-order tree.
 __device__ __forceinline__ void row_group_sum(uint32_t lo, uint32_t hi, int64_t row, int K, int k,
                                               float* __restrict__ gsum, int lane) {
-    float t = 0.f;
-#pragma unroll
-    for (int b = 0; b < 4; ++b)
-        t += e4m3_to_f32((lo >> (8 * b)) & 0xFF) + e4m3_to_f32((hi >> (8 * b)) & 0xFF);
+    float t = e4m3_pair_sum(0.f, lo, hi);
     t = lane_allreduce<4>(t, SumOp{});
     if ((lane & 15) == 0 && k < K) gsum[row * (K / 128) + k / 128] = t;
 }

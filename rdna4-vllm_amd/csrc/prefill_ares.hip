@@ -349,10 +349,7 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
                 const int k = ps * 512 + lane * 8;
                 *reinterpret_cast<uint2*>(s_a + ar_a_off(m, k / kGroup, (k % kGroup) / 16) + 8 * (lane & 1)) =
                     make_uint2(lo, hi);
-                float t = 0.f;
-#pragma unroll
-                for (int b = 0; b < 4; ++b)
-                    t += e4m3_to_f32((lo >> (8 * b)) & 0xFF) + e4m3_to_f32((hi >> (8 * b)) & 0xFF);
+                float t = e4m3_pair_sum(0.f, lo, hi);
                 t = lane_allreduce<4>(t, SumOp{});
                 if ((lane & 15) == 0) {
                     const __bf16 h = (__bf16)t;

@@ -76,6 +76,19 @@ __device__ __forceinline__ uint32_t pack4_e4m3(float a, float b, float c, float 
 __device__ __forceinline__ float e4m3_to_f32(uint32_t byte) {
     return __builtin_amdgcn_cvt_f32_fp8(static_cast<int>(byte), 0);
 }
+// Sum of a word's four e4m3 bytes, byte 0 first (bytes converted in pairs in place)
+// plus the same of a second word: t + e(a0) + e(b0) + e(a1) + e(b1) + ... in that order.
+__device__ __forceinline__ float e4m3_pair_sum(float t, uint32_t a, uint32_t b) {
+    const auto a01 = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(a), false);
+    const auto a23 = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(a), true);
+    const auto b01 = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(b), false);
+    const auto b23 = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(b), true);
+    t += a01[0] + b01[0];
+    t += a01[1] + b01[1];
+    t += a23[0] + b23[0];
+    t += a23[1] + b23[1];
+    return t;
+}
 
 // 16-entry byte lookup of each byte of x (values 0..15) in table t.
 // v_perm_b32 selects from 8 bytes; entries 8..15 come from a second select, and the
