@@ -44,7 +44,11 @@ PINNING = {
     "awq_to_op_layout / convert_awq_tensor / wna16_to_op_layout": "dequant equality "
         "against the unpacked ground truth (reference test property) + round trips",
     "moe_layer": "float64 un-quantised MoE within the fp8 quantisation error bound; "
-                 "composition equals the per-stage oracle chain",
+                 "composition equals the per-stage oracle chain; biases: closed form on a "
+                 "zero-weight layer and the per-stage chain with torch fp16 adds",
+    "expert_weights_f64": "equals the e4m3 byte round trip E4M3_TO_F64[dequant_codes] on "
+                           "random weights, sym and asym (exhaustive table test covers all "
+                           "256 nibble/zero-point pairs)",
     "repack_fragments": "per-element brute force of the layout definition on tiny shapes "
                         "(nibble of row n, k lands in lane n % 16 + 16 * ((k % 128) // 32)); "
                         "inverse restores the op layout exactly",
@@ -315,9 +319,20 @@ def moe_align(topk_ids, block_m: int, num_experts: int, expert_map=None):
 # --------------------------------------------------------------------------- #
 
 
-def _expert_weights_f64(w_packed_e, w_zeros_e, group_size, e2m1):
-    codes = dequant_codes(w_packed_e, w_zeros_e, group_size, e2m1)
-    return E4M3_TO_F64[codes]
+def expert_weights_f64(w_packed_e, w_zeros_e, group_size, e2m1):
+    """One expert's weights as the float64 values of their e4m3 codes. For int4 these are
+    the integers (nibble - zp) in [-15, 15], which e4m3 holds exactly (the exhaustive table
+    test pins decode(encode(n - z)) == n - z for all 256 pairs), so they are formed directly
+    instead of through the byte round trip; E2M1 goes through the codebook."""
+    if e2m1:
+        return E4M3_TO_F64[dequant_codes(w_packed_e, None, group_size, True)]
+    nib = unpack_nibbles(w_packed_e).astype(np.int16)
+    G = nib.shape[-1] // group_size
+    if w_zeros_e is None or np.asarray(w_zeros_e).size == 0:
+        zp = np.full(nib.shape[:-1] + (G,), 8, dtype=np.int16)
+    else:
+        zp = unpack_zeros(w_zeros_e, nib.shape[-2]).astype(np.int16)
+    return (nib - np.repeat(zp, group_size, axis=-1)).astype(np.float64)
 
 
 def grouped_run(a_codes, row_expert, w_packed, scales, w_zeros=None,
@@ -340,13 +355,15 @@ def grouped_run(a_codes, row_expert, w_packed, scales, w_zeros=None,
         if e < 0 or e >= E:
             continue
         idx = np.nonzero(row_expert == e)[0]
-        W = _expert_weights_f64(wp[e], None if zs is None else zs[e], group_size, e2m1)
-        Ae = A[idx]
+        W = expert_weights_f64(wp[e], None if zs is None else zs[e], group_size, e2m1)
+        # every group's partial sums in one batched product: (G, R, gs) @ (G, gs, N); exact
+        # in float64 (products of e4m3 and small integers), then one rounding to fp32
+        Ag = A[idx].reshape(idx.size, G, group_size).transpose(1, 0, 2)
+        Wg = W.reshape(N, G, group_size).transpose(1, 2, 0)
+        part = np.matmul(Ag, Wg).astype(np.float32)
         r = np.zeros((idx.size, N), dtype=np.float32)
         for g in range(G):
-            ks = slice(g * group_size, (g + 1) * group_size)
-            part = (Ae[:, ks] @ W[:, ks].T).astype(np.float32)   # exact, then one rounding
-            r = fma32(part, sc[e, :, g][None, :], r)
+            r = fma32(part[g], sc[e, :, g][None, :], r)
         run[idx] = r
     return run
 
@@ -460,20 +477,37 @@ def dense_gemm(x16, w_packed, scales, w_zeros=None, e2m1: bool = False) -> np.nd
 # --------------------------------------------------------------------------- #
 
 
+def _add_bias_f16(v16, bias, experts):
+    """fp16 tensor + per-expert fp16 bias row, as torch adds two fp16 tensors: exact sum of
+    the two values rounded once to fp16 (moe_experts.py:565-575, the unfused path's
+    ``out + _expand_bias(bias).to(out.dtype)``). Rows with an out-of-range expert use
+    expert 0's row, as the reference's ``expert_ids.clamp(min=0)`` does for padding."""
+    b = np.asarray(bias, dtype=np.float16)
+    e = np.clip(np.asarray(experts).astype(np.int64), 0, b.shape[0] - 1)
+    return (np.asarray(v16, np.float16).astype(np.float32)
+            + b[e].astype(np.float32)).astype(np.float16)
+
+
 def moe_layer(x, w13, s13, z13, w2, s2, z2, topk_weights, topk_ids,
               group_size: int = 128, round_y_fp16: bool = True, e2m1: bool = False,
-              return_stages: bool = False):
+              return_stages: bool = False, w1_bias=None, w2_bias=None, expert_map=None):
     """Whole gated MoE in token order (moe_experts.py:493-665, arithmetic per
     test_moe_experts.py:155-191 with the kernel SiLU moe_kernel.hip:555-561):
       x16 = fp16(x); a1,s1 = act_quant(x16); run1 over w13 per (t, j);
-      gate/up = fp16(run1 * s1); h = silu_and_mul; a2,s2 = act_quant(h);
+      gate/up = fp16(run1 * s1) (+ fp16 w1_bias[e]); h = silu_and_mul; a2,s2 = act_quant(h);
       y = run2 * s2 (fp16-rounded on the prefill path, moe_gemm_tiled.h:346; not on
-      the decode scatter path, moe_kernel.hip:1056);
+      the decode scatter path, moe_kernel.hip:1056; always fp16 with a w2_bias, which is
+      added to the fp16 rows, moe_experts.py:654-655);
       out[t] = sum_{j ascending} w[t,j] * y[t,j] in fp32.
+    With ``expert_map`` (global id -> local expert or -1) slots without a local expert add
+    nothing (moe_experts.py:587-589 aligns with global_num_experts and the map).
     ``x`` is float32 (holding bf16 or fp16 values). Returns float32 (T, H)."""
     x16 = np.asarray(x, dtype=np.float32).astype(np.float16)
     T, H = x16.shape
     ids = np.asarray(topk_ids).astype(np.int64)
+    if expert_map is not None:
+        em = np.asarray(expert_map).astype(np.int64)
+        ids = np.where((ids >= 0) & (ids < em.size), em[np.clip(ids, 0, em.size - 1)], -1)
     k = ids.shape[1]
     I2 = np.asarray(w13).shape[1]
     inter = I2 // 2
@@ -481,11 +515,15 @@ def moe_layer(x, w13, s13, z13, w2, s2, z2, topk_weights, topk_ids,
     tok = np.repeat(np.arange(T), k)
     run1 = grouped_run(a1[tok], ids.reshape(-1), w13, s13, z13, group_size, e2m1)
     g1 = (run1 * sc1[tok][:, None]).astype(np.float32).astype(np.float16)
+    if w1_bias is not None:
+        g1 = _add_bias_f16(g1, w1_bias, ids.reshape(-1))
     h = silu_and_mul(g1[:, :inter], g1[:, inter:])
     a2, sc2 = act_quant(h)
     run2 = grouped_run(a2, ids.reshape(-1), w2, s2, z2, group_size, e2m1)
     y = (run2 * sc2[:, None]).astype(np.float32)
-    if round_y_fp16:
+    if w2_bias is not None:
+        y = _add_bias_f16(y.astype(np.float16), w2_bias, ids.reshape(-1)).astype(np.float32)
+    elif round_y_fp16:
         y = y.astype(np.float16).astype(np.float32)
     tw = np.asarray(topk_weights, dtype=np.float32).reshape(T, k)
     y = y.reshape(T, k, H)

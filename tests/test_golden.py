@@ -8,6 +8,7 @@ import os
 
 import numpy as np
 import pytest
+import torch
 
 import oracle as O
 
@@ -137,3 +138,42 @@ def test_gpu_layer_fixture(gpu):
     got = out.float().cpu().numpy()
     ref = g["out"]
     assert np.abs(got - ref).max() / np.abs(ref).max() <= 1e-2
+
+
+def _conversion_cases():
+    f = load("conversion_ref.npz")
+    n = len({k.split("_")[0] for k in f})
+    return f, n
+
+
+def test_awq_conversion_matches_reference_vectors():
+    """AWQ -> op layout: the oracle and the torch converter both reproduce the vectors the
+    reference's own numpy conversion test wrote (tests/golden/make_conversion_golden.py),
+    which pins the AWQ nibble order independently of this repository's packer."""
+    from w4a8_fp8_wmma import moe_experts
+    f, n = _conversion_cases()
+    for i in range(n):
+        c = lambda k: f[f"c{i}_{k}"]  # noqa: E731
+        g = int(c("group"))
+        w, s, z = O.awq_to_op_layout(c("awq_qweight"), c("scales"), c("awq_qzeros"))
+        assert np.array_equal(w, c("awq_w_op")) and np.array_equal(z, c("awq_z_op"))
+        assert np.array_equal(s, c("awq_s_op"))
+        tw, ts, tz = moe_experts._awq_moe_to_op_layout(
+            torch.from_numpy(c("awq_qweight")), torch.from_numpy(c("scales")),
+            torch.from_numpy(c("awq_qzeros")), g)
+        assert np.array_equal(tw.numpy(), c("awq_w_op")) and np.array_equal(tz.numpy(), c("awq_z_op"))
+        # the converted nibbles are the ground-truth values the reference packed
+        assert np.array_equal(O.unpack_nibbles(w), np.swapaxes(c("qvals"), 1, 2))
+        assert np.array_equal(O.unpack_zeros(z, w.shape[1]), np.swapaxes(c("zeros"), 1, 2))
+        # and our AWQ packer writes the reference's words
+        assert np.array_equal(O.awq_pack(c("qvals")), c("awq_qweight"))
+
+
+def test_ct_conversion_matches_reference_vectors():
+    from w4a8_fp8_wmma import moe_experts
+    f, n = _conversion_cases()
+    for i in range(n):
+        c = lambda k: f[f"c{i}_{k}"]  # noqa: E731
+        cw, _ = moe_experts._ct_moe_to_op_layout(torch.from_numpy(c("gptq_qweight")),
+                                                 torch.from_numpy(c("scales")))
+        assert np.array_equal(cw.numpy(), c("ct_w_op"))

@@ -219,3 +219,82 @@ def test_layer_equals_stage_chain():
     lay = O.moe_layer(d["x"], d["w13"], d["s13"], d["z13"], d["w2"], d["s2"], d["z2"],
                       d["tw"], d["ids"], round_y_fp16=True)
     assert np.array_equal(chain, lay)
+
+
+@pytest.mark.parametrize("asym", [True, False])
+def test_integer_weights_equal_e4m3_round_trip(asym):
+    """The oracle's fast weight path (n - z as integers) equals decoding the e4m3 bytes the
+    kernels' tables produce, element for element."""
+    r = np.random.default_rng(23)
+    _, _, _, w, zz = make_weights(r, 2, 32, 512, 128, asym)
+    for e in range(2):
+        fast = O.expert_weights_f64(w[e], None if zz is None else zz[e], 128, False)
+        codes = O.dequant_codes(w[e], None if zz is None else zz[e], 128)
+        assert np.array_equal(fast, O.E4M3_TO_F64[codes])
+
+
+def test_layer_biases_closed_form():
+    """Zero weights: gemm1 gives exact zeros, so gate/up are the w1 bias itself and
+    out[t] = sum_j w_j * fp16(0 + b2[e_j]) with h = silu(b_gate) * b_up ignored by gemm2."""
+    r = np.random.default_rng(24)
+    T, E, H, I, k = 5, 4, 256, 128, 2
+    w13 = O.pack_nibbles(np.full((E, 2 * I, H), 8))
+    w2 = O.pack_nibbles(np.full((E, H, I), 8))
+    s13 = np.full((E, 2 * I, H // 128), 0.01, np.float16)
+    s2 = np.full((E, H, I // 128), 0.01, np.float16)
+    b1 = r.standard_normal((E, 2 * I)).astype(np.float16)
+    b2 = r.standard_normal((E, H)).astype(np.float16)
+    x = r.standard_normal((T, H)).astype(np.float32)
+    tw, ids = O.topk_softmax(r.standard_normal((T, E)).astype(np.float32), k)
+    out, st = O.moe_layer(x, w13, s13, None, w2, s2, None, tw, ids, w1_bias=b1, w2_bias=b2,
+                          return_stages=True)
+    e = ids.reshape(-1)
+    assert np.array_equal(st["g1"], b1[e])
+    exp = np.zeros((T, H), np.float32)
+    for j in range(k):
+        exp = O.fma32(tw[:, j:j + 1], b2[ids[:, j]].astype(np.float32), exp)
+    assert np.array_equal(out, exp)
+
+
+def test_layer_biases_equal_stage_chain():
+    """With biases the layer equals the per-op chain with torch's fp16 adds in between
+    (moe_experts.py:565-575,654-655)."""
+    import torch
+    r = np.random.default_rng(25)
+    d = layer_inputs(r, T=6, E=4, k=2)
+    E, N13 = d["w13"].shape[:2]
+    b1 = r.standard_normal((E, N13)).astype(np.float16)
+    b2 = r.standard_normal((E, d["w2"].shape[1])).astype(np.float16)
+    T, k = d["ids"].shape
+    bm = 8
+    sti, eid, ntp = O.moe_align(d["ids"], bm, 4)
+    row_e = np.repeat(np.maximum(eid, 0), bm)[:sti.size]
+    x16 = d["x"].astype(np.float16)
+    o1, valid = O.grouped_gemm_padded(x16, d["w13"], d["s13"], d["z13"], sti, eid, ntp, k, bm)
+    o1 = (torch.from_numpy(np.nan_to_num(o1)) + torch.from_numpy(b1[row_e])).numpy()
+    I = o1.shape[1] // 2
+    h = O.silu_and_mul(o1[:, :I], o1[:, I:])
+    P = sti.size
+    ident = np.where(valid, np.arange(P), P).astype(np.int32)
+    o2, _ = O.grouped_gemm_padded(h, d["w2"], d["s2"], d["z2"], ident, eid, ntp, 1, bm)
+    o2 = (torch.from_numpy(np.nan_to_num(o2)) + torch.from_numpy(b2[row_e])).numpy()
+    chain = O.gather_reduce(o2, sti, d["tw"].reshape(-1), ntp, k)
+    lay = O.moe_layer(d["x"], d["w13"], d["s13"], d["z13"], d["w2"], d["s2"], d["z2"],
+                      d["tw"], d["ids"], w1_bias=b1, w2_bias=b2)
+    assert np.array_equal(chain, lay)
+
+
+def test_layer_expert_map_equals_local_subset():
+    """Global ids 0..7 with experts 4..7 local (as 0..3): the layer equals the same layer on
+    the local weights with the non-local slots' router weights set to zero."""
+    r = np.random.default_rng(26)
+    d = layer_inputs(r, T=7, E=4, k=3)
+    ids_g = r.integers(0, 8, (7, 3)).astype(np.int32)
+    emap = np.array([-1, -1, -1, -1, 0, 1, 2, 3], np.int32)
+    got = O.moe_layer(d["x"], d["w13"], d["s13"], d["z13"], d["w2"], d["s2"], d["z2"],
+                      d["tw"], ids_g, expert_map=emap)
+    local = np.where(ids_g >= 4, ids_g - 4, 0)
+    tw0 = np.where(ids_g >= 4, d["tw"], 0).astype(np.float32)
+    ref = O.moe_layer(d["x"], d["w13"], d["s13"], d["z13"], d["w2"], d["s2"], d["z2"],
+                      tw0, local)
+    assert np.array_equal(got, ref)
