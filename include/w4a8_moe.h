@@ -91,8 +91,10 @@ W4A8_API int w4a8_topk_softmax(const float* logits, int64_t T, int64_t E, int64_
  * by test_moe_experts.py:136-152). Groups slots t*top_k+j by expert ascending, slot
  * ascending, pads each expert to a multiple of block_m with the sentinel numel.
  * sorted_len must equal w4a8_moe_align_sorted_len(); entries past ntp hold the
- * sentinel and expert_ids -1. expert_map (num_experts entries, -1 = not local) may be
- * NULL. Deterministic (no atomics decide the order).
+ * sentinel and expert_ids -1. num_experts is the global count (the range of topk_ids);
+ * expert_map (num_experts entries, -1 = not local) may be NULL; mapped ids must be below
+ * num_experts and slots mapped to -1 are dropped. Deterministic (no atomics decide the
+ * order).
  */
 W4A8_API int64_t w4a8_moe_align_sorted_len(int64_t numel, int64_t num_experts, int64_t block_m);
 W4A8_API size_t w4a8_moe_align_workspace_size(int64_t numel, int64_t num_experts);
@@ -178,7 +180,12 @@ W4A8_API int w4a8_mmq_fp8_gemm(const void* x_f16, int64_t M, int64_t K, const in
  * (moe_experts.py:1308-1332). x (T, H) in x_dtype -> out (T, H) in x_dtype.
  * w13 (E, 2*inter, H/8), w2 (E, H, inter/8); scales/zeros as above (zeros may be
  * NULL per weight). topk_ids (T, top_k) int32, topk_weights (T, top_k) fp32.
- * expert_map may be NULL. Chooses the decode (T <= 96) or prefill schedule itself.
+ * E is the LOCAL expert count (w13.shape[0]). topk_ids hold global expert ids in
+ * [0, num_global_experts) (vLLM's global_num_experts, moe_experts.py:587-589); with an
+ * expert_map (num_global_experts int32 entries, -1 = not local) each id is mapped to a local
+ * expert in [0, E) and slots without one contribute nothing. Without a map,
+ * num_global_experts must be E (or <= 0, meaning E). Chooses the decode (T <= 96) or
+ * prefill schedule itself.
  */
 W4A8_API size_t w4a8_moe_apply_workspace_size(int64_t T, int64_t H, int64_t inter, int64_t E,
                                      int64_t top_k);
@@ -187,8 +194,8 @@ W4A8_API int w4a8_moe_apply(const void* x, int x_dtype, int64_t T, int64_t H, in
                    const int32_t* w13, const void* w13_scales_f16, const int32_t* w13_zeros,
                    const int32_t* w2, const void* w2_scales_f16, const int32_t* w2_zeros,
                    const float* topk_weights, const int32_t* topk_ids,
-                   const int32_t* expert_map, int weight_is_e2m1, void* out,
-                   void* workspace, size_t workspace_bytes, void* stream);
+                   const int32_t* expert_map, int64_t num_global_experts, int weight_is_e2m1,
+                   void* out, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Load-time repack of int4 weights from the op layout (E, N, K/8) int32 (moe_kernel.hip:7-17)
  * into the fragment layout the gfx950 kernels stream: per expert, 16-row tile t and 128-wide
@@ -202,8 +209,9 @@ W4A8_API int w4a8_repack_int4_fragments(const int32_t* w_packed, int64_t E, int6
 
 /* w4a8_moe_apply on weights repacked by w4a8_repack_int4_fragments (w13 and w2); scales
  * and zero-points stay in the op layout. Same workspace (w4a8_moe_apply_workspace_size) and
- * bit-identical results. Needs group_size 128, int4 weights (no E2M1), and hidden and
- * intermediate sizes that are multiples of 128 with K/128 in {1,2,3,4,8,12,16} and <= 32.
+ * bit-identical results. Needs group_size 128 and int4 weights (no E2M1); hidden and
+ * intermediate sizes must be multiples of 128 that the schedule chosen for T takes: the
+ * decode GEMV (T <= 96) needs K/128 in {1,2,3,4,8,12,16,32}, the prefill tiles K <= 4096.
  * No reference counterpart (the reference's composition, moe_experts.py:493-665, runs on
  * the op layout). */
 W4A8_API int w4a8_moe_apply_fragments(const void* x, int x_dtype, int64_t T, int64_t H,
@@ -212,34 +220,43 @@ W4A8_API int w4a8_moe_apply_fragments(const void* x, int x_dtype, int64_t T, int
                                       const int32_t* w13_zeros, const int32_t* w2_frag,
                                       const void* w2_scales_f16, const int32_t* w2_zeros,
                                       const float* topk_weights, const int32_t* topk_ids,
-                                      const int32_t* expert_map, void* out, void* workspace,
-                                      size_t workspace_bytes, void* stream);
+                                      const int32_t* expert_map, int64_t num_global_experts,
+                                      void* out, void* workspace, size_t workspace_bytes,
+                                      void* stream);
+
+/* 1 when w4a8_moe_apply_fragments accepts weights of this shape for every T (both the
+ * decode and the prefill schedule take it), else 0: what a load hook checks before it
+ * repacks. No reference counterpart (layout query). */
+W4A8_API int w4a8_moe_fragments_supported(int64_t H, int64_t inter, int64_t group_size);
 
 /* Weight layouts for w4a8_moe_forward. */
 #define W4A8_WEIGHTS_OP 0          /* (E, N, K/8) int32, the reference op layout */
 #define W4A8_WEIGHTS_FRAGMENTS 1   /* w4a8_repack_int4_fragments output */
 
-/* Router + expert path in one call: softmax / top-k / renormalise of router_logits (T, E)
- * fp32 (the vLLM fused_topk the reference's caller runs before apply; ties go to the lower
- * expert id), then w4a8_moe_apply (op layout) or w4a8_moe_apply_fragments on the result.
- * topk_weights (T, top_k) fp32 and topk_ids (T, top_k) int32 are outputs. Same workspace
- * size as w4a8_moe_apply. No single reference counterpart (fused_topk is vLLM's, moe_experts.py:493-665 the
- * rest). */
+/* Router + expert path in one call: softmax / top-k / renormalise of router_logits
+ * (T, num_global_experts) fp32 (the vLLM fused_topk the reference's caller runs before apply;
+ * ties go to the lower expert id), then w4a8_moe_apply (op layout) or
+ * w4a8_moe_apply_fragments on the result (expert_map / num_global_experts as there).
+ * topk_weights (T, top_k) fp32 and topk_ids (T, top_k) int32 (global ids) are outputs. Same
+ * workspace size as w4a8_moe_apply. No single reference counterpart (fused_topk is vLLM's,
+ * moe_experts.py:493-665 the rest). */
 W4A8_API int w4a8_moe_forward(const void* x, int x_dtype, int64_t T, int64_t H, int64_t inter,
                               int64_t E, int64_t top_k, int64_t group_size,
                               const float* router_logits, int renormalize, const int32_t* w13,
                               const void* w13_scales_f16, const int32_t* w13_zeros,
                               const int32_t* w2, const void* w2_scales_f16,
                               const int32_t* w2_zeros, int weights_layout,
-                              const int32_t* expert_map, float* topk_weights, int32_t* topk_ids,
-                              void* out, void* workspace, size_t workspace_bytes, void* stream);
+                              const int32_t* expert_map, int64_t num_global_experts,
+                              float* topk_weights, int32_t* topk_ids, void* out,
+                              void* workspace, size_t workspace_bytes, void* stream);
 
-/* Optional per-stage timing of w4a8_moe_apply on the calling thread: when count == 8,
- * the next w4a8_moe_apply calls record events[0] before the first launch and events[i]
- * after stage i (1 align, 2 act-quant x, 3 reserved (empty), 4 gemm1+SiLU, 5 act-quant
- * h, 6 gemm2, 7 reduce/cast) on their stream. With count == 9, events[8] is recorded
- * immediately after events[1] (an empty bracket right after a kernel: the marker latency
- * included in every stage time). Events are hipEvent_t handles owned by the caller;
+/* Optional per-stage timing of the whole-layer calls on the calling thread: when count >= 8,
+ * the next w4a8_moe_apply / _fragments / w4a8_moe_forward calls record events[0] before the
+ * first expert-path launch and events[i] after stage i (1 align, 2 act-quant x, 3 reserved
+ * (empty), 4 gemm1+SiLU, 5 act-quant h, 6 gemm2, 7 reduce/cast) on their stream. With
+ * count == 12, events[8] / events[9] are also stamped at the start / end of the gemm1 kernel
+ * itself and events[10] / events[11] of the gemm2 kernel (hipExtLaunchKernel: the kernel's
+ * own duration, no marker latency). Events are hipEvent_t handles owned by the caller;
  * count == 0 switches recording off. No reference counterpart (measurement aid). */
 W4A8_API int w4a8_moe_apply_set_stage_events(void* const* events, int count);
 

@@ -87,6 +87,11 @@ int run_grouped(GroupedArgs& a, int64_t kernel, void* ws, size_t ws_bytes, hipSt
                                   filter ? a.sorted_ids : nullptr, filter ? a.ntp : nullptr,
                                   a.num_valid, a.act_group_sums))
         return rc;
+    // activation-resident tiles where the shape allows (the whole-layer prefill kernel, so
+    // the op API and moe_apply share it), the streamed-K tiles otherwise
+    if (prefill && prefill_ares_supported(a.K, a.N, a.group_size, a.e2m1, a.block_m, a.epi) &&
+        a.x_rows * a.K < ((int64_t)1 << 31))
+        return launch_grouped_prefill_ares(a, s);
     if (prefill) return launch_grouped_prefill(a, s);
     if (tiles) return launch_grouped_mfma(a, s);
     return launch_grouped_scalar(a, s);
@@ -95,6 +100,11 @@ int run_grouped(GroupedArgs& a, int64_t kernel, void* ws, size_t ws_bytes, hipSt
 }  // namespace
 
 void set_error(const std::string& msg) { g_error = msg; }
+
+KernelStamp& next_kernel_stamp() {
+    thread_local KernelStamp stamp;
+    return stamp;
+}
 void clear_error() { g_error.clear(); }
 
 int check_launch(const char* what) {
@@ -159,17 +169,33 @@ void carve_apply(WS& w, const ApplyPlan& pl, int64_t T, int64_t H, int64_t inter
 }
 
 constexpr int kStageEvents = 8;
-constexpr int kStageCalib = 8;   // optional 9th event: recorded right after event 1
-thread_local hipEvent_t g_stage_events[kStageEvents + 1];
+constexpr int kStampEvents = 4;   // optional: kernel-exact start / stop of gemm1 and gemm2
+thread_local hipEvent_t g_stage_events[kStageEvents + kStampEvents];
 thread_local bool g_stage_on = false;
-thread_local bool g_stage_calib = false;
+thread_local bool g_stage_stamps = false;
 
 inline void stage_mark(int i, hipStream_t s) {
     if (!g_stage_on) return;
     (void)hipEventRecord(g_stage_events[i], s);
-    // an empty bracket directly after a kernel launch: the marker latency every stage
-    // time includes
-    if (i == 1 && g_stage_calib) (void)hipEventRecord(g_stage_events[kStageCalib], s);
+}
+
+// Arms (gemm = 0 / 1) or clears (gemm < 0) the kernel-exact stamps of the next GEMM launch.
+inline void stamp_gemm(int gemm) {
+    if (!g_stage_on || !g_stage_stamps) return;
+    KernelStamp& st = next_kernel_stamp();
+    if (gemm < 0) {
+        st = KernelStamp{};
+        return;
+    }
+    st.start = g_stage_events[kStageEvents + 2 * gemm];
+    st.stop = g_stage_events[kStageEvents + 2 * gemm + 1];
+}
+
+// Fragment-layout weights are read by the decode GEMV and the prefill tiles only.
+bool fragments_schedule_ok(bool decode, int64_t H, int64_t inter, int64_t gs) {
+    if (gs != 128 || H % 128 != 0 || inter % 128 != 0) return false;
+    if (decode) return gemv_supported(H, gs) && gemv_supported(inter, gs);
+    return prefill_supported(H, gs, false) && prefill_supported(inter, gs, false);
 }
 
 struct SizeProbe {
@@ -193,8 +219,8 @@ int moe_apply_impl(const void* x, int x_dtype, int64_t T, int64_t H, int64_t int
                    const void* w13_scales_f16, const int32_t* w13_zeros, const int32_t* w2,
                    const void* w2_scales_f16, const int32_t* w2_zeros,
                    const float* topk_weights, const int32_t* topk_ids,
-                   const int32_t* expert_map, int weight_is_e2m1, void* out, void* workspace,
-                   size_t workspace_bytes, void* stream, bool frag,
+                   const int32_t* expert_map, int64_t n_global, int weight_is_e2m1, void* out,
+                   void* workspace, size_t workspace_bytes, void* stream, bool frag,
                    const float* logits = nullptr, bool renormalize = true) {
     W4A8_REQUIRE(x_dtype == W4A8_DTYPE_F16 || x_dtype == W4A8_DTYPE_BF16, "x dtype must be fp16 or bf16");
     W4A8_REQUIRE(T >= 0 && H > 0 && inter > 0 && E > 0 && top_k > 0, "moe_apply: invalid sizes");
@@ -204,18 +230,21 @@ int moe_apply_impl(const void* x, int x_dtype, int64_t T, int64_t H, int64_t int
     W4A8_REQUIRE(H % 8 == 0 && inter % 8 == 0, "moe_apply: sizes must be multiples of 8");
     W4A8_REQUIRE(!(weight_is_e2m1 && (w13_zeros || w2_zeros)),
                  "mxfp4 (E2M1) weights are symmetric; w_zeros must be empty");
-    W4A8_REQUIRE(!frag || (!weight_is_e2m1 && group_size == 128 && H % 128 == 0 &&
-                           inter % 128 == 0 && gemv_supported(H, group_size) &&
-                           gemv_supported(inter, group_size) &&
-                           prefill_supported(H, group_size, false) &&
-                           prefill_supported(inter, group_size, false)),
-                 "fragment-layout weights need int4 g128 with hidden and intermediate sizes "
-                 "the GEMV and the prefill tiles take");
+    if (n_global <= 0) n_global = E;
+    W4A8_REQUIRE(expert_map != nullptr || n_global == E,
+                 "moe_apply: global expert count differs from the local one; pass expert_map");
+    W4A8_REQUIRE(n_global <= (int64_t)1 << 20, "moe_apply: too many global experts");
+    const ApplyPlan pl = plan_apply(T, E, top_k);
+    W4A8_REQUIRE(!frag || (!weight_is_e2m1 && fragments_schedule_ok(pl.decode, H, inter, group_size)),
+                 "fragment-layout weights need int4 g128 with hidden and intermediate sizes the "
+                 "chosen schedule takes (decode GEMV: K/128 in {1,2,3,4,8,12,16,32}; prefill "
+                 "tiles: K <= 4096)");
     if (T == 0) return W4A8_OK;
     W4A8_REQUIRE(x && w13 && w13_scales_f16 && w2 && w2_scales_f16 && topk_weights && topk_ids && out,
                  "moe_apply: null pointer");
+    W4A8_REQUIRE(logits == nullptr || n_global <= 1024,
+                 "moe_forward: the router takes at most 1024 experts");
     hipStream_t s = as_stream(stream);
-    const ApplyPlan pl = plan_apply(T, E, top_k);
     Workspace w(workspace, workspace_bytes);
     int32_t *sti, *eid, *ntp; void* aws; size_t abytes; uint8_t* xq; float* s1; __half* h;
     uint8_t* hq; float* s2; float* acc; float* gs1; float* gs2; __half* y; int32_t* s2r;
@@ -237,22 +266,54 @@ int moe_apply_impl(const void* x, int x_dtype, int64_t T, int64_t H, int64_t int
     // many-token schedule: the routing waves also quantise x (one launch less)
     const bool route_quant = logits != nullptr && !(pl.decode && numel <= kAlignSmallMax);
     if (logits != nullptr)
-        if (int rc = launch_topk_softmax(logits, T, E, top_k, renormalize,
+        if (int rc = launch_topk_softmax(logits, T, n_global, top_k, renormalize,
                                          const_cast<float*>(topk_weights),
                                          const_cast<int32_t*>(topk_ids), s,
                                          route_quant ? x : nullptr, bf16, H, xq, s1,
                                          pf1 ? gs1 : nullptr))
             return rc;
     stage_mark(0, s);
+    if (frag && pl.decode && !e2m1 && decode_layer_supported(numel, E, H, inter, group_size)) {
+        // decode on fragment-layout weights: two GEMVs that group the slots by expert
+        // themselves (no align launch) and quantise their rows in registers (no act-quant
+        // launches), then the slot reduce
+        stage_mark(1, s);
+        stage_mark(2, s);
+        stage_mark(3, s);
+        DecodeLaunch d{};
+        d.topk_ids = topk_ids; d.expert_map = expert_map; d.emap_len = n_global;
+        d.numel = numel; d.top_k = top_k; d.E = E;
+        d.a = x; d.a_bf16 = bf16; d.silu = true;
+        d.w = w13; d.scales = w13_scales_f16; d.zeros = w13_zeros; d.out = h;
+        d.K = H; d.N = 2 * inter;
+        stamp_gemm(0);
+        int rc = launch_decode_gemv(d, s);
+        stamp_gemm(-1);
+        if (rc) return rc;
+        stage_mark(4, s);
+        stage_mark(5, s);
+        d.a = h; d.a_bf16 = false; d.silu = false;
+        d.w = w2; d.scales = w2_scales_f16; d.zeros = w2_zeros; d.out = acc;
+        d.K = inter; d.N = H;
+        stamp_gemm(1);
+        rc = launch_decode_gemv(d, s);
+        stamp_gemm(-1);
+        if (rc) return rc;
+        stage_mark(6, s);
+        rc = launch_slot_reduce(acc, topk_weights, topk_ids, expert_map, n_global, E, T, H, top_k,
+                                out, bf16, s);
+        stage_mark(7, s);
+        return rc;
+    }
     if (pl.decode && numel <= kAlignSmallMax) {
         // one launch: align in work-group 0, act-quant of x in the others
-        if (int rc = launch_align_quant(topk_ids, numel, E, pl.block_m, expert_map, sti, pl.P,
-                                        eid, ntp, s2r, x, bf16, T, H, xq, s1, nullptr, s))
+        if (int rc = launch_align_quant(topk_ids, numel, E, pl.block_m, expert_map, n_global, sti,
+                                        pl.P, eid, ntp, s2r, x, bf16, T, H, xq, s1, nullptr, s))
             return rc;
         stage_mark(1, s);
     } else {
-        if (int rc = launch_align(topk_ids, numel, E, pl.block_m, expert_map, sti, pl.P, eid,
-                                  ntp, aws, abytes, s, s2r))
+        if (int rc = launch_align(topk_ids, numel, E, pl.block_m, expert_map, n_global, sti, pl.P,
+                                  eid, ntp, aws, abytes, s, s2r))
             return rc;
         stage_mark(1, s);
         if (!route_quant)
@@ -273,12 +334,14 @@ int moe_apply_impl(const void* x, int x_dtype, int64_t T, int64_t H, int64_t int
     g1.act_group_sums = pf1 ? gs1 : nullptr;
     g1.w_frag = frag;
     int rc;
+    stamp_gemm(0);
     if (!mfma) rc = launch_grouped_scalar(g1, s);
     else if (pl.decode && !e2m1 && gemv_supported(H, group_size)) rc = launch_grouped_gemv(g1, s);
     else if (pf1 && prefill_ares_supported(H, 2 * inter, group_size, e2m1, pl.block_m, Epi::kSiluHalf))
         rc = launch_grouped_prefill_ares(g1, s);
     else if (pf1) rc = launch_grouped_prefill(g1, s);
     else rc = launch_grouped_mfma(g1, s);
+    stamp_gemm(-1);
     if (rc) return rc;
     stage_mark(4, s);
     // act-quant of h over real rows only, once per row (quantising inside the decode GEMV
@@ -304,17 +367,19 @@ int moe_apply_impl(const void* x, int x_dtype, int64_t T, int64_t H, int64_t int
     g2.act_scales = ares2_quant ? nullptr : s2;
     g2.act_group_sums = pf2 && !ares2_quant ? gs2 : nullptr;
     g2.w_frag = frag;
+    stamp_gemm(1);
     if (!mfma) rc = launch_grouped_scalar(g2, s);
     else if (gemv2) rc = launch_grouped_gemv(g2, s);
     else if (ares2) rc = launch_grouped_prefill_ares(g2, s);
     else if (pf2) rc = launch_grouped_prefill(g2, s);
     else rc = launch_grouped_mfma(g2, s);
+    stamp_gemm(-1);
     if (rc) return rc;
     stage_mark(6, s);
     // slots whose expert is not local / out of range contribute nothing
     if (pl.decode)
-        rc = launch_slot_reduce(acc, topk_weights, topk_ids, expert_map, E, T, H, top_k, out,
-                                bf16, s);
+        rc = launch_slot_reduce(acc, topk_weights, topk_ids, expert_map, n_global, E, T, H, top_k,
+                                out, bf16, s);
     else
         rc = launch_row_reduce(y, s2r, topk_weights, T, H, top_k, out, bf16, s);
     stage_mark(7, s);
@@ -324,7 +389,7 @@ int moe_apply_impl(const void* x, int x_dtype, int64_t T, int64_t H, int64_t int
 
 extern "C" {
 
-int w4a8_abi_version(void) { return 1; }
+int w4a8_abi_version(void) { return 2; }
 
 const char* w4a8_last_error(void) { return g_error.c_str(); }
 
@@ -383,9 +448,9 @@ int w4a8_moe_align_block_size(const int32_t* topk_ids, int64_t numel, int64_t nu
     W4A8_REQUIRE(sorted_token_ids && expert_ids && num_tokens_post_padded,
                  "moe_align: null output pointer");
     W4A8_REQUIRE(numel == 0 || topk_ids, "moe_align: null topk_ids");
-    return launch_align(topk_ids, numel, num_experts, block_m, expert_map, sorted_token_ids,
-                        sorted_len, expert_ids, num_tokens_post_padded, workspace,
-                        workspace_bytes, as_stream(stream));
+    return launch_align(topk_ids, numel, num_experts, block_m, expert_map, num_experts,
+                        sorted_token_ids, sorted_len, expert_ids, num_tokens_post_padded,
+                        workspace, workspace_bytes, as_stream(stream));
 }
 
 size_t w4a8_moe_gemm_workspace_size(int64_t x_rows, int64_t K) {
@@ -538,14 +603,18 @@ int w4a8_mmq_fp8_gemm(const void* x_f16, int64_t M, int64_t K, const int32_t* w_
 
 int w4a8_moe_apply_set_stage_events(void* const* events, int count) {
     clear_error();
-    if (count == 0) { g_stage_on = false; return W4A8_OK; }
-    W4A8_REQUIRE((count == kStageEvents || count == kStageEvents + 1) && events != nullptr,
-                 "stage events: need 8 events (or 9 with the calibration event)");
+    if (count == 0) {
+        g_stage_on = false;
+        next_kernel_stamp() = KernelStamp{};
+        return W4A8_OK;
+    }
+    W4A8_REQUIRE((count == kStageEvents || count == kStageEvents + kStampEvents) && events != nullptr,
+                 "stage events: need 8 events (or 12 with the GEMM kernel stamps)");
     for (int i = 0; i < count; ++i) {
         W4A8_REQUIRE(events[i] != nullptr, "stage events: null event");
         g_stage_events[i] = reinterpret_cast<hipEvent_t>(events[i]);
     }
-    g_stage_calib = count == kStageEvents + 1;
+    g_stage_stamps = count == kStageEvents + kStampEvents;
     g_stage_on = true;
     return W4A8_OK;
 }
@@ -566,13 +635,13 @@ int w4a8_moe_apply(const void* x, int x_dtype, int64_t T, int64_t H, int64_t int
                    const void* w13_scales_f16, const int32_t* w13_zeros, const int32_t* w2,
                    const void* w2_scales_f16, const int32_t* w2_zeros,
                    const float* topk_weights, const int32_t* topk_ids,
-                   const int32_t* expert_map, int weight_is_e2m1, void* out, void* workspace,
-                   size_t workspace_bytes, void* stream) {
+                   const int32_t* expert_map, int64_t num_global_experts, int weight_is_e2m1,
+                   void* out, void* workspace, size_t workspace_bytes, void* stream) {
     clear_error();
     return moe_apply_impl(x, x_dtype, T, H, inter, E, top_k, group_size, w13, w13_scales_f16,
                           w13_zeros, w2, w2_scales_f16, w2_zeros, topk_weights, topk_ids,
-                          expert_map, weight_is_e2m1, out, workspace, workspace_bytes, stream,
-                          false);
+                          expert_map, num_global_experts, weight_is_e2m1, out, workspace,
+                          workspace_bytes, stream, false);
 }
 
 int w4a8_moe_apply_fragments(const void* x, int x_dtype, int64_t T, int64_t H, int64_t inter,
@@ -580,13 +649,14 @@ int w4a8_moe_apply_fragments(const void* x, int x_dtype, int64_t T, int64_t H, i
                              const void* w13_scales_f16, const int32_t* w13_zeros,
                              const int32_t* w2_frag, const void* w2_scales_f16,
                              const int32_t* w2_zeros, const float* topk_weights,
-                             const int32_t* topk_ids, const int32_t* expert_map, void* out,
-                             void* workspace, size_t workspace_bytes, void* stream) {
+                             const int32_t* topk_ids, const int32_t* expert_map,
+                             int64_t num_global_experts, void* out, void* workspace,
+                             size_t workspace_bytes, void* stream) {
     clear_error();
     return moe_apply_impl(x, x_dtype, T, H, inter, E, top_k, group_size, w13_frag,
                           w13_scales_f16, w13_zeros, w2_frag, w2_scales_f16, w2_zeros,
-                          topk_weights, topk_ids, expert_map, 0, out, workspace, workspace_bytes,
-                          stream, true);
+                          topk_weights, topk_ids, expert_map, num_global_experts, 0, out,
+                          workspace, workspace_bytes, stream, true);
 }
 
 int w4a8_moe_forward(const void* x, int x_dtype, int64_t T, int64_t H, int64_t inter, int64_t E,
@@ -594,17 +664,22 @@ int w4a8_moe_forward(const void* x, int x_dtype, int64_t T, int64_t H, int64_t i
                      int renormalize, const int32_t* w13, const void* w13_scales_f16,
                      const int32_t* w13_zeros, const int32_t* w2, const void* w2_scales_f16,
                      const int32_t* w2_zeros, int weights_layout, const int32_t* expert_map,
-                     float* topk_weights, int32_t* topk_ids, void* out, void* workspace,
-                     size_t workspace_bytes, void* stream) {
+                     int64_t num_global_experts, float* topk_weights, int32_t* topk_ids,
+                     void* out, void* workspace, size_t workspace_bytes, void* stream) {
     clear_error();
     W4A8_REQUIRE(weights_layout == W4A8_WEIGHTS_OP || weights_layout == W4A8_WEIGHTS_FRAGMENTS,
                  "moe_forward: weights_layout must be W4A8_WEIGHTS_OP or W4A8_WEIGHTS_FRAGMENTS");
     W4A8_REQUIRE(T == 0 || (router_logits && topk_weights && topk_ids), "moe_forward: null pointer");
     return moe_apply_impl(x, x_dtype, T, H, inter, E, top_k, group_size, w13, w13_scales_f16,
                           w13_zeros, w2, w2_scales_f16, w2_zeros, topk_weights, topk_ids,
-                          expert_map, 0, out, workspace, workspace_bytes, stream,
-                          weights_layout == W4A8_WEIGHTS_FRAGMENTS, router_logits,
+                          expert_map, num_global_experts, 0, out, workspace, workspace_bytes,
+                          stream, weights_layout == W4A8_WEIGHTS_FRAGMENTS, router_logits,
                           renormalize != 0);
+}
+
+int w4a8_moe_fragments_supported(int64_t H, int64_t inter, int64_t group_size) {
+    return fragments_schedule_ok(true, H, inter, group_size) &&
+           fragments_schedule_ok(false, H, inter, group_size);
 }
 
 int w4a8_repack_int4_fragments(const int32_t* w_packed, int64_t E, int64_t N, int64_t K,

@@ -89,8 +89,8 @@ __global__ void gather_reduce_kernel(const __half* __restrict__ out2,
 template <bool BF16>
 __global__ void slot_reduce_kernel(const float* __restrict__ y, const float* __restrict__ tw,
                                    const int32_t* __restrict__ ids,
-                                   const int32_t* __restrict__ emap, int E, int64_t T, int N,
-                                   int top_k, void* __restrict__ out) {
+                                   const int32_t* __restrict__ emap, int emap_len, int E,
+                                   int64_t T, int N, int top_k, void* __restrict__ out) {
     const int64_t t = blockIdx.y;
     const int n = (blockIdx.x * blockDim.x + threadIdx.x) * 4;
     if (n >= N || t >= T) return;
@@ -98,7 +98,7 @@ __global__ void slot_reduce_kernel(const float* __restrict__ y, const float* __r
 #pragma unroll 8
     for (int j = 0; j < top_k; ++j) {
         int e = ids[t * top_k + j];
-        if (emap != nullptr) e = (e >= 0 && e < E) ? emap[e] : -1;
+        if (emap != nullptr) e = (e >= 0 && e < emap_len) ? emap[e] : -1;
         if (e < 0 || e >= E) continue;
         const float w = tw[t * top_k + j];
         const float4 v = *reinterpret_cast<const float4*>(y + (t * top_k + j) * N + n);
@@ -112,7 +112,7 @@ __global__ void slot_reduce_kernel(const float* __restrict__ y, const float* __r
         if constexpr (BF16)
             reinterpret_cast<__hip_bfloat16*>(out)[t * N + n + i] = __float2bfloat16(acc[i]);
         else
-            reinterpret_cast<__half*>(out)[t * N + n + i] = __float2half(acc[i]);
+            reinterpret_cast<__half*>(out)[t * N + n + i] = __float2half(as_f32(acc[i]));
     }
 }
 
@@ -166,8 +166,8 @@ __global__ void row_reduce_kernel(const __half* __restrict__ y, const int32_t* _
             const uint32_t hi = __bfloat16_as_ushort(__float2bfloat16(acc[2 * i + 1]));
             o[i] = lo | (hi << 16);
         } else {
-            const uint32_t lo = __half_as_ushort(__float2half(acc[2 * i]));
-            const uint32_t hi = __half_as_ushort(__float2half(acc[2 * i + 1]));
+            const uint32_t lo = __half_as_ushort(__float2half(as_f32(acc[2 * i])));
+            const uint32_t hi = __half_as_ushort(__float2half(as_f32(acc[2 * i + 1])));
             o[i] = lo | (hi << 16);
         }
     }
@@ -254,16 +254,16 @@ int launch_gather_reduce(const void* out2, int64_t P, int64_t N, const int32_t* 
 }
 
 int launch_slot_reduce(const float* y, const float* tw, const int32_t* ids,
-                       const int32_t* emap, int64_t E, int64_t T, int64_t N, int64_t top_k,
-                       void* out, bool out_bf16, hipStream_t stream) {
+                       const int32_t* emap, int64_t emap_len, int64_t E, int64_t T, int64_t N,
+                       int64_t top_k, void* out, bool out_bf16, hipStream_t stream) {
     if (T == 0 || N == 0) return W4A8_OK;
     dim3 grid(blocks_for(N / 4, 256), (unsigned)T);
     if (out_bf16)
-        slot_reduce_kernel<true><<<grid, 256, 0, stream>>>(y, tw, ids, emap, (int)E, T, (int)N,
-                                                          (int)top_k, out);
+        slot_reduce_kernel<true><<<grid, 256, 0, stream>>>(y, tw, ids, emap, (int)emap_len,
+                                                          (int)E, T, (int)N, (int)top_k, out);
     else
-        slot_reduce_kernel<false><<<grid, 256, 0, stream>>>(y, tw, ids, emap, (int)E, T, (int)N,
-                                                           (int)top_k, out);
+        slot_reduce_kernel<false><<<grid, 256, 0, stream>>>(y, tw, ids, emap, (int)emap_len,
+                                                           (int)E, T, (int)N, (int)top_k, out);
     return check_launch("slot_reduce_kernel");
 }
 

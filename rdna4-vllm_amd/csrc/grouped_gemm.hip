@@ -29,11 +29,11 @@ __device__ __forceinline__ void store_out(const Params& p, int64_t row_pad, int 
                                           int col, float run_a, float run_b) {
     const float a = p.asc[src];
     if constexpr (EPI == Epi::kHalf) {
-        reinterpret_cast<__half*>(p.out)[row_pad * p.N + col] = __float2half(run_a * a);
+        reinterpret_cast<__half*>(p.out)[row_pad * p.N + col] = __float2half(as_f32(run_a * a));
     } else if constexpr (EPI == Epi::kSiluHalf) {
         const int inter = p.N / 2;
         reinterpret_cast<__half*>(p.out)[row_pad * inter + col] =
-            silu_mul_h(__float2half(run_a * a), __float2half(run_b * a));
+            silu_mul_h(__float2half(as_f32(run_a * a)), __float2half(as_f32(run_b * a)));
     } else if constexpr (EPI == Epi::kScatter) {
         const int64_t tok = slot / p.out_top_k;
         atomicAdd(reinterpret_cast<float*>(p.out) + tok * p.N + col, p.tw[slot] * run_a * a);
@@ -665,10 +665,10 @@ __global__ void __launch_bounds__(256, 2) grouped_gemv_kernel(Params p, int tpt)
             const int oslot = s_oslot[wave][mi];
             const float a = s_oasc[wave][mi];
             if constexpr (EPI == Epi::kHalf) {
-                reinterpret_cast<__half*>(p.out)[opad * p.N + col] = __float2half(ra * a);
+                reinterpret_cast<__half*>(p.out)[opad * p.N + col] = __float2half(as_f32(ra * a));
             } else if constexpr (EPI == Epi::kSiluHalf) {
                 reinterpret_cast<__half*>(p.out)[opad * ncols + col] =
-                    silu_mul_h(__float2half(ra * a), __float2half(rb * a));
+                    silu_mul_h(__float2half(as_f32(ra * a)), __float2half(as_f32(rb * a)));
             } else if constexpr (EPI == Epi::kScatter) {
                 atomicAdd(reinterpret_cast<float*>(p.out) + (int64_t)(oslot / p.out_top_k) * p.N + col,
                           p.tw[oslot] * ra * a);
@@ -836,6 +836,7 @@ GemvSplit gemv_split(int G) {
         case 8: return {4, 2};
         case 12: return {3, 4};
         case 16: return {4, 4};
+        case 32: return {8, 4};
         default: return {0, 0};
     }
 }
@@ -865,7 +866,7 @@ int launch_gemv_a(const Params& p, int tpt, dim3 grid, size_t lds, hipStream_t s
         }
         attr_set = true;
     }
-    grouped_gemv_kernel<EPI, GPW, KSPLIT, AQ, FRAG><<<grid, 256, lds, s>>>(p, tpt);
+    launch_kernel(&grouped_gemv_kernel<EPI, GPW, KSPLIT, AQ, FRAG>, grid, dim3(256), lds, s, p, tpt);
     return check_launch("grouped_gemv_kernel");
 }
 
@@ -902,6 +903,7 @@ int launch_gemv_e(const Params& p, int tpt, hipStream_t s) {
         case 4 * 8 + 2: return launch_gemv_t<EPI, 4, 2>(p, tpt, s);
         case 3 * 8 + 4: return launch_gemv_t<EPI, 3, 4>(p, tpt, s);
         case 4 * 8 + 4: return launch_gemv_t<EPI, 4, 4>(p, tpt, s);
+        case 8 * 8 + 4: return launch_gemv_t<EPI, 8, 4>(p, tpt, s);
     }
     set_error("gemv grouped GEMM: unsupported number of K groups");
     return W4A8_ERR_INVALID;
@@ -957,7 +959,7 @@ int launch_grouped_gemv_tpt(const GroupedArgs& a, int tpt, hipStream_t s) {
         return W4A8_ERR_INVALID;
     }
     if (!gemv_supported(a.K, a.group_size)) {
-        set_error("gemv grouped GEMM: K / group_size must be one of 1,2,3,4,8,12,16");
+        set_error("gemv grouped GEMM: K / group_size must be one of 1,2,3,4,8,12,16,32");
         return W4A8_ERR_INVALID;
     }
     if (a.e2m1) {

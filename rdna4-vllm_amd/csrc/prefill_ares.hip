@@ -26,7 +26,8 @@
 //     weight rows, so no work-group barrier follows the prologue;
 //   * after the last group of a range the zero-point term sum_g sum_k a * z * s is formed by
 //     bf16 MFMAs over (row group sums) x (s*z), out = asc * (512 * run - term) is stored as
-//     8-byte row pieces (fp16, or fp16 SiLU(gate) * up) and the accumulators restart;
+//     8-byte row pieces (fp16, or fp16 SiLU(gate) * up, bit-identical to silu_and_mul) and
+//     the accumulators restart;
 //   * the two waves of a SIMD take turns at the higher issue priority, one range each, so
 //     neither ends a tile far behind the other;
 //   * the main loop is instantiated per live 16-row fragment count (1..4), so partial tiles
@@ -91,13 +92,11 @@ __device__ __forceinline__ int ar_row(int r, int w, int j, int c, int ncols) {
     return ar_col<kSilu>(r, w, j, c) + (kSilu && j == 1 ? ncols : 0);
 }
 
-// SiLU(gate) * up on the fp16 gate/up values (moe_kernel.hip:555-561), with the hardware
-// exp2 and reciprocal (1 ulp each) in place of the correctly rounded expf and division.
-__device__ __forceinline__ __half silu_mul_fast(float gate, float up) {
-    const float g = __half2float(__float2half(gate));
-    const float e = __builtin_amdgcn_exp2f(g * -1.44269504088896341f);
-    const __half silu_h = __float2half(g * __builtin_amdgcn_rcpf(1.0f + e));
-    return __hmul(silu_h, __float2half(up));
+// SiLU(gate) * up on the fp16 gate/up values: the same silu_mul_h (expf and an IEEE
+// division, moe_kernel.hip:555-561) as silu_and_mul_kernel, so the fused epilogue is
+// bit-identical to gemm1 followed by silu_and_mul.
+__device__ __forceinline__ __half silu_mul_tile(float gate, float up) {
+    return silu_mul_h(__float2half(gate), __float2half(up));
 }
 
 using bf16x8 = __bf16 __attribute__((ext_vector_type(8)));
@@ -470,14 +469,14 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
                 float va[4], vb[4];
 #pragma unroll
                 for (int rr = 0; rr < 4; ++rr) {
-                    va[rr] = av * (kNibbleScale * run[i][0][rr] - za[rr]);
-                    vb[rr] = av * (kNibbleScale * run[i][1][rr] - zb[rr]);
+                    va[rr] = as_f32(av * (kNibbleScale * run[i][0][rr] - za[rr]));
+                    vb[rr] = as_f32(av * (kNibbleScale * run[i][1][rr] - zb[rr]));
                 }
                 __half* rowp = outp + (row0 + m) * ldo;
                 const bool live = (vmask >> m) & 1;
                 if constexpr (kSilu) {
-                    const __half2 h01 = __halves2half2(silu_mul_fast(va[0], vb[0]), silu_mul_fast(va[1], vb[1]));
-                    const __half2 h23 = __halves2half2(silu_mul_fast(va[2], vb[2]), silu_mul_fast(va[3], vb[3]));
+                    const __half2 h01 = __halves2half2(silu_mul_tile(va[0], vb[0]), silu_mul_tile(va[1], vb[1]));
+                    const __half2 h23 = __halves2half2(silu_mul_tile(va[2], vb[2]), silu_mul_tile(va[3], vb[3]));
                     if (live)
                         *reinterpret_cast<uint2*>(rowp) = make_uint2(__builtin_bit_cast(uint32_t, h01),
                                                                      __builtin_bit_cast(uint32_t, h23));
@@ -560,7 +559,7 @@ int launch_ares_t(const Params& p, hipStream_t s) {
     // a multiple of 8 work-groups covers every tile under the XCD-aware order
     const int64_t tiles = (p.P + kArBM - 1) / kArBM;
     const unsigned grid = (unsigned)((tiles + kArXcds - 1) / kArXcds * kArXcds);
-    prefill_ares_kernel<EPI, FRAG><<<grid, kArThreads, lds, s>>>(p);
+    launch_kernel(&prefill_ares_kernel<EPI, FRAG>, dim3(grid), dim3(kArThreads), lds, s, p);
     return check_launch("prefill_ares_kernel");
 }
 

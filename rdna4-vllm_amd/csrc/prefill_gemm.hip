@@ -355,8 +355,8 @@ __global__ void __launch_bounds__(256, 1) prefill_mfma_kernel(Params p, int nblo
                 const int src = s_src[m];
                 if (src < 0) continue;
                 const float a = p.asc[src];
-                const float va = a * (kNibbleScale * run[i][ja][r] - za[r]);
-                const float vb = a * (kNibbleScale * run[i][jb][r] - zb[r]);
+                const float va = as_f32(a * (kNibbleScale * run[i][ja][r] - za[r]));
+                const float vb = as_f32(a * (kNibbleScale * run[i][jb][r] - zb[r]));
                 if constexpr (kSilu) {
                     if (ocol[ja] < ncols) store(m, ocol[ja], va, vb);
                 } else {
@@ -387,7 +387,8 @@ int launch_prefill_t(const Params& p, hipStream_t s) {
         }
         attr_set = true;
     }
-    prefill_mfma_kernel<EPI, MT, FRAG><<<(unsigned)grid, 256, L.total, s>>>(p, nblocks, ntiles);
+    launch_kernel(&prefill_mfma_kernel<EPI, MT, FRAG>, dim3((unsigned)grid), dim3(256),
+                  (size_t)L.total, s, p, nblocks, ntiles);
     return check_launch("prefill_mfma_kernel");
 }
 

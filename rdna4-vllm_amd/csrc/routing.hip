@@ -31,10 +31,12 @@ struct ChunkScratch {
     int warp_tot[kAlignThreads / 64];
 };
 
+// Expert of slot i: with an expert map (emap_len entries, indexed by the routed global id)
+// the id is mapped to a local expert first; -1 when the slot has no local expert in [0, E).
 __device__ __forceinline__ int map_expert(const int32_t* __restrict__ ids, int64_t i,
-                                          const int32_t* __restrict__ emap, int E) {
+                                          const int32_t* __restrict__ emap, int emap_len, int E) {
     int e = ids[i];
-    if (emap != nullptr) e = (e >= 0 && e < E) ? emap[e] : -1;
+    if (emap != nullptr) e = (e >= 0 && e < emap_len) ? emap[e] : -1;
     return (e >= 0 && e < E) ? e : -1;
 }
 
@@ -79,11 +81,11 @@ __device__ __forceinline__ uint64_t same_expert_lanes(int e, int nbits) {
 // Phase A for one chunk: histogram (s.hist) and the stable rank of this thread's slot among
 // the chunk's slots of its expert. Returns the expert (or -1) of slot `base + threadIdx.x`.
 __device__ int chunk_rank(const int32_t* __restrict__ ids, int64_t numel, int64_t base,
-                          const int32_t* __restrict__ emap, int E, ChunkScratch& s,
+                          const int32_t* __restrict__ emap, int emap_len, int E, ChunkScratch& s,
                           int& rank) {
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int64_t i = base + tid;
-    const int e = (i < numel) ? map_expert(ids, i, emap, E) : -1;
+    const int e = (i < numel) ? map_expert(ids, i, emap, emap_len, E) : -1;
     int* z = reinterpret_cast<int*>(&s.wpre[0][0]);
     for (int k = tid; k < (kAlignThreads / 64) * kMaxExperts / 2; k += kAlignThreads) z[k] = 0;
     __syncthreads();
@@ -137,13 +139,13 @@ __device__ void write_layout(const int* cnt, const int* eoff, int E, int64_t blo
 // Whole align for numel <= kChunk inside one work-group of kAlignThreads threads.
 __device__ __forceinline__ void align_small_body(
     const int32_t* __restrict__ ids, int64_t numel, int E, int64_t block_m,
-    const int32_t* __restrict__ emap, int32_t* __restrict__ sorted_ids, int64_t sorted_len,
-    int32_t* __restrict__ expert_ids, int32_t* __restrict__ ntp,
+    const int32_t* __restrict__ emap, int emap_len, int32_t* __restrict__ sorted_ids,
+    int64_t sorted_len, int32_t* __restrict__ expert_ids, int32_t* __restrict__ ntp,
     int32_t* __restrict__ slot_to_row) {
     __shared__ ChunkScratch s;
     __shared__ int eoff[kMaxExperts];
     int rank;
-    const int e = chunk_rank(ids, numel, 0, emap, E, s, rank);
+    const int e = chunk_rank(ids, numel, 0, emap, emap_len, E, s, rank);
     const int tid = threadIdx.x;
     int total;
     const int padded = (tid < E) ? (int)((s.hist[tid] + block_m - 1) / block_m * block_m) : 0;
@@ -158,11 +160,11 @@ __device__ __forceinline__ void align_small_body(
 
 __global__ void __launch_bounds__(kAlignThreads) align_small_kernel(
     const int32_t* __restrict__ ids, int64_t numel, int E, int64_t block_m,
-    const int32_t* __restrict__ emap, int32_t* __restrict__ sorted_ids, int64_t sorted_len,
-    int32_t* __restrict__ expert_ids, int32_t* __restrict__ ntp,
+    const int32_t* __restrict__ emap, int emap_len, int32_t* __restrict__ sorted_ids,
+    int64_t sorted_len, int32_t* __restrict__ expert_ids, int32_t* __restrict__ ntp,
     int32_t* __restrict__ slot_to_row) {
-    align_small_body(ids, numel, E, block_m, emap, sorted_ids, sorted_len, expert_ids, ntp,
-                     slot_to_row);
+    align_small_body(ids, numel, E, block_m, emap, emap_len, sorted_ids, sorted_len, expert_ids,
+                     ntp, slot_to_row);
 }
 
 // Multi-chunk phase 1: per-chunk histograms -> counts[chunk][E], and every slot's expert
@@ -170,11 +172,11 @@ __global__ void __launch_bounds__(kAlignThreads) align_small_kernel(
 __device__ __forceinline__ int slot_key_pack(int e, int rank) { return e >= 0 ? (rank << 10) | e : -1; }
 __global__ void __launch_bounds__(kAlignThreads) align_count_kernel(
     const int32_t* __restrict__ ids, int64_t numel, int E, const int32_t* __restrict__ emap,
-    int32_t* __restrict__ counts, int32_t* __restrict__ slot_key) {
+    int emap_len, int32_t* __restrict__ counts, int32_t* __restrict__ slot_key) {
     __shared__ ChunkScratch s;
     int rank;
     const int64_t base = (int64_t)blockIdx.x * kChunk;
-    const int e = chunk_rank(ids, numel, base, emap, E, s, rank);
+    const int e = chunk_rank(ids, numel, base, emap, emap_len, E, s, rank);
     if (base + threadIdx.x < numel) slot_key[base + threadIdx.x] = slot_key_pack(e, rank);
     for (int x = threadIdx.x; x < E; x += kAlignThreads) counts[(int64_t)blockIdx.x * E + x] = s.hist[x];
 }
@@ -425,8 +427,8 @@ __global__ void __launch_bounds__(256) topk_softmax_kernel(
 template <bool BF16>
 __global__ void __launch_bounds__(kAlignThreads) align_quant_kernel(
     const int32_t* __restrict__ ids, int64_t numel, int E, int64_t block_m,
-    const int32_t* __restrict__ emap, int32_t* __restrict__ sorted_ids, int64_t sorted_len,
-    int32_t* __restrict__ expert_ids, int32_t* __restrict__ ntp,
+    const int32_t* __restrict__ emap, int emap_len, int32_t* __restrict__ sorted_ids,
+    int64_t sorted_len, int32_t* __restrict__ expert_ids, int32_t* __restrict__ ntp,
     int32_t* __restrict__ slot_to_row, const void* __restrict__ x, int64_t rows, int K,
     uint8_t* __restrict__ xq, float* __restrict__ xs, float* __restrict__ gsum) {
     if (blockIdx.x > 0) {
@@ -434,8 +436,8 @@ __global__ void __launch_bounds__(kAlignThreads) align_quant_kernel(
         if (row < rows) quantize_row<BF16>(x, row, K, xq, xs, true, gsum, threadIdx.x & 63);
         return;
     }
-    align_small_body(ids, numel, E, block_m, emap, sorted_ids, sorted_len, expert_ids, ntp,
-                     slot_to_row);
+    align_small_body(ids, numel, E, block_m, emap, emap_len, sorted_ids, sorted_len, expert_ids,
+                     ntp, slot_to_row);
 }
 
 
@@ -452,7 +454,7 @@ size_t align_workspace_bytes(int64_t numel, int64_t num_experts) {
 }
 
 int launch_align(const int32_t* ids, int64_t numel, int64_t E, int64_t block_m,
-                 const int32_t* emap, int32_t* sorted_ids, int64_t sorted_len,
+                 const int32_t* emap, int64_t emap_len, int32_t* sorted_ids, int64_t sorted_len,
                  int32_t* expert_ids, int32_t* ntp, void* ws, size_t ws_bytes,
                  hipStream_t stream, int32_t* slot_to_row) {
     if (E > kMaxExperts) {
@@ -461,8 +463,8 @@ int launch_align(const int32_t* ids, int64_t numel, int64_t E, int64_t block_m,
     }
     if (numel <= kChunk) {
         align_small_kernel<<<1, kAlignThreads, 0, stream>>>(ids, numel, (int)E, block_m, emap,
-                                                           sorted_ids, sorted_len, expert_ids,
-                                                           ntp, slot_to_row);
+                                                           (int)emap_len, sorted_ids, sorted_len,
+                                                           expert_ids, ntp, slot_to_row);
         return check_launch("align_small_kernel");
     }
     const int64_t nchunks = (numel + kChunk - 1) / kChunk;
@@ -475,7 +477,8 @@ int launch_align(const int32_t* ids, int64_t numel, int64_t E, int64_t block_m,
         return W4A8_ERR_WORKSPACE;
     }
     align_count_kernel<<<(unsigned)nchunks, kAlignThreads, 0, stream>>>(ids, numel, (int)E, emap,
-                                                                        counts, slot_key);
+                                                                        (int)emap_len, counts,
+                                                                        slot_key);
     if (int rc = check_launch("align_count_kernel")) return rc;
     if (nchunks * E <= kScanPlaceMaxCounts) {
         align_scan_place_kernel<<<(unsigned)nchunks, kAlignThreads, 0, stream>>>(
@@ -520,7 +523,8 @@ int launch_topk_softmax(const float* logits, int64_t T, int64_t E, int64_t top_k
 
 
 int launch_align_quant(const int32_t* ids, int64_t numel, int64_t E, int64_t block_m,
-                       const int32_t* emap, int32_t* sorted_ids, int64_t sorted_len,
+                       const int32_t* emap, int64_t emap_len, int32_t* sorted_ids,
+                       int64_t sorted_len,
                        int32_t* expert_ids, int32_t* ntp, int32_t* slot_to_row,
                        const void* x, bool x_bf16, int64_t rows, int64_t K, uint8_t* xq,
                        float* xs, float* gsum, hipStream_t stream) {
@@ -531,12 +535,12 @@ int launch_align_quant(const int32_t* ids, int64_t numel, int64_t E, int64_t blo
     const unsigned grid = 1u + (unsigned)((rows + kAlignThreads / 64 - 1) / (kAlignThreads / 64));
     if (x_bf16)
         align_quant_kernel<true><<<grid, kAlignThreads, 0, stream>>>(
-            ids, numel, (int)E, block_m, emap, sorted_ids, sorted_len, expert_ids, ntp,
-            slot_to_row, x, rows, (int)K, xq, xs, gsum);
+            ids, numel, (int)E, block_m, emap, (int)emap_len, sorted_ids, sorted_len, expert_ids,
+            ntp, slot_to_row, x, rows, (int)K, xq, xs, gsum);
     else
         align_quant_kernel<false><<<grid, kAlignThreads, 0, stream>>>(
-            ids, numel, (int)E, block_m, emap, sorted_ids, sorted_len, expert_ids, ntp,
-            slot_to_row, x, rows, (int)K, xq, xs, gsum);
+            ids, numel, (int)E, block_m, emap, (int)emap_len, sorted_ids, sorted_len, expert_ids,
+            ntp, slot_to_row, x, rows, (int)K, xq, xs, gsum);
     return check_launch("align_quant_kernel");
 }
 

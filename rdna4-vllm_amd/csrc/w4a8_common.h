@@ -206,6 +206,16 @@ __device__ __forceinline__ float act_scale_from_absmax(float amax) {
     return s;
 }
 
+// x as an fp32 value in a register. Conversions to fp16 go through it: without it the
+// compiler may fold the product that forms x into the conversion (one f16-output FMA,
+// v_fma_mixlo_f16) and round once, where the numerics contract rounds the fp32 product and
+// then to fp16; the fused and unfused epilogues of one GEMM would then differ in rare
+// elements. The empty asm only pins the value; it emits no instruction.
+__device__ __forceinline__ float as_f32(float x) {
+    asm("" : "+v"(x));
+    return x;
+}
+
 // vLLM silu_and_mul on fp16 gate/up stores (moe_kernel.hip:555-561).
 __device__ __forceinline__ __half silu_mul_h(__half gate_h, __half up_h) {
     const float g = __half2float(gate_h);

@@ -2,6 +2,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <cstdint>
 #include <cstddef>
 #include <string>
@@ -18,6 +19,29 @@ void clear_error();
 int check_launch(const char* what);
 
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// Kernel-exact timing (measurement aid): when set, the next launch made through
+// launch_kernel() on this thread records `start` when that kernel begins and `stop` when it
+// ends (hipExtLaunchKernel stamps the events from the dispatch itself, so the interval is
+// the kernel's own duration, as a kernel trace reports it); the slot is then cleared.
+struct KernelStamp {
+    hipEvent_t start = nullptr;
+    hipEvent_t stop = nullptr;
+};
+KernelStamp& next_kernel_stamp();
+
+template <typename... Params, typename... Args>
+inline void launch_kernel(void (*kernel)(Params...), dim3 grid, dim3 block, size_t lds,
+                          hipStream_t s, Args... args) {
+    KernelStamp& st = next_kernel_stamp();
+    if (st.start != nullptr) {
+        hipExtLaunchKernelGGL(kernel, grid, block, (uint32_t)lds, s, st.start, st.stop, 0u,
+                              static_cast<Params>(args)...);
+        st = KernelStamp{};
+    } else {
+        kernel<<<grid, block, lds, s>>>(static_cast<Params>(args)...);
+    }
+}
 
 // Bump allocator over a caller workspace (256-byte aligned carve-outs).
 struct Workspace {
@@ -60,23 +84,27 @@ int launch_topk_softmax(const float* logits, int64_t T, int64_t E, int64_t top_k
 size_t align_workspace_bytes(int64_t numel, int64_t num_experts);
 // Decode prologue in one launch (numel <= 1024): the single-work-group align plus per-row
 // act-quant of x (k8-interleaved) with optional group sums.
+// emap (emap_len entries) maps routed ids to local experts in [0, E); slots without a
+// local expert are dropped.
 int launch_align_quant(const int32_t* ids, int64_t numel, int64_t E, int64_t block_m,
-                       const int32_t* emap, int32_t* sorted_ids, int64_t sorted_len,
+                       const int32_t* emap, int64_t emap_len, int32_t* sorted_ids,
+                       int64_t sorted_len,
                        int32_t* expert_ids, int32_t* ntp, int32_t* slot_to_row,
                        const void* x, bool x_bf16, int64_t rows, int64_t K, uint8_t* xq,
                        float* xs, float* gsum, hipStream_t stream);
 int launch_align(const int32_t* topk_ids, int64_t numel, int64_t E, int64_t block_m,
-                 const int32_t* expert_map, int32_t* sorted_ids, int64_t sorted_len,
+                 const int32_t* expert_map, int64_t emap_len, int32_t* sorted_ids,
+                 int64_t sorted_len,
                  int32_t* expert_ids, int32_t* ntp, void* ws, size_t ws_bytes,
                  hipStream_t stream, int32_t* slot_to_row = nullptr);   // optional inverse map
 int launch_gather_reduce(const void* out2, int64_t P, int64_t N, const int32_t* sorted_ids,
                          const float* tw, int64_t m_tk, const int32_t* ntp, int64_t top_k,
                          float* out, int32_t* slot_to_row, hipStream_t stream);
 // out[t, n] = cast(sum_{j asc} w[t*k+j] * y[(t*k+j), n]) with y fp32 (rows = T*k);
-// slots whose (mapped) expert is outside [0, E) are skipped.
+// slots whose (mapped) expert is outside [0, E) are skipped (map as launch_align_quant).
 int launch_slot_reduce(const float* y, const float* tw, const int32_t* topk_ids,
-                       const int32_t* expert_map, int64_t E, int64_t T, int64_t N,
-                       int64_t top_k, void* out, bool out_bf16, hipStream_t stream);
+                       const int32_t* expert_map, int64_t emap_len, int64_t E, int64_t T,
+                       int64_t N, int64_t top_k, void* out, bool out_bf16, hipStream_t stream);
 int launch_cast_f32(const float* in, int64_t n, void* out, bool out_bf16, hipStream_t stream);
 // out[t, n] = cast(sum_{j asc} w[t*k+j] * f32(y[slot_to_row[t*k+j], n])), y fp16 (rows, N);
 // rows < 0 (slots dropped by expert_map) contribute nothing. N % 8 == 0.
@@ -142,7 +170,27 @@ bool prefill_supported(int64_t K, int64_t group_size, bool e2m1);   // g128, K <
 // Same, with an explicit column-tile count per wave team (0 = default heuristic).
 int launch_grouped_gemv_tpt(const GroupedArgs& a, int tiles_per_team, hipStream_t stream);
 bool mfma_supported(int64_t K, int64_t group_size);
-// mfma_supported and K / group_size in {1,2,3,4,8,12,16} (split-K table of the GEMV)
+// mfma_supported and K / group_size in {1,2,3,4,8,12,16,32} (split-K table of the GEMV)
 bool gemv_supported(int64_t K, int64_t group_size);
+
+// Whole-layer decode GEMV on fragment-layout weights (decode_gemv.hip): each work-group
+// groups the slots by expert from topk_ids itself and quantises its activation rows in
+// registers. silu: gemm1 (a = x (T, K) by token, out = h (numel, N/2) fp16 after SiLU*mul);
+// else gemm2 (a = h (numel, K) fp16 by slot, out = y (numel, N) fp32).
+struct DecodeLaunch {
+    const int32_t* topk_ids;
+    const int32_t* expert_map;
+    int64_t emap_len, numel, top_k, E;
+    const void* a;
+    bool a_bf16;
+    bool silu;
+    const int32_t* w;
+    const void* scales;
+    const int32_t* zeros;
+    void* out;
+    int64_t K, N;
+};
+bool decode_layer_supported(int64_t numel, int64_t E, int64_t H, int64_t inter, int64_t gs);
+int launch_decode_gemv(const DecodeLaunch& d, hipStream_t stream);
 
 }  // namespace w4a8

@@ -16,6 +16,7 @@ from . import _ops  # noqa: F401  registers torch.ops.w4a8_fp8_wmma.*
 from ._ops import (  # noqa: F401
     act_quant_fp8,
     dequant_fp8,
+    fragments_supported,
     fused_topk,
     moe_align_block_size,
     moe_apply,
@@ -117,6 +118,7 @@ def mmq_fp8_moe_gather_reduce(out2, sorted_token_ids, topk_weights, num_tokens_p
 
 __all__ = [
     "mmq_fp8_gemm", "mmq_fp8_moe_gemm", "mmq_fp8_moe_gemm1_silu", "mmq_fp8_moe_gemm_scatter",
-    "mmq_fp8_moe_gather_reduce", "act_quant_fp8", "dequant_fp8", "fused_topk",
+    "mmq_fp8_moe_gather_reduce", "act_quant_fp8", "dequant_fp8", "fragments_supported",
+    "fused_topk",
     "moe_align_block_size", "moe_apply", "moe_forward", "repack_fragments", "silu_and_mul",
 ]

@@ -53,20 +53,21 @@ SIGNATURES = {
     "w4a8_moe_apply_set_stage_events": (_int, [ctypes.POINTER(_c_void_p), _int]),
     "w4a8_moe_apply": (_int, [_c_void_p, _int, _i64, _i64, _i64, _i64, _i64, _i64, _c_void_p,
                               _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
-                              _c_void_p, _c_void_p, _int, _c_void_p, _c_void_p, _size,
+                              _c_void_p, _c_void_p, _i64, _int, _c_void_p, _c_void_p, _size,
                               _c_void_p]),
     "w4a8_repack_int4_fragments": (_int, [_c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p]),
     "w4a8_moe_forward": (_int, [_c_void_p, _int, _i64, _i64, _i64, _i64, _i64, _i64, _c_void_p,
                                 _int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
-                                _c_void_p, _int, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
-                                _c_void_p, _size, _c_void_p]),
+                                _c_void_p, _int, _c_void_p, _i64, _c_void_p, _c_void_p,
+                                _c_void_p, _c_void_p, _size, _c_void_p]),
     "w4a8_moe_apply_fragments": (_int, [_c_void_p, _int, _i64, _i64, _i64, _i64, _i64, _i64,
                                         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
-                                        _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
-                                        _c_void_p, _size, _c_void_p]),
+                                        _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64,
+                                        _c_void_p, _c_void_p, _size, _c_void_p]),
+    "w4a8_moe_fragments_supported": (_int, [_i64, _i64, _i64]),
 }
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 
 class W4A8LibraryError(RuntimeError):

@@ -362,79 +362,132 @@ def repack_fragments(w_packed: torch.Tensor) -> torch.Tensor:
     return out
 
 
-def _layer_args(x, w13, w2, w13_s, w2_s, w13_z, w2_z, top_k, weight_is_e2m1):
-    """Shared validation of the whole-layer entry points; returns the size and pointer pack."""
-    _check(x.is_cuda and x.dtype in (torch.float16, torch.bfloat16) and x.dim() == 2,
-           "x must be CUDA fp16/bf16 (T, H)")
+def _zeros_of(z, E, N, G, name):
+    """Optional packed zero-points (E, N/8, G) int32 of one weight, or None."""
+    if z is None or z.numel() == 0:
+        return None
+    _check(z.dtype == torch.int32, f"{name} must be int32 (packed)")
+    _check(N % 8 == 0 and tuple(z.shape) == (E, N // 8, G),
+           f"{name} must be (E, N/8, K/group)=({E},{N // 8},{G}); got {tuple(z.shape)}")
+    return z.contiguous()
+
+
+def _layer_args(x, w13, w2, w13_s, w2_s, w13_z, w2_z, topk_weights, topk_ids, expert_map,
+                global_num_experts, weight_is_e2m1):
+    """Validation shared by the whole-layer entry points (the checks bindings.cpp:191-221 and
+    _check_moe_common make for the grouped ops, applied to both GEMMs of the layer), so a
+    mismatched tensor raises here instead of becoming an out-of-bounds read on the device.
+    Shapes are checked before devices. Returns the sizes, the zero-point tensors, the expert
+    map and the workspace."""
+    _check(x.dtype in (torch.float16, torch.bfloat16) and x.dim() == 2,
+           "x must be fp16/bf16 (T, H)")
     T, H = x.shape
     frag = w13.dim() == 5
     _check(w2.dim() == w13.dim(), "w13 and w2 must share a layout")
     if frag:
-        E, nt13, g13, _, _ = w13.shape
-        inter = nt13 * 16 // 2
-        _check(g13 * 128 == H, "w13 fragments must cover K = H")
-        _check(w2.shape[:3] == (E, H // 16, inter // 128), "w2 fragments must be (E, H/16, I/128, 64, 4)")
+        _check(tuple(w13.shape[3:]) == (64, 4) and tuple(w2.shape[3:]) == (64, 4),
+               "fragment-layout weights must be (E, N/16, K/128, 64, 4)")
+        E, nt13, g13 = w13.shape[:3]
+        _check(nt13 % 2 == 0, "w13 fragments must hold 2*inter rows")
+        inter = nt13 * 8
+        _check(g13 * 128 == H, f"w13 fragments must cover K = H = {H}")
+        _check(tuple(w2.shape[:3]) == (E, H // 16, inter // 128),
+               f"w2 fragments must be (E, H/16, inter/128, 64, 4)=({E},{H // 16},{inter // 128},64,4)")
         _check(not weight_is_e2m1, "fragment layout holds int4 weights only")
     else:
-        E, I2, _ = w13.shape
+        _check(w13.dim() == 3, "w13 must be (E, 2*inter, H/8) int32")
+        E, I2, kw = w13.shape
+        _check(kw * 8 == H and I2 % 2 == 0, f"w13 must be (E, 2*inter, H/8) with H={H}")
         inter = I2 // 2
-        _check(w2.shape == (E, H, inter // 8), f"w2 must be (E, H, inter/8)=({E},{H},{inter // 8})")
-    gs = H // w13_s.shape[2]
+        _check(tuple(w2.shape) == (E, H, inter // 8),
+               f"w2 must be (E, H, inter/8)=({E},{H},{inter // 8})")
     _check(w13.dtype == torch.int32 and w2.dtype == torch.int32, "weights must be int32")
     _check(w13_s.dtype == torch.float16 and w2_s.dtype == torch.float16, "scales must be fp16")
-    _check(inter // w2_s.shape[2] == gs, "w13 and w2 must share the group size")
+    _check(w13_s.dim() == 3 and tuple(w13_s.shape[:2]) == (E, 2 * inter) and w13_s.shape[2] > 0
+           and H % w13_s.shape[2] == 0, f"w13 scales must be (E, 2*inter, H/group)")
+    gs = H // w13_s.shape[2]
+    _check(inter % gs == 0 and tuple(w2_s.shape) == (E, H, inter // gs),
+           f"w2 scales must be (E, H, inter/group)=({E},{H},{inter // gs})")
     for t in (w13, w2, w13_s, w2_s):
-        _check(t.is_cuda and t.is_contiguous(), "weights/scales must be contiguous CUDA")
-    z13 = None if w13_z is None or w13_z.numel() == 0 else w13_z.contiguous()
-    z2 = None if w2_z is None or w2_z.numel() == 0 else w2_z.contiguous()
+        _check(t.is_contiguous(), "weights/scales must be contiguous")
+    z13 = _zeros_of(w13_z, E, 2 * inter, H // gs, "w13 zeros")
+    z2 = _zeros_of(w2_z, E, H, inter // gs, "w2 zeros")
+    _check(topk_ids.dim() == 2 and topk_ids.shape[0] == T, f"topk_ids must be (T, top_k) with T={T}")
+    top_k = topk_ids.shape[1]
+    _check(topk_weights.numel() == T * top_k, f"topk_weights must have T*top_k={T * top_k} entries")
+    emap = None
+    if expert_map is not None:
+        _check(expert_map.dim() == 1, "expert_map must be 1-d (global_num_experts,)")
+        emap = expert_map.to(torch.int32).contiguous()
+        n_global = emap.numel() if global_num_experts is None else int(global_num_experts)
+        _check(n_global == emap.numel(),
+               f"expert_map must have global_num_experts={n_global} entries")
+    else:
+        n_global = E if global_num_experts is None else int(global_num_experts)
+        _check(n_global == E, "global_num_experts differs from the local expert count; "
+                              "pass expert_map")
+    tensors = [x, w13, w2, w13_s, w2_s, topk_weights, topk_ids]
+    tensors += [t for t in (z13, z2, emap) if t is not None]
+    _check(all(t.is_cuda and t.device == x.device for t in tensors),
+           "all tensors must be CUDA tensors on x's device")
     ws = _workspace(lib.w4a8_moe_apply_workspace_size(T, H, inter, E, top_k), x.device)
-    return T, H, inter, E, gs, frag, z13, z2, ws
+    return T, H, inter, E, gs, top_k, frag, z13, z2, emap, n_global, ws
 
 
 def moe_apply(x, w13, w2, w13_s, w2_s, w13_z, w2_z, topk_weights, topk_ids, expert_map=None,
-              weight_is_e2m1: bool = False) -> torch.Tensor:
+              weight_is_e2m1: bool = False, global_num_experts: int | None = None) -> torch.Tensor:
     """Whole gated-SiLU MoE layer in one C-ABI call (the _run_grouped_moe composition,
     moe_experts.py:493-665). x (T, H) fp16/bf16 -> (T, H) same dtype. w13 / w2 are op-layout
-    (E, N, K/8) int32, or both fragment layout from repack_fragments (5-d)."""
+    (E, N, K/8) int32, or both fragment layout from repack_fragments (5-d). topk_ids hold
+    global expert ids; with expert_map (global_num_experts entries, -1 = not local) they are
+    mapped to the E local experts."""
     x = x.contiguous()
-    top_k = topk_ids.shape[1]
-    T, H, inter, E, gs, frag, z13, z2, ws = _layer_args(x, w13, w2, w13_s, w2_s, w13_z, w2_z,
-                                                        top_k, weight_is_e2m1)
+    T, H, inter, E, gs, top_k, frag, z13, z2, emap, n_global, ws = _layer_args(
+        x, w13, w2, w13_s, w2_s, w13_z, w2_z, topk_weights, topk_ids, expert_map,
+        global_num_experts, weight_is_e2m1)
     tw = topk_weights.to(torch.float32).contiguous()
     ids = topk_ids.to(torch.int32).contiguous()
-    emap = None if expert_map is None else expert_map.to(torch.int32).contiguous()
     out = torch.empty_like(x)
     dt = 1 if x.dtype == torch.bfloat16 else 0
     if frag:
         check(lib.w4a8_moe_apply_fragments(
             _ptr(x), dt, T, H, inter, E, top_k, gs, _ptr(w13), _ptr(w13_s), _ptr(z13), _ptr(w2),
-            _ptr(w2_s), _ptr(z2), _ptr(tw), _ptr(ids), _ptr(emap), _ptr(out), ws.data_ptr(),
-            ws.numel(), _stream(x)), "moe_apply")
+            _ptr(w2_s), _ptr(z2), _ptr(tw), _ptr(ids), _ptr(emap), n_global, _ptr(out),
+            ws.data_ptr(), ws.numel(), _stream(x)), "moe_apply")
     else:
         check(lib.w4a8_moe_apply(
             _ptr(x), dt, T, H, inter, E, top_k, gs, _ptr(w13), _ptr(w13_s), _ptr(z13), _ptr(w2),
-            _ptr(w2_s), _ptr(z2), _ptr(tw), _ptr(ids), _ptr(emap), int(bool(weight_is_e2m1)),
-            _ptr(out), ws.data_ptr(), ws.numel(), _stream(x)), "moe_apply")
+            _ptr(w2_s), _ptr(z2), _ptr(tw), _ptr(ids), _ptr(emap), n_global,
+            int(bool(weight_is_e2m1)), _ptr(out), ws.data_ptr(), ws.numel(), _stream(x)),
+            "moe_apply")
     return out
 
 
 def moe_forward(x, router_logits, top_k: int, w13, w2, w13_s, w2_s, w13_z, w2_z,
                 renormalize: bool = True, expert_map=None):
     """Router (softmax / top-k / renormalise, the vLLM fused_topk contract) plus the expert
-    path in one C-ABI call.
-    Returns (out (T, H) in x.dtype, topk_weights (T, k) fp32, topk_ids (T, k) int32)."""
+    path in one C-ABI call. router_logits is (T, global experts): E without expert_map, else
+    the map's length. Returns (out (T, H) in x.dtype, topk_weights (T, k) fp32, topk_ids
+    (T, k) int32)."""
     x = x.contiguous()
-    T, H, inter, E, gs, frag, z13, z2, ws = _layer_args(x, w13, w2, w13_s, w2_s, w13_z, w2_z,
-                                                        top_k, False)
-    lg = router_logits.to(torch.float32).contiguous()
-    _check(lg.shape == (T, E), f"router_logits must be (T, E)=({T},{E})")
-    emap = None if expert_map is None else expert_map.to(torch.int32).contiguous()
-    out = torch.empty_like(x)
+    _check(router_logits.dim() == 2 and router_logits.shape[0] == x.shape[0],
+           "router_logits must be (T, global experts)")
+    T = x.shape[0]
     tw = torch.empty((T, top_k), dtype=torch.float32, device=x.device)
     ids = torch.empty((T, top_k), dtype=torch.int32, device=x.device)
+    T, H, inter, E, gs, top_k, frag, z13, z2, emap, n_global, ws = _layer_args(
+        x, w13, w2, w13_s, w2_s, w13_z, w2_z, tw, ids, expert_map, router_logits.shape[1], False)
+    lg = router_logits.to(torch.float32).contiguous()
+    out = torch.empty_like(x)
     check(lib.w4a8_moe_forward(
         _ptr(x), 1 if x.dtype == torch.bfloat16 else 0, T, H, inter, E, top_k, gs, _ptr(lg),
         int(bool(renormalize)), _ptr(w13), _ptr(w13_s), _ptr(z13), _ptr(w2), _ptr(w2_s),
-        _ptr(z2), 1 if frag else 0, _ptr(emap), _ptr(tw), _ptr(ids), _ptr(out), ws.data_ptr(),
-        ws.numel(), _stream(x)), "moe_forward")
+        _ptr(z2), 1 if frag else 0, _ptr(emap), n_global, _ptr(tw), _ptr(ids), _ptr(out),
+        ws.data_ptr(), ws.numel(), _stream(x)), "moe_forward")
     return out, tw, ids
+
+
+def fragments_supported(hidden: int, inter: int, group_size: int) -> bool:
+    """Whether moe_apply takes fragment-layout weights of this shape for every batch size
+    (what a load hook checks before it repacks)."""
+    return bool(lib.w4a8_moe_fragments_supported(int(hidden), int(inter), int(group_size)))

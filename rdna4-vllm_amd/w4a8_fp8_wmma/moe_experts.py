@@ -1,17 +1,20 @@
-"""MoE composition, weight-layout converters and the vLLM MoeWNA16 hook (gfx950).
+"""MoE composition, weight-format conversion and the vLLM MoeWNA16 load/apply hook (gfx950).
 
-Mirrors w4a8_fp8_wmma/w4a8_fp8_wmma/moe_experts.py of patcarter883/rdna4-vllm:
-  * ``_run_grouped_moe`` keeps the reference signature and return contract
-    (moe_experts.py:493-665): (M, K) output in ``out_dtype``, topk-weighted and reduced;
-  * the AWQ / compressed-tensors / MoeWNA16 converters (:331-482) produce the op layout;
+Call surface of w4a8_fp8_wmma/w4a8_fp8_wmma/moe_experts.py in patcarter883/rdna4-vllm:
+  * ``_run_grouped_moe`` keeps the reference argument list and return contract
+    (moe_experts.py:493-665): an (M, K) output in ``out_dtype``, top-k weighted and reduced;
+  * ``_awq_moe_to_op_layout`` / ``_ct_moe_to_op_layout`` / ``_wna16_moe_to_op_layout`` turn the
+    on-disk formats into the op layout (:331-482);
   * ``register_moe_wna16`` patches ``MoeWNA16Method`` (:1253-1341) when vLLM is present.
 
-On MI355X the SiLU-gated path is one C-ABI call (``moe_apply``) that schedules
-align -> act-quant -> gemm1+SiLU -> act-quant -> gemm2 -> weighted reduce on the GPU.
-There is no crossover gate and no stock fallback: every supported batch runs here.
+On MI355X the SiLU-gated layer is one C-ABI call (``moe_apply``): align, act-quant,
+gemm1+SiLU, act-quant, gemm2 and the weighted reduce all run on the GPU. The load hook
+repacks the int4 weights once into the fragment layout the gfx950 kernels stream, in place
+of the u8 parameters (no second copy). There is no crossover gate and no stock fallback.
 """
 from __future__ import annotations
 
+import dataclasses
 import logging
 import os
 from typing import Optional
@@ -24,123 +27,142 @@ from . import (mmq_fp8_moe_gemm, mmq_fp8_moe_gather_reduce, moe_align_block_size
 
 logger = logging.getLogger(__name__)
 
-_REVERSE_AWQ_PACK_ORDER = [0, 4, 1, 5, 2, 6, 3, 7]   # moe_experts.py:47
-_VALID_MOE_KERNELS = ("scalar", "wmma", "gemv")      # moe_experts.py:72
+# Bit position (in nibbles) of logical column c inside an AWQ-packed int32 word: the AWQ
+# writer interleaves the eight columns as 0, 2, 4, 6, 1, 3, 5, 7 (moe_experts.py:47 holds the
+# inverse list, [0, 4, 1, 5, 2, 6, 3, 7], which reads column c from nibble AWQ_NIBBLE_OF[c]).
+AWQ_NIBBLE_OF = (0, 4, 1, 5, 2, 6, 3, 7)
+MOE_KERNEL_NAMES = ("scalar", "wmma", "gemv")        # moe_experts.py:72
 GEMV_MAX_M = 96                                      # moe_experts.py:563
 APPLY_CHUNK = 4096                                   # moe_experts.py:533
+# Transient bytes a converter may hold per chunk of experts (unpacked nibbles are bytes).
+_CONVERT_CHUNK_BYTES = 256 << 20
 
 
 # --------------------------------------------------------------------------- #
-# env surface (moe_experts.py:61-122)
+# configuration (environment names of moe_experts.py:61-122)
 # --------------------------------------------------------------------------- #
+@dataclasses.dataclass(frozen=True)
+class MoeEnv:
+    enabled: bool            # VLLM_ROCM_USE_W4A8_FP8_WMMA and VLLM_ROCM_W4A8_FP8_WMMA_MOE
+    kernel: str              # VLLM_ROCM_W4A8_FP8_WMMA_MOE_KERNEL (scalar | wmma | gemv)
+    block_m: Optional[int]   # VLLM_ROCM_W4A8_FP8_WMMA_MOE_BLOCK_M (op-by-op composition)
+    apply_chunk: int         # VLLM_ROCM_W4A8_FP8_WMMA_MOE_APPLY_CHUNK (tokens per call)
+
+    REMOVED = ("VLLM_ROCM_W4A8_FP8_WMMA_MOE_VERSION",)
+
+    @classmethod
+    def read(cls) -> "MoeEnv":
+        env = os.environ
+        for name in cls.REMOVED:
+            if name in env:
+                raise RuntimeError(
+                    f"{name} is removed; set VLLM_ROCM_W4A8_FP8_WMMA_MOE_KERNEL="
+                    f"{'|'.join(MOE_KERNEL_NAMES)} instead.")
+        kernel = env.get("VLLM_ROCM_W4A8_FP8_WMMA_MOE_KERNEL", "wmma")
+        if kernel not in MOE_KERNEL_NAMES:
+            raise RuntimeError(f"VLLM_ROCM_W4A8_FP8_WMMA_MOE_KERNEL={kernel!r} invalid; "
+                               f"use one of {list(MOE_KERNEL_NAMES)}")
+        bm = env.get("VLLM_ROCM_W4A8_FP8_WMMA_MOE_BLOCK_M")
+        return cls(
+            enabled=(env.get("VLLM_ROCM_USE_W4A8_FP8_WMMA", "1") == "1"
+                     and env.get("VLLM_ROCM_W4A8_FP8_WMMA_MOE", "1") == "1"),
+            kernel=kernel,
+            block_m=int(bm) if bm else None,
+            apply_chunk=int(env.get("VLLM_ROCM_W4A8_FP8_WMMA_MOE_APPLY_CHUNK", str(APPLY_CHUNK))))
+
+
 def _moe_enabled() -> bool:
-    if os.environ.get("VLLM_ROCM_USE_W4A8_FP8_WMMA", "1") != "1":
-        return False
-    return os.environ.get("VLLM_ROCM_W4A8_FP8_WMMA_MOE", "1") == "1"
-
-
-def _raise_if_removed_moe_env() -> None:
-    """Hard-break on the removed numeric kernel override (moe_experts.py:75-86)."""
-    if "VLLM_ROCM_W4A8_FP8_WMMA_MOE_VERSION" in os.environ:
-        raise RuntimeError(
-            "VLLM_ROCM_W4A8_FP8_WMMA_MOE_VERSION is removed; set "
-            "VLLM_ROCM_W4A8_FP8_WMMA_MOE_KERNEL=wmma|scalar|gemv instead.")
+    return MoeEnv.read().enabled
 
 
 def _moe_kernel() -> str:
-    """Grouped-kernel name from VLLM_ROCM_W4A8_FP8_WMMA_MOE_KERNEL (moe_experts.py:89-100)."""
-    _raise_if_removed_moe_env()
-    kernel = os.environ.get("VLLM_ROCM_W4A8_FP8_WMMA_MOE_KERNEL", "wmma")
-    if kernel not in _VALID_MOE_KERNELS:
-        raise RuntimeError(
-            f"VLLM_ROCM_W4A8_FP8_WMMA_MOE_KERNEL={kernel!r} invalid; "
-            f"use one of {list(_VALID_MOE_KERNELS)}")
-    return kernel
-
-
-def _choose_block_m(M: int, top_k: int, num_experts: int) -> int:
-    """moe_align block size for the op-composed path (moe_experts.py:314-325)."""
-    env = os.environ.get("VLLM_ROCM_W4A8_FP8_WMMA_MOE_BLOCK_M")
-    if env:
-        return int(env)
-    return 64
+    """Grouped-kernel name (moe_experts.py:89-100); raises on removed or invalid knobs."""
+    return MoeEnv.read().kernel
 
 
 def _supported_group_size(gs) -> bool:
-    return gs is not None and 16 <= gs <= 128 and gs % 16 == 0   # moe_experts.py:485-486
+    """Group sizes the kernels take: multiples of 16 up to 128 (moe_experts.py:485-486)."""
+    return gs is not None and gs % 16 == 0 and 16 <= gs <= 128
 
 
 # --------------------------------------------------------------------------- #
-# weight-layout converters
+# weight formats -> op layout
+#
+# Op layout (moe_kernel.hip:7-17): w (E, N, K/8) int32 with nibble j of word w at k = 8w + j,
+# which is byte-for-byte vLLM's standard u8 layout (E, N, K/2) (byte b: k = 2b low nibble,
+# 2b + 1 high); zero-points (E, N/8, G) int32 with nibble n % 8 of word n / 8, i.e. four
+# consecutive bytes along N of the u8 layout (E, N/2, G).
 # --------------------------------------------------------------------------- #
-def _awq_to_op_layout_single(qw_e, sc_e, qz_e, pf, size_bits, rev, shifts):
-    """One expert AWQ (K, N/pf) packed along output, AWQ order -> op layout
-    w (N, K/pf) int32, scales (N, G) fp16, zeros (N/pf, G) int32 (moe_experts.py:331-368)."""
-    mask = (1 << size_bits) - 1
-    K, Np = qw_e.shape
-    N = Np * pf
-    G = qz_e.shape[0]
-    uw = ((qw_e.unsqueeze(-1) >> shifts) & mask)[:, :, rev].reshape(K, N)
-    uw = uw.t().contiguous().to(torch.int32)                     # (N, K)
-    w = torch.zeros((N, K // pf), dtype=torch.int32, device=qw_e.device)
-    for j in range(pf):
-        w |= (uw[:, j::pf] & mask) << (j * size_bits)
-    s = sc_e.t().contiguous().to(torch.float16)
-    uz = ((qz_e.unsqueeze(-1) >> shifts) & mask)[:, :, rev].reshape(G, N)
-    uz = uz.t().contiguous().to(torch.int32)                     # (N, G)
-    z = torch.zeros((N // pf, G), dtype=torch.int32, device=qw_e.device)
-    for j in range(pf):
-        z |= (uz[j::pf, :] & mask) << (j * size_bits)
-    return w, s, z
+def _nibbles(words: torch.Tensor) -> torch.Tensor:
+    """(..., W) int32 -> (..., W, 8) uint8: nibble p of each word, p = 0 lowest."""
+    b = words.contiguous().view(torch.uint8).reshape(*words.shape, 4)
+    return torch.stack((b & 0xF, b >> 4), dim=-1).reshape(*words.shape, 8)
+
+
+def _pack_bytes_last(nib: torch.Tensor) -> torch.Tensor:
+    """(..., L) nibbles (L even) -> (..., L/2) uint8, element 2i low, 2i + 1 high."""
+    return nib[..., 0::2] | (nib[..., 1::2] << 4)
+
+
+def _zero_bytes_to_op(zb: torch.Tensor) -> torch.Tensor:
+    """Zero-point bytes grouped by K group, (E, G, N/2) u8 (byte i: n = 2i low, 2i + 1 high)
+    -> op layout (E, N/8, G) int32: four consecutive bytes are one little-endian word."""
+    E, G, nh = zb.shape
+    words = zb.contiguous().view(-1).view(torch.int32).view(E, G, nh // 4)
+    return words.transpose(1, 2).contiguous()
+
+
+def _expert_chunks(E: int, bytes_per_expert: int):
+    step = max(1, _CONVERT_CHUNK_BYTES // max(1, bytes_per_expert))
+    for lo in range(0, E, step):
+        yield lo, min(E, lo + step)
 
 
 def _awq_moe_to_op_layout(qweight, scales, qzeros, group_size, size_bits: int = 4):
-    """AWQ MoE (E, K, N/8) -> (w (E,N,K/8), scales (E,N,G) fp16, zeros (E,N/8,G))
-    (moe_experts.py:371-396). Looped over experts to bound transient memory."""
-    pf = 32 // size_bits
-    dev = qweight.device
-    rev = torch.tensor(_REVERSE_AWQ_PACK_ORDER[:pf], dtype=torch.long, device=dev)
-    shifts = torch.arange(0, 32, size_bits, dtype=torch.int32, device=dev)
-    outs = [_awq_to_op_layout_single(qweight[e], scales[e], qzeros[e], pf, size_bits, rev, shifts)
-            for e in range(qweight.shape[0])]
-    return tuple(torch.stack(t).contiguous() for t in zip(*outs))
+    """AWQ MoE checkpoint tensors -> op layout (moe_experts.py:371-396).
 
-
-def _ct_to_op_layout_single(qw_e, sc_e, pf, size_bits, shifts):
-    """compressed-tensors (GPTQ-convention, packed along K) -> op layout
-    (moe_experts.py:409-434)."""
-    mask = (1 << size_bits) - 1
-    Kp, N = qw_e.shape
-    K = Kp * pf
-    uw = ((qw_e.unsqueeze(1) >> shifts.view(1, pf, 1)) & mask).reshape(K, N)
-    w_kn = uw.t().contiguous().to(torch.int32)
-    w = torch.zeros((N, K // pf), dtype=torch.int32, device=qw_e.device)
-    for j in range(pf):
-        w |= (w_kn[:, j::pf] & mask) << (j * size_bits)
-    return w, sc_e.t().contiguous().to(torch.float16)
+    qweight (E, K, N/8) int32 and qzeros (E, G, N/8) int32 pack eight output columns per word
+    in the AWQ interleave; scales (E, G, N). The nibbles are regrouped by column, transposed
+    to (N, K) and re-packed as the standard u8 layout, which the op layout views as int32."""
+    if size_bits != 4:
+        raise NotImplementedError("AWQ MoE conversion supports int4 weights only")
+    order = torch.tensor(AWQ_NIBBLE_OF, dtype=torch.long, device=qweight.device)
+    E, K, Nw = qweight.shape
+    N = Nw * 8
+    w = torch.empty((E, N, K // 2), dtype=torch.uint8, device=qweight.device)
+    for lo, hi in _expert_chunks(E, K * N):
+        cols = _nibbles(qweight[lo:hi]).index_select(-1, order).reshape(hi - lo, K, N)
+        w[lo:hi] = _pack_bytes_last(cols.transpose(1, 2))
+    zcols = _nibbles(qzeros).index_select(-1, order).reshape(E, qzeros.shape[1], N)
+    return (w.view(torch.int32), scales.transpose(1, 2).contiguous().to(torch.float16),
+            _zero_bytes_to_op(_pack_bytes_last(zcols)))
 
 
 def _ct_moe_to_op_layout(qweight, scales, size_bits: int = 4):
-    """(moe_experts.py:437-454); symmetric uint4b8, no zero-points."""
-    pf = 32 // size_bits
-    shifts = torch.arange(0, 32, size_bits, dtype=torch.int32, device=qweight.device)
-    outs = [_ct_to_op_layout_single(qweight[e], scales[e], pf, size_bits, shifts)
-            for e in range(qweight.shape[0])]
-    return tuple(torch.stack(t).contiguous() for t in zip(*outs))
+    """compressed-tensors / GPTQ MoE (moe_experts.py:437-454): qweight (E, K/8, N) int32 packs
+    eight consecutive k per word with nibble j = k % 8, the op layout's own word format, so
+    the conversion is a transpose of whole words. Symmetric uint4b8: no zero-points."""
+    if size_bits != 4:
+        raise NotImplementedError("compressed-tensors MoE conversion supports int4 weights only")
+    return (qweight.transpose(1, 2).contiguous(),
+            scales.transpose(1, 2).contiguous().to(torch.float16))
 
 
 def _wna16_moe_to_op_layout(qweight_u8, scales, qzeros_u8):
-    """MoeWNA16 u8 params -> op layout, zero-copy for the weights (moe_experts.py:473-482):
-    (E, N, K/2) u8 .view(int32) -> (E, N, K/8); qzeros (E, N/2, G) u8 -> (E, N/8, G) int32."""
+    """MoeWNA16 parameters (standard u8 layout, moe_experts.py:473-482) -> op layout: the
+    weights are a zero-copy int32 view; zero-points regroup four N-bytes per int32."""
     w = qweight_u8.contiguous().view(torch.int32)
     s = scales if scales.dtype == torch.float16 else scales.to(torch.float16)
-    z = None
-    if qzeros_u8 is not None:
-        E, Nh, G = qzeros_u8.shape
-        zi = qzeros_u8.contiguous().to(torch.int32).reshape(E, Nh // 4, 4, G)
-        z = (zi[:, :, 0, :] | (zi[:, :, 1, :] << 8) | (zi[:, :, 2, :] << 16)
-             | (zi[:, :, 3, :] << 24)).contiguous()
+    z = None if qzeros_u8 is None else _zero_bytes_to_op(qzeros_u8.transpose(1, 2))
     return w, s, z
+
+
+def _fragments_to_op_layout(w_frag: torch.Tensor) -> torch.Tensor:
+    """Fragment layout (E, N/16, K/128, 64, 4) -> op layout (E, N, K/8): lane l = 16 q + c of
+    block (t, g) holds row 16 t + c, words 16 g + 4 q .. + 3."""
+    E, NT, G = w_frag.shape[:3]
+    v = w_frag.reshape(E, NT, G, 4, 16, 4).permute(0, 1, 4, 2, 3, 5)
+    return v.reshape(E, NT * 16, G * 16).contiguous()
 
 
 # --------------------------------------------------------------------------- #
@@ -152,29 +174,28 @@ def _activation_name(activation) -> str:
 
 
 def _run_unfused(x16, w1, w2, w1_s, w2_s, w1_zp, w2_zp, tw_flat, topk_ids, top_k,
-                 global_num_experts, expert_map, kernel, weight_is_e2m1, w1_bias, w2_bias):
-    """Op-by-op composition (moe_experts.py:587-665): align -> gemm1 -> (+bias) ->
-    silu_and_mul -> gemm2 (identity gather) -> (+bias) -> gather-reduce. Used for the
-    "scalar" golden kernel and for per-expert biases."""
-    block_m = _choose_block_m(x16.size(0), top_k, w1.size(0))
+                 global_num_experts, expert_map, kernel, weight_is_e2m1, w1_bias, w2_bias,
+                 block_m):
+    """Op-by-op composition (moe_experts.py:587-665): align, gemm1, + bias, silu_and_mul,
+    gemm2 on the padded rows, + bias, gather-reduce. Runs the "scalar" golden kernel and
+    layers with per-expert biases."""
     sorted_ids, expert_ids, ntp = moe_align_block_size(
         topk_ids, block_m, global_num_experts, expert_map)
     P = sorted_ids.size(0)
-
-    def _expand_bias(bias):
-        return bias[expert_ids.clamp(min=0).long()].repeat_interleave(block_m, dim=0)[:P]
+    # per-padded-row expert of every block, for the (E, N) bias tables
+    row_expert = expert_ids.clamp(min=0).long().repeat_interleave(block_m)[:P]
 
     out1 = mmq_fp8_moe_gemm(x16, w1, w1_s, sorted_ids, expert_ids, ntp, top_k, block_m,
                             kernel=kernel, w_zeros=w1_zp, weight_is_e2m1=weight_is_e2m1)
     if w1_bias is not None:
-        out1 = out1 + _expand_bias(w1_bias).to(out1.dtype)
-    buf2 = torch.empty((P, out1.size(1) // 2), dtype=torch.float16, device=x16.device)
-    silu_and_mul(buf2, out1.contiguous())
-    ident = torch.arange(P, dtype=torch.int32, device=x16.device)
-    out2 = mmq_fp8_moe_gemm(buf2, w2, w2_s, ident, expert_ids, ntp, 1, block_m,
+        out1 = out1 + w1_bias.to(out1.dtype).index_select(0, row_expert)
+    h = torch.empty((P, out1.size(1) // 2), dtype=torch.float16, device=x16.device)
+    silu_and_mul(h, out1.contiguous())
+    rows = torch.arange(P, dtype=torch.int32, device=x16.device)   # gemm2 gathers by row
+    out2 = mmq_fp8_moe_gemm(h, w2, w2_s, rows, expert_ids, ntp, 1, block_m,
                             kernel=kernel, w_zeros=w2_zp, weight_is_e2m1=weight_is_e2m1)
     if w2_bias is not None:
-        out2 = out2 + _expand_bias(w2_bias).to(out2.dtype)
+        out2 = out2 + w2_bias.to(out2.dtype).index_select(0, row_expert)
     return mmq_fp8_moe_gather_reduce(out2.contiguous(), sorted_ids, tw_flat, ntp, top_k)
 
 
@@ -185,54 +206,55 @@ def _run_grouped_moe(x, w1, w2, w1_s, w2_s, w1_zp, w2_zp,
                      weight_is_e2m1=False, w1_bias=None, w2_bias=None):
     """Whole gated MoE -> (M, K) in ``out_dtype`` (moe_experts.py:493-665).
 
-    Weights are in op layout: w1 (E, 2*inter, K/8), w2 (E, K, inter/8), scales
-    (E, N, K/g), zero-points (E, N/8, K/g) or None (symmetric, zp = 8)."""
+    w1 (E, 2*inter, K/8) / w2 (E, K, inter/8) int32 in the op layout, or both in the fragment
+    layout (5-d, ``repack_fragments``); scales (E, N, K/g); zero-points (E, N/8, K/g) or None
+    (symmetric, zp = 8). topk_ids are global expert ids; ``expert_map`` maps them to the E
+    local experts."""
     M, K = x.shape
     top_k = topk_ids.size(1)
-    if out_dtype is None:
-        out_dtype = x.dtype
+    out_dtype = x.dtype if out_dtype is None else out_dtype
     if _activation_name(activation) != "silu":
         raise NotImplementedError(
             f"w4a8_fp8_wmma (gfx950) implements the SiLU-gated MoE; got {activation!r}")
-    if kernel not in _VALID_MOE_KERNELS:
-        raise ValueError(f"unknown moe kernel {kernel!r}; known: {list(_VALID_MOE_KERNELS)}")
+    if kernel not in MOE_KERNEL_NAMES:
+        raise ValueError(f"unknown moe kernel {kernel!r}; known: {list(MOE_KERNEL_NAMES)}")
+    env = MoeEnv.read()
 
-    chunk = int(os.environ.get("VLLM_ROCM_W4A8_FP8_WMMA_MOE_APPLY_CHUNK", str(APPLY_CHUNK)))
-    if chunk and M > chunk and not apply_router_weight_on_input:
+    if env.apply_chunk and M > env.apply_chunk and not apply_router_weight_on_input:
+        # bounded intermediates: the layer is token-separable, so chunks are independent
         out = torch.empty((M, K), dtype=out_dtype, device=x.device)
-        for lo in range(0, M, chunk):
-            hi = min(lo + chunk, M)
+        for lo in range(0, M, env.apply_chunk):
+            hi = min(lo + env.apply_chunk, M)
             out[lo:hi] = _run_grouped_moe(
                 x[lo:hi], w1, w2, w1_s, w2_s, w1_zp, w2_zp, topk_weights[lo:hi],
                 topk_ids[lo:hi], activation, global_num_experts, expert_map, False, kernel,
                 out_dtype, weight_is_e2m1=weight_is_e2m1, w1_bias=w1_bias, w2_bias=w2_bias)
         return out
 
-    w1_s = w1_s if w1_s.dtype == torch.float16 else w1_s.to(torch.float16)
-    w2_s = w2_s if w2_s.dtype == torch.float16 else w2_s.to(torch.float16)
-    x_in = x
+    w1_s = w1_s.to(torch.float16)
+    w2_s = w2_s.to(torch.float16)
     if apply_router_weight_on_input:
-        assert top_k == 1, "router-weight-on-input requires top_k==1"
-        x_in = x_in * topk_weights.reshape(M, 1).to(x_in.dtype)
+        if top_k != 1:
+            raise ValueError("router-weight-on-input requires top_k == 1")
+        x = x * topk_weights.reshape(M, 1).to(x.dtype)
         tw = torch.ones((M, top_k), dtype=torch.float32, device=x.device)
     else:
         tw = topk_weights.to(torch.float32)
     ids = topk_ids.to(torch.int32)
 
-    has_bias = w1_bias is not None or w2_bias is not None
-    if kernel == "scalar" or has_bias:
-        x16 = x_in.to(torch.float16).contiguous()
-        acc = _run_unfused(x16, w1, w2, w1_s, w2_s, w1_zp, w2_zp, tw.reshape(-1).contiguous(),
-                           ids, top_k, global_num_experts, expert_map, kernel, weight_is_e2m1,
-                           w1_bias, w2_bias)
+    if kernel == "scalar" or w1_bias is not None or w2_bias is not None:
+        if w1.dim() == 5:   # the op-by-op kernels read the op layout
+            w1, w2 = _fragments_to_op_layout(w1), _fragments_to_op_layout(w2)
+        acc = _run_unfused(x.to(torch.float16).contiguous(), w1, w2, w1_s, w2_s, w1_zp, w2_zp,
+                           tw.reshape(-1).contiguous(), ids, top_k, global_num_experts,
+                           expert_map, kernel, weight_is_e2m1, w1_bias, w2_bias,
+                           env.block_m or 64)
         return acc.to(out_dtype)
 
-    if global_num_experts != w1.size(0) and expert_map is None:
-        raise ValueError("global_num_experts differs from the local expert count; "
-                         "pass expert_map")
-    xin = x_in if x_in.dtype in (torch.float16, torch.bfloat16) else x_in.to(torch.float16)
-    out = _ops.moe_apply(xin, w1, w2, w1_s, w2_s, w1_zp, w2_zp, tw, ids, expert_map,
-                         weight_is_e2m1)
+    if x.dtype not in (torch.float16, torch.bfloat16):
+        x = x.to(torch.float16)
+    out = _ops.moe_apply(x, w1, w2, w1_s, w2_s, w1_zp, w2_zp, tw, ids, expert_map,
+                         weight_is_e2m1, global_num_experts=global_num_experts)
     return out if out.dtype == out_dtype else out.to(out_dtype)
 
 
@@ -264,19 +286,117 @@ if not hasattr(torch.ops.vllm, "w4a8_moe_apply"):
 # --------------------------------------------------------------------------- #
 # vLLM MoeWNA16 hook (moe_experts.py:1253-1341)
 # --------------------------------------------------------------------------- #
+class MoeWNA16Hook:
+    """Load and apply hooks for a ``MoeWNA16Method``-like class.
+
+    Load (``process_weights_after_loading``): after the stock step, an int4 layer with a
+    supported group size gets op-layout scales and zero-points, and its weights are repacked
+    once into the gfx950 fragment layout, written over the u8 parameters' own storage (same
+    byte count, no second copy; the parameters keep their shapes). Shapes the fragment
+    kernels do not take, and the "scalar" golden kernel, keep zero-copy op-layout views.
+    Apply: every batch of an engaged layer runs ``_run_grouped_moe``; other layers keep the
+    stock apply."""
+
+    ATTR = "_w4a8_wna16"
+
+    def __init__(self, method_cls, verbose: bool = False):
+        self.method_cls = method_cls
+        self.verbose = verbose
+        self.stock_process = method_cls.process_weights_after_loading
+        self.stock_apply = method_cls.apply
+
+    @staticmethod
+    def engages(method, layer) -> bool:
+        try:
+            return (method.quant_config.weight_bits == 4
+                    and _supported_group_size(layer.group_size))
+        except AttributeError:
+            return False
+
+    @staticmethod
+    def prepare(layer, has_zp: bool, kernel: str) -> str:
+        """Builds the layer's ``_w4a8`` weight record; returns the weight layout used."""
+        views = {}
+        for name in ("w13", "w2"):
+            views[name] = _wna16_moe_to_op_layout(
+                getattr(layer, f"{name}_qweight").data, getattr(layer, f"{name}_scales").data,
+                getattr(layer, f"{name}_qzeros").data if has_zp else None)
+        w13, s13, z13 = views["w13"]
+        w2, s2, z2 = views["w2"]
+        E, N13, kw = w13.shape
+        hidden, inter = kw * 8, N13 // 2
+        group = hidden // s13.shape[2]
+        layout = "op"
+        if kernel != "scalar" and _ops.fragments_supported(hidden, inter, group):
+            layout = "fragments"
+            for name in ("w13", "w2"):
+                param = getattr(layer, f"{name}_qweight")
+                frag = _ops.repack_fragments(views[name][0])
+                # the fragments replace the u8 bytes in place: same size, same parameter
+                param.data.view(torch.int32).view(-1).copy_(frag.view(-1))
+                views[name] = (param.data.view(torch.int32).view(frag.shape),) + views[name][1:]
+            w13, w2 = views["w13"][0], views["w2"][0]
+        layer._w4a8 = dict(w13=w13, w2=w2, s13=s13, s2=s2, z13=z13, z2=z2, layout=layout)
+        return layout
+
+    def process(self, method, layer):
+        engaged = self.engages(method, layer)
+        setattr(method, self.ATTR, engaged)
+        self.stock_process(method, layer)
+        if not engaged:
+            return
+        has_zp = bool(getattr(method.quant_config, "has_zp", False))
+        layout = self.prepare(layer, has_zp, _moe_kernel())
+        if self.verbose:
+            print(f"[w4a8_fp8_wmma] WNA16 MoE weights ready (int4 g={layer.group_size} "
+                  f"has_zp={has_zp}, {layout} layout) -> gfx950 grouped fp8 MFMA")
+
+    def apply(self, method, layer, x, topk_weights, topk_ids, shared_experts=None,
+              shared_experts_input=None):
+        if not getattr(method, self.ATTR, False):
+            return self.stock_apply(method, layer, x, topk_weights, topk_ids, shared_experts,
+                                    shared_experts_input)
+        w = layer._w4a8
+        flat = x.reshape(-1, x.shape[-1])
+        out = _run_grouped_moe(
+            flat, w["w13"], w["w2"], w["s13"], w["s2"], w["z13"], w["z2"], topk_weights,
+            topk_ids, layer.activation, layer.global_num_experts, layer.expert_map,
+            layer.apply_router_weight_on_input, _moe_kernel(), out_dtype=x.dtype)
+        return out.reshape(*x.shape[:-1], out.shape[-1])
+
+    def install(self) -> None:
+        hook = self
+
+        def process_weights_after_loading(self, layer):
+            hook.process(self, layer)
+
+        def apply(self, layer, x, topk_weights, topk_ids, shared_experts=None,
+                  shared_experts_input=None):
+            return hook.apply(self, layer, x, topk_weights, topk_ids, shared_experts,
+                              shared_experts_input)
+
+        self.method_cls.process_weights_after_loading = process_weights_after_loading
+        self.method_cls.apply = apply
+
+
 _MOE_WNA16_REGISTERED = False
 
 
+def install_moe_wna16_hooks(method_cls, verbose: bool = False) -> MoeWNA16Hook:
+    """Patch a MoeWNA16Method-like class (split out so tests can use a stand-in class)."""
+    hook = MoeWNA16Hook(method_cls, verbose)
+    hook.install()
+    return hook
+
+
 def register_moe_wna16(verbose: bool = True) -> bool:
-    """Route int4 MoeWNA16 expert layers to the gfx950 path by patching
-    ``MoeWNA16Method.process_weights_after_loading`` (zero-copy op-layout views) and
-    ``.apply`` (``_run_grouped_moe``). Idempotent; returns False without vLLM or when
-    disabled by env. Engages for every batch (no crossover gate)."""
+    """Route int4 MoeWNA16 expert layers to the gfx950 path. Idempotent; False without vLLM
+    or when disabled by the environment. Engages for every batch (no crossover gate)."""
     global _MOE_WNA16_REGISTERED
     if _MOE_WNA16_REGISTERED:
         return True
-    _raise_if_removed_moe_env()
-    if not _moe_enabled():
+    env = MoeEnv.read()   # raises on removed knobs at boot
+    if not env.enabled:
         if verbose:
             print("[w4a8_fp8_wmma] WNA16 MoE disabled via env")
         return False
@@ -289,50 +409,3 @@ def register_moe_wna16(verbose: bool = True) -> bool:
     install_moe_wna16_hooks(MoeWNA16Method, verbose)
     _MOE_WNA16_REGISTERED = True
     return True
-
-
-def install_moe_wna16_hooks(method_cls, verbose: bool = False) -> None:
-    """Patch ``process_weights_after_loading`` / ``apply`` on a MoeWNA16Method-like class
-    (split out so tests can drive it with a stand-in class)."""
-    _orig_process = method_cls.process_weights_after_loading
-    _orig_apply = method_cls.apply
-
-    def _patched_process(self, layer):
-        try:
-            eng = (self.quant_config.weight_bits == 4
-                   and _supported_group_size(layer.group_size))
-        except Exception:  # noqa: BLE001
-            eng = False
-        self._w4a8_wna16 = eng
-        _orig_process(self, layer)
-        if not eng:
-            return
-        has_zp = bool(getattr(self.quant_config, "has_zp", False))
-        w13, w13_s, w13_z = _wna16_moe_to_op_layout(
-            layer.w13_qweight.data, layer.w13_scales.data,
-            layer.w13_qzeros.data if has_zp else None)
-        w2, w2_s, w2_z = _wna16_moe_to_op_layout(
-            layer.w2_qweight.data, layer.w2_scales.data,
-            layer.w2_qzeros.data if has_zp else None)
-        layer._w4a8_w13, layer._w4a8_w2 = w13, w2
-        layer._w4a8_w13s, layer._w4a8_w2s = w13_s, w2_s
-        layer._w4a8_w13z, layer._w4a8_w2z = w13_z, w2_z
-        if verbose:
-            print(f"[w4a8_fp8_wmma] WNA16 MoE weights ready (int4 g={layer.group_size} "
-                  f"has_zp={has_zp}) -> gfx950 grouped fp8 MFMA")
-
-    def _patched_apply(self, layer, x, topk_weights, topk_ids, shared_experts=None,
-                       shared_experts_input=None):
-        if not getattr(self, "_w4a8_wna16", False):
-            return _orig_apply(self, layer, x, topk_weights, topk_ids, shared_experts,
-                               shared_experts_input)
-        x2 = x.reshape(-1, x.shape[-1])
-        out = _run_grouped_moe(
-            x2, layer._w4a8_w13, layer._w4a8_w2, layer._w4a8_w13s, layer._w4a8_w2s,
-            layer._w4a8_w13z, layer._w4a8_w2z, topk_weights, topk_ids, layer.activation,
-            layer.global_num_experts, layer.expert_map, layer.apply_router_weight_on_input,
-            _moe_kernel(), out_dtype=x.dtype)
-        return out.reshape(x.shape[:-1] + (out.shape[-1],))
-
-    method_cls.process_weights_after_loading = _patched_process
-    method_cls.apply = _patched_apply

@@ -39,7 +39,7 @@ def test_library_exports_exactly_the_header():
 
 def test_abi_version_and_sizes():
     L = _lib.lib
-    assert L.w4a8_abi_version() == 1
+    assert L.w4a8_abi_version() == 2
     assert L.w4a8_moe_align_sorted_len(256, 256, 16) == O.align_alloc_len(256, 256, 16)
     assert L.w4a8_moe_align_sorted_len(32768, 256, 64) == 48896      # SURVEY C4 P_alloc
     assert L.w4a8_moe_align_sorted_len(8, 256, 8) == 1800            # C2 with block_m 8
@@ -85,8 +85,27 @@ def test_validation_errors_are_reported_without_gpu():
     assert rc == 1 and "group_size" in _err()
     # moe_apply bad dtype
     rc = L.w4a8_moe_apply(1, 7, 4, 256, 128, 8, 2, 128, 1, 1, None, 1, 1, None, 1, 1, None, 0,
-                          1, 1, 1 << 20, None)
+                          0, 1, 1, 1 << 20, None)
     assert rc == 1 and "dtype" in _err()
+    # global expert count without a map
+    rc = L.w4a8_moe_apply(1, 0, 4, 256, 128, 8, 2, 128, 1, 1, None, 1, 1, None, 1, 1, None, 16,
+                          0, 1, 1, 1 << 20, None)
+    assert rc == 1 and "expert_map" in _err()
+    # fragment layout: decode needs a GEMV split for K/128 (5 is not one), prefill K <= 4096
+    rc = L.w4a8_moe_apply_fragments(1, 0, 4, 640, 128, 8, 2, 128, 1, 1, None, 1, 1, None, 1, 1,
+                                    None, 0, 1, 1, 1 << 20, None)
+    assert rc == 1 and "fragment" in _err()
+    rc = L.w4a8_moe_apply_fragments(1, 0, 200, 8192, 128, 8, 2, 128, 1, 1, None, 1, 1, None, 1,
+                                    1, None, 0, 1, 1, 1 << 20, None)
+    assert rc == 1 and "fragment" in _err()
+    # the router covers at most 1024 experts
+    rc = L.w4a8_moe_forward(1, 0, 4, 256, 128, 8, 2, 128, 1, 1, 1, 1, None, 1, 1, None, 0, 1,
+                            2048, 1, 1, 1, 1, 1 << 20, None)
+    assert rc == 1 and "1024" in _err()
+    assert L.w4a8_moe_fragments_supported(2048, 512, 128) == 1     # c2-c4 shape
+    assert L.w4a8_moe_fragments_supported(4096, 1536, 128) == 1    # c5 shape (K/128 = 32, 12)
+    assert L.w4a8_moe_fragments_supported(640, 512, 128) == 0      # K/128 = 5: no GEMV split
+    assert L.w4a8_moe_fragments_supported(2048, 512, 64) == 0      # g64: op layout only
     with pytest.raises(RuntimeError, match="multiple of 8"):
         _lib.check(L.w4a8_act_quant_fp8(1, 4, 12, 1, 1, 0, None), "act_quant")
 
@@ -229,12 +248,59 @@ def test_wna16_hook_with_stand_in_class(monkeypatch):
     m, layer = Method(), Layer()
     m.process_weights_after_loading(layer)
     assert calls["process"] and m._w4a8_wna16
-    assert layer._w4a8_w13.shape == (E, N, K // 8) and layer._w4a8_w13.dtype == torch.int32
-    assert layer._w4a8_w13z.shape == (E, N // 8, K // g)
-    assert layer._w4a8_w13s.dtype == torch.float16
+    rec = layer._w4a8
+    # inter = 8 is no multiple of 128: the fragment kernels do not take it, op-layout views stay
+    assert rec["layout"] == "op"
+    assert rec["w13"].shape == (E, N, K // 8) and rec["w13"].dtype == torch.int32
+    assert rec["w13"].data_ptr() == layer.w13_qweight.data.data_ptr()      # zero-copy view
+    assert rec["z13"].shape == (E, N // 8, K // g)
+    assert rec["s13"].dtype == torch.float16
     # unsupported group size keeps the stock apply
     layer2 = Layer()
     layer2.group_size = 256
     m2 = Method()
     m2.process_weights_after_loading(layer2)
     assert m2.apply(layer2, None, None, None) == "stock"
+
+
+def test_fragments_to_op_layout_inverts_the_repack():
+    r = np.random.default_rng(31)
+    w = r.integers(-2**31, 2**31 - 1, (3, 48, 384 // 8), dtype=np.int64).astype(np.int32)
+    f = O.repack_fragments(w)
+    back = moe_experts._fragments_to_op_layout(torch.from_numpy(f))
+    assert np.array_equal(back.numpy(), w)
+
+
+def _layer_tensors(T=4, E=4, H=256, I=128, k=2, g=128):
+    i32 = torch.int32
+    return dict(
+        x=torch.zeros(T, H, dtype=torch.bfloat16), w13=torch.zeros(E, 2 * I, H // 8, dtype=i32),
+        w2=torch.zeros(E, H, I // 8, dtype=i32),
+        w13_s=torch.zeros(E, 2 * I, H // g, dtype=torch.float16),
+        w2_s=torch.zeros(E, H, I // g, dtype=torch.float16),
+        w13_z=torch.zeros(E, 2 * I // 8, H // g, dtype=i32), w2_z=torch.zeros(E, H // 8, I // g, dtype=i32),
+        topk_weights=torch.zeros(T, k), topk_ids=torch.zeros(T, k, dtype=i32))
+
+
+@pytest.mark.parametrize("bad,match", [
+    (dict(w2=torch.zeros(4, 256, 8, dtype=torch.int32)), "w2 must be"),
+    (dict(w13_s=torch.zeros(4, 256, 3, dtype=torch.float16)), "w13 scales"),
+    (dict(w2_s=torch.zeros(4, 256, 2, dtype=torch.float16)), "w2 scales"),
+    (dict(w13_z=torch.zeros(4, 16, 2, dtype=torch.int32)), "w13 zeros"),
+    (dict(w2_z=torch.zeros(4, 32, 2, dtype=torch.int32)), "w2 zeros"),
+    (dict(topk_ids=torch.zeros(5, 2, dtype=torch.int32)), "topk_ids"),
+    (dict(topk_weights=torch.zeros(4, 3)), "topk_weights"),
+    (dict(expert_map=torch.zeros(8, dtype=torch.int32), global_num_experts=6), "expert_map"),
+    (dict(global_num_experts=8), "pass expert_map"),
+    ({}, "CUDA"),                 # shapes all fine: the device check is last
+])
+def test_layer_args_rejections(bad, match):
+    """Every shape the whole-layer kernels index by is checked on the host (no device read
+    can run past a tensor)."""
+    t = _layer_tensors()
+    extra = {k: bad.pop(k) for k in ("expert_map", "global_num_experts") if k in bad}
+    t.update(bad)
+    with pytest.raises(RuntimeError, match=match):
+        W.moe_apply(t["x"], t["w13"], t["w2"], t["w13_s"], t["w2_s"], t["w13_z"], t["w2_z"],
+                    t["topk_weights"], t["topk_ids"], extra.get("expert_map"),
+                    global_num_experts=extra.get("global_num_experts"))

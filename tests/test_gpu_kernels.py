@@ -240,10 +240,13 @@ def test_gemv_in_kernel_quant_matches_prequant(case):
 
 
 @pytest.mark.parametrize("case", [(64, 8, 256, 256, 2, 16, 128), (128, 8, 512, 512, 2, 64, 128),
-                                  (256, 4, 1024, 2048, 2, 128, 128), (16, 16, 256, 256, 4, 16, 32)])
+                                  (256, 4, 1024, 2048, 2, 128, 128), (16, 16, 256, 256, 4, 16, 32),
+                                  (512, 16, 1024, 2048, 8, 64, 128), (200, 8, 768, 1536, 4, 64, 128)])
 def test_gemm1_silu_fused_bit_exact_to_unfused(case):
     """Fused gemm1+SiLU == gemm1 fp16 store + silu_and_mul, bit for bit
-    (test_moe_experts.py:283-315)."""
+    (test_moe_experts.py:283-315). Shapes with K % 512 == 0, K <= 2048, block_m % 64 == 0
+    run the activation-resident prefill tiles (the whole layer's gemm1), the others the
+    streamed-K and small tiles."""
     T, E, N, K, k, bm, g = case
     x, w, z, sc, ids, _ = make_case(sum(case), T, E, N, K, k, g)
     sti, eid, ntp = O.moe_align(ids, bm, E)

@@ -88,6 +88,99 @@ def test_expert_map_drops_non_local_experts():
     assert maxrel(out.float().cpu().numpy(), ref) <= REL_TOL
 
 
+@pytest.mark.parametrize("T,frag", [(16, False), (16, True), (200, False), (200, True)])
+def test_expert_map_global_ids_beyond_local_count(T, frag):
+    """EP layout: 4 local experts, 8 global ids, experts 4..7 local (as 0..3). Ids >= the
+    local count must be mapped, not dropped (decode and prefill schedules, both layouts)."""
+    cfg = dict(T=T, H=256, E=4, k=3, I=128, g=128, routing="uniform")
+    ws = bench.make_weights(cfg, 410 + T, DEV)
+    g_cfg = dict(cfg, E=8)
+    x, logits = bench.make_inputs(g_cfg, 411 + T, DEV)
+    emap_np = np.array([-1, -1, -1, -1, 0, 1, 2, 3], np.int32)
+    emap = torch.from_numpy(emap_np).to(DEV)
+    w13, w2 = ws["w13"], ws["w2"]
+    if frag:
+        w13, w2 = W.repack_fragments(w13), W.repack_fragments(w2)
+    out, tw, ids = W.moe_forward(x, logits, 3, w13, w2, ws["s13"], ws["s2"], ws["z13"], ws["z2"],
+                                 expert_map=emap)
+    assert int(ids.max()) >= 4 and int(ids.min()) < 4
+    h = {kk: v.cpu().numpy() for kk, v in ws.items()}
+    ref = O.moe_layer(x.float().cpu().numpy(), h["w13"], h["s13"], h["z13"], h["w2"], h["s2"],
+                      h["z2"], tw.cpu().numpy(), ids.cpu().numpy(), 128, round_y_fp16=T > 96,
+                      expert_map=emap_np)
+    assert maxrel(out.float().cpu().numpy(), ref) <= REL_TOL
+    # _run_grouped_moe with global_num_experts = 8 takes the same path
+    out2 = moe_experts._run_grouped_moe(x, w13, w2, ws["s13"], ws["s2"], ws["z13"], ws["z2"], tw,
+                                        ids, "silu", 8, emap, False, "wmma")
+    assert torch.equal(out2, out)
+
+
+@pytest.mark.parametrize("g,T", [(128, 8), (128, 160), (32, 8)])
+def test_e2m1_layer(g, T):
+    """mxfp4 (OCP E2M1 codebook, symmetric) weights through the whole layer
+    (moe_experts.py:1351-1450, tile_config.h:47-71): the matrix-core tiles at g128, the
+    scalar schedule at the mxfp4 block size 32."""
+    cfg = dict(T=T, H=256, E=8, k=2, I=128, g=g, routing="uniform")
+    ws = bench.make_weights(cfg, 420 + g + T, DEV)
+    x, logits = bench.make_inputs(cfg, 421 + g + T, DEV)
+    tw, ids = W.fused_topk(None, logits, 2, True)
+    out = moe_experts._run_grouped_moe(x, ws["w13"], ws["w2"], ws["s13"], ws["s2"], None, None,
+                                       tw, ids, "silu", 8, None, False, "wmma",
+                                       weight_is_e2m1=True)
+    h = {kk: v.cpu().numpy() for kk, v in ws.items()}
+    ref = O.moe_layer(x.float().cpu().numpy(), h["w13"], h["s13"], None, h["w2"], h["s2"], None,
+                      tw.cpu().numpy(), ids.cpu().numpy(), g, round_y_fp16=False, e2m1=True)
+    assert maxrel(out.float().cpu().numpy(), ref) <= REL_TOL
+
+
+@pytest.mark.parametrize("e2m1", [False, True])
+@pytest.mark.parametrize("T", [6, 130])
+def test_per_expert_biases(e2m1, T):
+    """gpt-oss style per-expert biases (moe_experts.py:565-575,654-655): added to gemm1's fp16
+    output before the activation and to gemm2's fp16 rows before the weighted reduce."""
+    cfg = dict(T=T, H=256, E=8, k=2, I=128, g=128, routing="uniform")
+    ws = bench.make_weights(cfg, 430 + T, DEV)
+    x, logits = bench.make_inputs(cfg, 431 + T, DEV)
+    tw, ids = W.fused_topk(None, logits, 2, True)
+    r = np.random.default_rng(432 + T)
+    b1 = (r.standard_normal((8, 256)) * 0.1).astype(np.float16)
+    b2 = (r.standard_normal((8, 256)) * 0.1).astype(np.float16)
+    z13, z2 = (None, None) if e2m1 else (ws["z13"], ws["z2"])
+    out = moe_experts._run_grouped_moe(
+        x, ws["w13"], ws["w2"], ws["s13"], ws["s2"], z13, z2, tw, ids, "silu", 8, None, False,
+        "wmma", weight_is_e2m1=e2m1, w1_bias=torch.from_numpy(b1).to(DEV),
+        w2_bias=torch.from_numpy(b2).to(DEV))
+    h = {kk: v.cpu().numpy() for kk, v in ws.items()}
+    ref = O.moe_layer(x.float().cpu().numpy(), h["w13"], h["s13"], None if e2m1 else h["z13"],
+                      h["w2"], h["s2"], None if e2m1 else h["z2"], tw.cpu().numpy(),
+                      ids.cpu().numpy(), 128, e2m1=e2m1, w1_bias=b1, w2_bias=b2)
+    assert maxrel(out.float().cpu().numpy(), ref) <= REL_TOL
+
+
+@pytest.mark.parametrize("T,frag", [(160, False), (300, True), (1024, True)])
+def test_prefill_layer_equals_op_composition(T, frag):
+    """The whole-layer prefill tiles (fused gemm1+SiLU, gemm2 quantising its own rows, row
+    reduce) against the op-by-op composition of the reference's ops (gemm1, silu_and_mul,
+    gemm2, gather-reduce; moe_experts.py:587-665). The fused SiLU is silu_mul_h, the
+    unfused kernel's own function (test_moe_experts.py:283-315 property)."""
+    cfg = dict(bench.CONFIGS["c4"])
+    cfg["T"] = T
+    ws = bench.make_weights(cfg, 440 + T, DEV)
+    x, logits = bench.make_inputs(cfg, 441 + T, DEV)
+    tw, ids = W.fused_topk(None, logits, cfg["k"], True)
+    w13, w2 = ws["w13"], ws["w2"]
+    if frag:
+        w13, w2 = W.repack_fragments(w13), W.repack_fragments(w2)
+    fused = W.moe_apply(x, w13, w2, ws["s13"], ws["s2"], ws["z13"], ws["z2"], tw, ids)
+    unfused = moe_experts._run_unfused(
+        x.to(torch.float16), ws["w13"], ws["w2"], ws["s13"], ws["s2"], ws["z13"], ws["z2"],
+        tw.reshape(-1).contiguous(), ids, cfg["k"], cfg["E"], None, "wmma", False, None, None,
+        64).to(x.dtype)
+    same = (fused == unfused).float().mean().item()
+    print(f"  identical elements: {same:.6f}")
+    assert torch.equal(fused, unfused)
+
+
 @pytest.mark.parametrize("name", ["c2", "c3", "c4", "c5"])
 def test_baseline_configs_sampled_tokens(name):
     """Full-size BASELINE.json layers; the oracle checks 3 tokens (first, middle, last)."""
