@@ -6,9 +6,11 @@ A step is: router softmax/top-k on the logits, then the whole expert path
 on one batch of synthetic tokens whose weights are already resident in HBM. Weights
 rotate over several independent sets so the 256 MB Infinity Cache cannot hold them.
 
-Prints ONE JSON line: MoE-layer tokens/s, the dominant kernel's roofline fraction
-(HIP-event timed on the kernels' own stream) and the CPU oracle timed on a bounded
-sample of the same workload. ``--gpus N`` with N > 1 exits: this build runs on one GPU.
+Prints ONE JSON line: MoE-layer tokens/s (HIP-graph replays of the step), the dominant
+kernel's roofline fraction (kernel-exact HIP events on the kernels' own stream) beside the
+layer's own fraction, and the torch-CPU port of the reference layer timed on a bounded
+sample of the same workload on the host cores. ``--gpus N`` with N > 1 exits: this build
+runs on one GPU.
 """
 from __future__ import annotations
 
@@ -114,44 +116,82 @@ STAGES = ["align", "act_quant_x", "reserved", "gemm1_silu", "act_quant_h", "gemm
           "reduce_cast"]
 
 
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
 def cpu_baseline(cfg, ws, x, tw, ids, out_gpu, budget_s):
-    """Time the numpy oracle on the first S tokens (S grows until ~budget_s of work) and
-    check the GPU output on those tokens."""
+    """The torch-CPU port of the reference layer (oracle/cpu_port.py, vectorised per expert)
+    on all host cores: the sample S (the first S tokens) doubles until one pass takes about a
+    fifth of the budget, then three timed passes give the median. The same pass checks the
+    GPU output on those tokens."""
     import numpy as np
     import torch
     import oracle as O
-    try:
-        from threadpoolctl import threadpool_info
-        cores = max([i.get("num_threads", 1) for i in threadpool_info()] + [1])
-    except Exception:  # noqa: BLE001
-        cores = 1
-    host = {k: (None if v is None else v.cpu().numpy()) for k, v in ws.items()}
-    for k in ("w13", "w2"):   # the oracle reads the op layout
-        if host[k].ndim == 5:
-            host[k] = O.unrepack_fragments(host[k])
-    xf = x.float().cpu().numpy()
-    twn, idn = tw.cpu().numpy(), ids.cpu().numpy()
-    T = xf.shape[0]
-    S, spent, samples = 1, 0.0, []
-    t_start = time.perf_counter()
-    while True:
+    from oracle import cpu_port
+    # every core the process may use (its affinity set), within the host's thread budget
+    # for one GPU (OMP_NUM_THREADS on the GPU boxes)
+    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+        cores = min(cores, int(os.environ["OMP_NUM_THREADS"]))
+    cores = max(1, cores)
+    torch.set_num_threads(cores)
+    host = {k: (None if v is None else v.cpu()) for k, v in ws.items()}
+    for k in ("w13", "w2"):   # the port reads the op layout
+        if host[k].dim() == 5:
+            host[k] = torch.from_numpy(O.unrepack_fragments(host[k].numpy()))
+    xc, twc, idc = x.float().cpu(), tw.cpu(), ids.cpu()
+    T = xc.shape[0]
+    round_y = T > 96
+
+    def run(S):
         t0 = time.perf_counter()
-        ref = O.moe_layer(xf[:S], host["w13"], host["s13"], host["z13"], host["w2"],
-                          host["s2"], host["z2"], twn[:S], idn[:S], cfg["g"],
-                          round_y_fp16=False)
-        dt = time.perf_counter() - t0
-        samples.append((S, dt, ref))
-        spent = time.perf_counter() - t_start
-        if S >= T or spent + 2.2 * dt > budget_s:
+        ref = cpu_port.moe_layer(xc[:S], host["w13"], host["s13"], host["z13"], host["w2"],
+                                 host["s2"], host["z2"], twc[:S], idc[:S], cfg["g"],
+                                 round_y_fp16=round_y)
+        return time.perf_counter() - t0, ref
+
+    S, spent = min(T, 8), 0.0
+    while True:
+        dt, ref = run(S)
+        spent += dt
+        if S >= T or dt * 5 > budget_s or spent + 2 * dt > budget_s / 2:
             break
         S = min(T, S * 2)
-    S, dt, ref = samples[-1]
+    times = [run(S)[0] for _ in range(3)]        # the sizing passes warmed the caches
+    med = sorted(times)[1]
     got = out_gpu[:S].float().cpu().numpy()
-    maxrel = float(np.abs(got - ref).max() / max(np.abs(ref).max(), 1e-30))
-    return dict(value=S / dt, unit="tokens/s", cores=int(cores), kind="port",
-                sample=f"first {S} of {T} tokens through the numpy oracle (oracle.moe_layer), "
-                       f"{dt:.2f} s; BLAS threads={cores}; host={platform.processor() or platform.machine()}"
-                       f" cpu_count={os.cpu_count()}"), maxrel, S
+    refn = ref.numpy()
+    maxrel = float(np.abs(got - refn).max() / max(np.abs(refn).max(), 1e-30))
+    return dict(value=S / med, unit="tokens/s", cores=int(cores), kind="port",
+                sample=f"first {S} of {T} tokens through the torch-CPU port of the reference "
+                       f"layer (oracle/cpu_port.py, float64 group sums, per-expert batches); "
+                       f"median of 3 passes {med:.3f} s ({', '.join(f'{t:.3f}' for t in times)}); "
+                       f"torch threads={torch.get_num_threads()}; cpu='{cpu_model()}' "
+                       f"os.cpu_count={os.cpu_count()}"), maxrel, S
+
+
+def gemm1_kernel_name(cfg, decode, layout):
+    frag = "true" if layout == "fragments" else "false"
+    H = cfg["H"]
+    if decode and layout == "fragments":
+        # persistent decode kernel (decode_gemv.hip dec_split): groups per wave, split-K
+        split = {1: "1, 1", 2: "2, 1", 3: "3, 1", 4: "4, 1", 8: "2, 4", 12: "3, 4", 16: "4, 4",
+                 32: "8, 4"}[H // 128]
+        return f"decode_gemv_kernel<(w4a8::Epi)1, {split}, false>"
+    if decode:
+        split = {1: "1, 1", 2: "2, 1", 3: "3, 1", 4: "4, 1", 8: "4, 2", 12: "3, 4", 16: "4, 4",
+                 32: "8, 4"}[H // 128]
+        return f"grouped_gemv_kernel<kSiluHalf, {split}, false, {frag}>"
+    if H % 512 == 0 and H <= 2048:
+        return f"prefill_ares_kernel<kSiluHalf, {frag}>"
+    return f"prefill_mfma_kernel<kSiluHalf, 4, {frag}>"
 
 
 def main():
@@ -163,7 +203,7 @@ def main():
     ap.add_argument("--rotate", type=int, default=0, help="weight sets (0 = auto, >= 1 GiB)")
     ap.add_argument("--no-graph", action="store_true", help="time eager launches")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-budget", type=float, default=15.0)
+    ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--layout", choices=["fragments", "op"], default="fragments",
                     help="weights as stored after loading: the gfx950 fragment layout "
@@ -230,7 +270,7 @@ def main():
         torch.cuda.synchronize()
 
     # ---- timed region: exactly K steps ----
-    ev = HipEvents(2 + 8 + 2)
+    ev = HipEvents(2 + 12)
     stream = torch.cuda.current_stream().cuda_stream
     hip = ev.hip
     hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
@@ -248,25 +288,25 @@ def main():
     total_ms = ev.elapsed(0, 1)
     ms_per_step = total_ms / args.steps
 
-    # ---- per-stage timing (eager, events inside the C ABI on the kernels' stream) ----
-    # The 9th event is recorded right after the align stage's event with no work between
-    # them: that empty bracket measures the marker latency (~5 us) every stage time
-    # includes, and kernel durations subtract it.
-    stage_ev = (ctypes.c_void_p * 9)(*[e.value for e in ev.ev[2:11]])
-    _lib.check(_lib.lib.w4a8_moe_apply_set_stage_events(stage_ev, 9), "stage events")
+    # ---- per-stage and per-kernel timing (eager layer calls; events recorded by the C ABI
+    # on the kernels' own stream). events[8..11] are stamped by hipExtLaunchKernel at the
+    # start and end of the gemm1 and gemm2 kernels themselves: their interval is the
+    # kernel's duration, the figure a rocprofv3 kernel trace reports for it. ----
+    stage_ev = (ctypes.c_void_p * 12)(*[e.value for e in ev.ev[2:14]])
+    _lib.check(_lib.lib.w4a8_moe_apply_set_stage_events(stage_ev, 12), "stage events")
     n_stage = max(10, min(50, args.steps))
     acc = [0.0] * 7
-    calib = 0.0
+    k1 = k2 = 0.0
     for i in range(n_stage):
         step(i)
         torch.cuda.synchronize()
-        calib += ev.elapsed(3, 10)
         for j in range(7):
-            acc[j] += ev.elapsed(10 if j == 1 else 2 + j, 3 + j)
+            acc[j] += ev.elapsed(2 + j, 3 + j)
+        k1 += ev.elapsed(10, 11)
+        k2 += ev.elapsed(12, 13)
     _lib.check(_lib.lib.w4a8_moe_apply_set_stage_events(None, 0), "stage events off")
-    calib_ms = calib / n_stage
     stage_ms = {STAGES[j]: acc[j] / n_stage for j in range(7)}
-    kernel_ms = {k_: max(v - calib_ms, 0.0) for k_, v in stage_ms.items()}
+    g1_ms, g2_ms = k1 / n_stage, k2 / n_stage
 
     # ---- algorithmic work ----
     distinct = int(torch.unique(ids0).numel())
@@ -274,26 +314,46 @@ def main():
     layer_flops = 2 * T * k * (H * 2 * I + I * H)
     decode = T <= 96
     g1_bytes = distinct * b13 + T * H + T * k * I * 2        # weights + fp8 x in + fp16 h out
+    g2_bytes = distinct * b2 + T * k * I * 2 + T * k * H * (4 if decode else 2)
     g1_flops = 2 * T * k * H * 2 * I
-    g1_ms = kernel_ms["gemm1_silu"]
+    g2_flops = 2 * T * k * I * H
+    layer_s = ms_per_step * 1e-3
+    kname = gemm1_kernel_name(cfg, decode, args.layout)
     if decode:
         achieved = g1_bytes / (g1_ms * 1e-3) / 1e9
         roof = dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
-                    frac=round(achieved / HBM_PEAK_GBS, 4), traffic=None,
-                    kernel="grouped_gemv_kernel<kSiluHalf> (gemm1+SiLU)",
+                    frac=round(achieved / HBM_PEAK_GBS, 4), traffic=None, kernel=kname,
                     algorithmic_bytes=g1_bytes, avg_ms=round(g1_ms, 5))
+        lay_ach = layer_bytes / layer_s / 1e9
+        roof["layer"] = dict(bound="hbm", achieved=round(lay_ach, 1), unit="GB/s",
+                             frac=round(lay_ach / HBM_PEAK_GBS, 4),
+                             algorithmic_bytes=layer_bytes, ms=round(ms_per_step, 5),
+                             target_frac=0.70)
+        roof["gemm2"] = dict(achieved=round(g2_bytes / (g2_ms * 1e-3) / 1e9, 1), unit="GB/s",
+                             frac=round(g2_bytes / (g2_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                             algorithmic_bytes=g2_bytes, avg_ms=round(g2_ms, 5))
     else:
         achieved = g1_flops / (g1_ms * 1e-3) / 1e12
         roof = dict(bound="mfma", achieved=round(achieved, 1), peak=FP8_PEAK_TFLOPS,
                     unit="TFLOP/s", frac=round(achieved / FP8_PEAK_TFLOPS, 4), traffic=None,
-                    kernel="prefill_ares_kernel<kSiluHalf> (gemm1+SiLU)",
-                    algorithmic_flops=g1_flops, avg_ms=round(g1_ms, 5))
-    # HBM bytes per launch of that kernel, measured with rocprofv3 --pmc on this workload and
-    # weight layout (profiles/roofline_traffic.json); null for other configurations
+                    kernel=kname, algorithmic_flops=g1_flops, avg_ms=round(g1_ms, 5))
+        lay_ach = layer_flops / layer_s / 1e12
+        roof["layer"] = dict(bound="mfma", achieved=round(lay_ach, 1), unit="TFLOP/s",
+                             frac=round(lay_ach / FP8_PEAK_TFLOPS, 4), flops=layer_flops,
+                             ms=round(ms_per_step, 5), target_frac=0.50,
+                             hbm_frac=round(layer_bytes / layer_s / 1e9 / HBM_PEAK_GBS, 4))
+        roof["gemm2"] = dict(achieved=round(g2_flops / (g2_ms * 1e-3) / 1e12, 1),
+                             unit="TFLOP/s",
+                             frac=round(g2_flops / (g2_ms * 1e-3) / 1e12 / FP8_PEAK_TFLOPS, 4),
+                             algorithmic_flops=g2_flops, avg_ms=round(g2_ms, 5))
+    roof["timing"] = (f"kernel-exact HIP events (hipExtLaunchKernel start/stop of the kernel "
+                      f"itself) over {n_stage} eager layer calls on the launch stream")
+    # HBM bytes per launch of that kernel, from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs
+    # of this workload and weight layout (profiles/roofline_traffic.json); null otherwise
     tr_file = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "roofline_traffic.json")
-    if os.path.exists(tr_file) and args.layout == "fragments":
-        tr = json.load(open(tr_file)).get(args.config)
-        if tr is not None:
+    if os.path.exists(tr_file):
+        tr = json.load(open(tr_file)).get(f"{args.config}/{args.layout}")
+        if tr is not None and tr.get("kernel") == kname:
             roof["traffic"] = tr["traffic_bytes"]
             roof["traffic_source"] = "profiles/roofline_traffic.json (" + tr["kernel"] + ")"
     layer_s = ms_per_step * 1e-3
@@ -325,8 +385,8 @@ def main():
                   "hbm_frac": round(layer_bytes / layer_s / 1e9 / HBM_PEAK_GBS, 4),
                   "flops": layer_flops,
                   "mfma_frac": round(layer_flops / layer_s / 1e12 / FP8_PEAK_TFLOPS, 4),
-                  "stage_ms": {k_: round(v, 5) for k_, v in stage_ms.items()},
-                  "event_overhead_ms": round(calib_ms, 5),
+                  "stage_ms_eager": {k_: round(v, 5) for k_, v in stage_ms.items()},
+                  "kernel_ms": {"gemm1": round(g1_ms, 5), "gemm2": round(g2_ms, 5)},
                   "wall_ms_timed_region": round(wall_ms, 3)},
     }
     if not args.no_cpu_baseline:
