@@ -7,17 +7,19 @@
 // bit-identical to the grouped GEMV of grouped_gemm.hip (same raw-nibble MFMA operands,
 // zero-point term, scale fold order and split-K sum order). The schedule is this file's own:
 //
-//   * every work-group builds, in LDS, the list of touched experts and each one's slots from
-//     topk_ids (the order of slots inside an expert does not matter: every output row
-//     depends on its own activation row only);
+//   * one four-wave work-group per CU (one wave per SIMD, so a wave holds four weight chunks
+//     in registers); every work-group builds, in LDS, the list of touched experts and each
+//     one's slots from topk_ids (the order of slots inside an expert does not matter: every
+//     output row depends on its own activation row only);
 //   * the layer's work is a list of units (touched expert, column unit: 16 gate + 16 up
-//     columns for gemm1+SiLU, 32 columns for gemm2), split exactly evenly over a persistent
-//     grid of teams (a team is one wave, or the whole work-group when the K groups are split
-//     over its 4 waves), so every CU streams the same number of weight bytes in one round;
-//   * a team walks its contiguous unit range expert by expert; per expert (and 16 rows at a
-//     time) it loads the activation rows (gemm1: x rows of the slots' tokens, fp16 or bf16;
-//     gemm2: the slots' h rows) and quantises them in registers, bit-identical to
-//     act_quant_kernel, then streams the units' weights two chunks ahead of the MFMAs;
+//     columns for gemm1+SiLU, 32 columns for gemm2), streamed once per 16-row pass over the
+//     expert's slots; it is split over teams (a team is one wave, or the whole work-group
+//     when the K groups are split over its 4 waves) in contiguous ranges of equal work, a
+//     pass start (row load and quantisation) counting kDecPassCost units;
+//   * a team walks its range expert by expert and pass by pass; at a pass start it loads the
+//     activation rows (gemm1: x rows of the slots' tokens, fp16 or bf16; gemm2: the slots'
+//     h rows) and quantises them in registers, bit-identical to act_quant_kernel; the weight
+//     loads run three or four chunks ahead of the MFMAs across expert and pass boundaries;
 //   * outputs are per slot: gemm1 writes h (numel, I) fp16 after SiLU*mul, gemm2 writes
 //     y (numel, H) fp32, which the slot reduce sums in j order.
 #include <algorithm>
@@ -31,7 +33,8 @@ namespace {
 constexpr int kDecThreads = 256;
 constexpr int kDecMaxSlots = 1024;      // T * top_k
 constexpr int kDecMaxExperts = 1024;
-constexpr int kDecBatch = 8;            // units per LDS round of split-K partial sums
+constexpr int kDecRing = 3;             // weight chunks in flight per wave (a ring slot each)
+constexpr int kDecPassCost = 2;         // partition cost of a pass start (row load), in units
 constexpr uint32_t kDecOnes = 0x38383838u;   // four e4m3 bytes of 1.0
 using u16x2 = unsigned short __attribute__((ext_vector_type(2)));
 
@@ -55,11 +58,15 @@ struct DecodeLists {
     int16_t first[kDecMaxExperts + 1];     // its slots are slot[first[r] .. first[r + 1])
     int16_t slot[kDecMaxSlots];
     int cnt[kDecMaxExperts];
-    int wtot[2][kDecThreads / 64];
+    int cost[kDecMaxExperts + 1];          // work before touched expert r (partition units)
+    int wtot[3][kDecThreads / 64];
 };
 
-// Touched experts and their slot lists (the align's grouping, without padding) in LDS.
-__device__ void build_lists(const DecodeParams& p, DecodeLists& L) {
+// Touched experts and their slot lists (the align's grouping, without padding) in LDS, and
+// the work of each touched expert for the partition: every 16-row pass over the expert's
+// upe column units streams their weights once and starts with an activation-row load,
+// charged as kDecPassCost units.
+__device__ void build_lists(const DecodeParams& p, int upe, DecodeLists& L) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     constexpr int kPer = kDecMaxSlots / kDecThreads;
     for (int e = tid; e < p.E; e += kDecThreads) L.cnt[e] = 0;
@@ -76,33 +83,37 @@ __device__ void build_lists(const DecodeParams& p, DecodeLists& L) {
     for (int i = 0; i < kPer; ++i)
         if (es[i] >= 0) atomicAdd(&L.cnt[es[i]], 1);
     __syncthreads();
-    // exclusive scans of (slots, touched) over experts; thread t owns experts 4t .. 4t + 3
-    int c[4], tot = 0, tch = 0;
+    // exclusive scans of (slots, touched, work) over experts; thread t owns experts 4t .. 4t + 3
+    int c[4], tot = 0, tch = 0, twk = 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int e = 4 * tid + j;
         c[j] = e < p.E ? L.cnt[e] : 0;
         tot += c[j];
         tch += c[j] > 0 ? 1 : 0;
+        twk += ((c[j] + 15) >> 4) * (upe + kDecPassCost);
     }
-    int it = tot, ic = tch;
+    int it = tot, ic = tch, iw = twk;
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
-        const int y = __shfl_up(it, o, 64), z = __shfl_up(ic, o, 64);
+        const int y = __shfl_up(it, o, 64), z = __shfl_up(ic, o, 64), v = __shfl_up(iw, o, 64);
         if (lane >= o) {
             it += y;
             ic += z;
+            iw += v;
         }
     }
     if (lane == 63) {
         L.wtot[0][wave] = it;
         L.wtot[1][wave] = ic;
+        L.wtot[2][wave] = iw;
     }
     __syncthreads();
-    int off = it - tot, r = ic - tch;
+    int off = it - tot, r = ic - tch, wk = iw - twk;
     for (int w = 0; w < wave; ++w) {
         off += L.wtot[0][w];
         r += L.wtot[1][w];
+        wk += L.wtot[2][w];
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -110,6 +121,8 @@ __device__ void build_lists(const DecodeParams& p, DecodeLists& L) {
         if (c[j] > 0) {
             L.expert[r] = (int16_t)e;
             L.first[r] = (int16_t)off;
+            L.cost[r] = wk;
+            wk += ((c[j] + 15) >> 4) * (upe + kDecPassCost);
             ++r;
         }
         if (e < p.E) L.cnt[e] = off;     // becomes the fill cursor of expert e
@@ -118,12 +131,31 @@ __device__ void build_lists(const DecodeParams& p, DecodeLists& L) {
     if (tid == kDecThreads - 1) {
         L.n_touched = r;
         L.first[r] = (int16_t)off;
+        L.cost[r] = wk;
     }
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < kPer; ++i)
         if (es[i] >= 0) L.slot[atomicAdd(&L.cnt[es[i]], 1)] = (int16_t)(tid + kDecThreads * i);
     __syncthreads();
+}
+
+// First unit whose work start is at or past X: the work start of unit u of touched expert r
+// is cost[r] + np (kDecPassCost + u - r upe), np = its passes. Wave-wide 64-ary search.
+__device__ int unit_at_cost(const DecodeLists& L, int n_t, int upe, int X) {
+    const int lane = threadIdx.x & 63;
+    const int step = (n_t + 64) / 64;       // candidates cost[0], cost[step], ... cover [0, n_t]
+    int cand = lane * step;
+    uint64_t m = __ballot(cand <= n_t && L.cost[cand] <= X);    // bit 0: cost[0] = 0 <= X
+    const int base = (63 - __clzll(m)) * step;
+    cand = base + lane;
+    m = __ballot(lane < step && cand <= n_t && L.cost[cand] <= X);
+    const int r = base + 63 - __clzll(m);    // largest r with cost[r] <= X
+    if (r >= n_t) return n_t * upe;
+    const int np = ((int)L.first[r + 1] - (int)L.first[r] + 15) >> 4;
+    const int d = X - L.cost[r] - np * kDecPassCost;
+    const int k = d <= 0 ? 0 : (d + np - 1) / np;
+    return r * upe + min(k, upe);
 }
 
 template <Epi EPI, int GPW, int KSPLIT>
@@ -135,20 +167,27 @@ struct DecCfg {
     static constexpr int GC = GPW < 4 ? GPW : 4;  // groups per chunk
     static constexpr int NB = GPW / GC;           // chunks per unit
     static constexpr int TEAMS = 4 / KSPLIT;      // teams per work-group
-    static constexpr int LDS_BYTES = KSPLIT > 1 ? KSPLIT * kDecBatch * FR * 64 * 16 : 0;
     static_assert(KSPLIT == 1 || KSPLIT == 4, "a team is one wave or the whole work-group");
     static_assert(GPW % GC == 0 && (NB == 1 || NB == 2), "unsupported groups per wave");
+    // ring slots: a multiple of NB, so a slot's group batch is fixed
+    static constexpr int D = NB == 1 ? kDecRing : 4;
+    static_assert(D % NB == 0 && D >= 3 && D <= 4, "ring of three or four slots");
+    // split-K partials of a batch of up to D units (one per ring slot), double-buffered:
+    // [batch parity][slot][wave][FR][lane]
+    static constexpr int LDS_BYTES = KSPLIT > 1 ? 2 * D * KSPLIT * FR * 64 * 16 : 0;
 };
 
+// GC fp16 scales, two per word (group u in the low half of word u / 2 when u is even)
 template <int GC>
-__device__ __forceinline__ void dec_load_scales(const __half* ptr, uint32_t (&s)[GC]) {
+__device__ __forceinline__ void dec_load_scales(const __half* ptr, uint32_t (&s)[(GC + 1) / 2]) {
     const uint16_t* h = reinterpret_cast<const uint16_t*>(ptr);
     if constexpr (GC == 4) {
         const uint2 v = *reinterpret_cast<const uint2*>(h);
-        s[0] = v.x & 0xFFFFu; s[1] = v.x >> 16; s[2] = v.y & 0xFFFFu; s[3] = v.y >> 16;
+        s[0] = v.x; s[1] = v.y;
     } else {
 #pragma unroll
-        for (int u = 0; u < GC; ++u) s[u] = h[u];
+        for (int u = 0; u < GC; u += 2)
+            s[u / 2] = (uint32_t)h[u] | (u + 1 < GC ? (uint32_t)h[u + 1] << 16 : 0u);
     }
 }
 template <int GC>
@@ -171,17 +210,32 @@ __device__ __forceinline__ float dec_act_f32(uint32_t bits) {
     return __half2float(__ushort_as_half(static_cast<unsigned short>(bits)));
 }
 
+// Position in a team's work: touched expert r, pass rows [m0, m0 + 16), unit u, chunk b.
+struct DecCursor {
+    int r, e, m0, u, b;
+};
+
 template <Epi EPI, int GPW, int KSPLIT, bool ABF16>
-__global__ void __launch_bounds__(kDecThreads, 2) decode_gemv_kernel(DecodeParams p) {
+__global__ void __launch_bounds__(kDecThreads, 1) decode_gemv_kernel(DecodeParams p) {
     using C = DecCfg<EPI, GPW, KSPLIT>;
     __shared__ DecodeLists L;
     __shared__ float s_amax[4][16];
-    __shared__ int s_oslot[4][16];
-    __shared__ float s_oasc[4][16];
     extern __shared__ __attribute__((aligned(16))) uint8_t s_dyn[];
-    v4f* s_part = reinterpret_cast<v4f*>(s_dyn);      // KSPLIT > 1: [wave][unit][FR][lane]
+    v4f* s_part = reinterpret_cast<v4f*>(s_dyn);
 
-    build_lists(p, L);
+    const int ncols = C::kSilu ? p.N / 2 : p.N;
+    const int upe = ncols / (16 * C::CT);                 // units per expert
+    // Warm this XCD's L2 with the activation rows (one 128-byte line per lane; work-group b
+    // runs on XCD b % 8): they are cold (h was just written on other XCDs) and the row loads
+    // of a pass start are on the critical path. The value is only kept alive, never used.
+    uint32_t warm;
+    {
+        const int nrows = p.a_per_token ? p.numel / p.top_k : p.numel;
+        const int lines = (int)(((int64_t)nrows * p.K * 2 + 127) / 128);
+        const int idx = ((int)(blockIdx.x / 8) * 4 + (int)(threadIdx.x >> 6)) * 64 + (int)(threadIdx.x & 63);
+        warm = lines > 0 ? reinterpret_cast<const uint32_t*>(p.a)[(int64_t)min(idx, lines - 1) * 32] : 0u;
+    }
+    build_lists(p, upe, L);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -190,254 +244,329 @@ __global__ void __launch_bounds__(kDecThreads, 2) decode_gemv_kernel(DecodeParam
     const int c16 = lane & 15;
     const int team = wave / KSPLIT;
     const int g0 = (wave % KSPLIT) * GPW;
-    const int ncols = C::kSilu ? p.N / 2 : p.N;
-    const int upe = ncols / (16 * C::CT);                 // units per expert
-    const int U = L.n_touched * upe;
+    const int n_t = L.n_touched;
     const int nteams = (int)gridDim.x * C::TEAMS;
     const int tm = (int)blockIdx.x * C::TEAMS + team;
-    const int ua = (int)((int64_t)U * tm / nteams);
-    const int ub = (int)((int64_t)U * (tm + 1) / nteams);
+    // team tm starts at work floor(W tm / nteams), in 32-bit arithmetic (W < 2^25)
+    const int work = L.cost[n_t];
+    const int wq = work / nteams, wr = work % nteams;
+    auto work_at = [&](int t) { return wq * t + wr * t / nteams; };
+    const int ua = __builtin_amdgcn_readfirstlane(unit_at_cost(L, n_t, upe, work_at(tm)));
+    const int ub = __builtin_amdgcn_readfirstlane(unit_at_cost(L, n_t, upe, work_at(tm + 1)));
+    if (ua >= ub) return;      // team-uniform; a K-split team is the whole work-group
 
-    uint4 wv[2][C::GC * C::FR];
-    uint32_t sw[2][C::FR][C::GC];
-    int32_t zw[2][C::FR][C::GC];
-    using B0 = std::integral_constant<int, 0>;
-    using B1 = std::integral_constant<int, 1>;
+    // the team's work in order: touched experts r, 16-row passes over each expert's slots,
+    // the units of the team's range inside the expert, NB chunks per unit
+    auto seg_lo = [&](int r) __attribute__((always_inline)) { return max(ua, r * upe); };
+    auto seg_hi = [&](int r) __attribute__((always_inline)) { return min(ub, (r + 1) * upe); };
+    // true: c entered a new pass
+    auto advance = [&](DecCursor& c) __attribute__((always_inline)) -> bool {
+        if (c.u >= ub) return false;
+        if (++c.b < C::NB) return false;
+        c.b = 0;
+        if (++c.u < seg_hi(c.r)) return false;
+        c.m0 += 16;
+        if (c.m0 >= (int)L.first[c.r + 1] - (int)L.first[c.r]) {
+            ++c.r;
+            c.m0 = 0;
+            c.e = c.r < n_t ? (int)L.expert[c.r] : 0;
+        }
+        c.u = seg_lo(c.r);
+        return true;
+    };
 
-    for (int u = ua; u < ub;) {                           // one expert segment per step
-        const int r = u / upe;
-        const int ue = min(ub, (r + 1) * upe);
-        const int e = L.expert[r];
-        const int s0 = L.first[r];
-        const int cnt = L.first[r + 1] - s0;
-        const int t0 = (u - r * upe) * C::CT;             // first column tile of the segment
-        const int nunits = ue - u;
-        const int nch = nunits * C::NB;
-        const int32_t* we = p.w + (int64_t)e * p.N * (p.K / 8);
-        const __half* se = p.scales + (int64_t)e * p.N * p.G;
-        const int32_t* ze = p.zeros ? p.zeros + (int64_t)e * (p.N / 8) * p.G : nullptr;
+    uint4 wv[C::D][C::GC * C::FR];
+    uint32_t sw[C::D][C::FR][(C::GC + 1) / 2];
+    int32_t zw[C::D][C::FR][C::GC];
+    uint4 raw[GPW][4];
+    v8i af[GPW];
+    v4f sa[GPW];   // 2^-9 * group sums of rows 4q .. 4q + 3 (zero-point term)
+    v4f run[C::FR];
+    // output rows of the pass for this lane: rows 4q .. 4q + 3 (one wave per row of the
+    // four with a K split); pad rows store to the last real row's slot the value computed
+    // for it (their activations repeat that row, so the value is the same)
+    constexpr int NRO = KSPLIT > 1 ? 1 : 4;
+    int osl[NRO];
+    float oasc[NRO];
 
-        // weight row of fragment f, column cc of chunk c (its unit's tiles)
-        auto row_of = [&](int c, int f, int cc) -> int {
-            const int col = (t0 + (c / C::NB) * C::CT + f % C::CT) * 16 + cc;
-            return (C::kSilu && f >= C::CT) ? col + ncols : col;
-        };
-        // chunk c: groups g0 + (c % NB) * GC .. + GC - 1 of the unit's FR fragments; chunks
-        // past the end reload the expert's first 16 bytes (unconditional issues keep the
-        // compiler's wait counts exact)
-        auto issue = [&](int c, auto bufc) {
-            constexpr int b = decltype(bufc)::value;
-            const bool live = c < nch;
-            const int g = g0 + (live ? (c % C::NB) * C::GC : 0);
+    // weight row of fragment f, column cc of unit column ucol
+    auto row_of = [&](int ucol, int f, int cc) __attribute__((always_inline)) -> int {
+        const int col = (ucol * C::CT + f % C::CT) * 16 + cc;
+        return (C::kSilu && f >= C::CT) ? col + ncols : col;
+    };
+    // chunk at cursor c: groups g0 + b GC .. + GC - 1 of the unit's FR fragments; past the
+    // team's end it reloads expert 0's first bytes (unconditional issues keep the compiler's
+    // wait counts exact)
+    auto issue = [&](const DecCursor& c, auto slot) __attribute__((always_inline)) {
+        constexpr int b = decltype(slot)::value;
+        const bool live = c.u < ub;
+        const int g = g0 + (live ? c.b * C::GC : 0);
+        const int ucol = live ? c.u - c.r * upe : 0;
+        const int64_t e = live ? c.e : 0;
+        const int32_t* we = p.w + e * p.N * (p.K / 8);
+        const __half* se = p.scales + e * p.N * p.G;
+        // symmetric weights read (and ignore) the scale words in place of zero points: one
+        // address computation, no branch (branches here make the compiler's waits conservative)
+        const int32_t* zb = p.zeros ? p.zeros : reinterpret_cast<const int32_t*>(p.scales);
+        const int64_t zstride = p.zeros ? (int64_t)p.G : 0;
+        const int32_t* ze = zb + (p.zeros ? e * (p.N / 8) * p.G : 0);
 #pragma unroll
-            for (int f = 0; f < C::FR; ++f) {
-                const int n = live ? row_of(c, f, c16) : 0;
-                const int32_t* wr = we + (live ? ((int64_t)(n >> 4) * p.G + g) * 256 + lane * 4 : 0);
+        for (int f = 0; f < C::FR; ++f) {
+            const int n = row_of(ucol, f, c16);
+            const int32_t* wr = we + ((int64_t)(n >> 4) * p.G + g) * 256 + lane * 4;
 #pragma unroll
-                for (int uu = 0; uu < C::GC; ++uu)
-                    wv[b][uu * C::FR + f] = load_stream16(wr + (live ? uu * 256 : 0));
-                dec_load_scales<C::GC>(se + (int64_t)n * p.G + g, sw[b][f]);
-                dec_load_zeros<C::GC>(ze ? ze + (int64_t)(n >> 3) * p.G + g
-                                         : reinterpret_cast<const int32_t*>(p.scales), zw[b][f]);
+            for (int uu = 0; uu < C::GC; ++uu) wv[b][uu * C::FR + f] = load_stream16(wr + uu * 256);
+            dec_load_scales<C::GC>(se + (int64_t)n * p.G + g, sw[b][f]);
+            dec_load_zeros<C::GC>(ze + (n >> 3) * zstride + (p.zeros ? g : 0), zw[b][f]);
+        }
+    };
+
+    // activation rows of pass c (pad rows repeat the last real row): lane (q, c16) holds k
+    // in [128 g + 32 q, +32) of row c16
+    auto load_rows = [&](const DecCursor& c) __attribute__((always_inline)) {
+        const int s0 = (int)L.first[c.r] + c.m0;
+        const int mreal = min(16, (int)L.first[c.r + 1] - s0);
+        const int my_slot = L.slot[s0 + min(c16, mreal - 1)];
+        const int arow = p.a_per_token ? my_slot / p.top_k : my_slot;
+        const uint16_t* xr = reinterpret_cast<const uint16_t*>(p.a) + (int64_t)arow * p.K + q * 32;
+#pragma unroll
+        for (int g = 0; g < GPW; ++g)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                raw[g][i] = reinterpret_cast<const uint4*>(xr + (g0 + g) * kGroup)[i];
+    };
+    // quantise the pass's rows, bit-identical to act_quant_kernel: absmax on the magnitude
+    // bits (both conversions are monotone in them; NaNs, which fmaxf skips, count as 0), then
+    // over the row's four quarter-lanes and the team's K-split waves. Two values per
+    // instruction (packed 16-bit max); a maximum above the infinity pattern means a NaN is
+    // present, and only then the exact NaN-skipping pass runs.
+    auto quantize = [&](const DecCursor& c) __attribute__((always_inline)) {
+        constexpr uint32_t nan_above = ABF16 ? 0x7F80u : 0x7C00u;
+        u16x2 m2 = {0, 0};
+#pragma unroll
+        for (int g = 0; g < GPW; ++g)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t wd[4] = {raw[g][i].x, raw[g][i].y, raw[g][i].z, raw[g][i].w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    m2 = __builtin_elementwise_max(m2, __builtin_bit_cast(u16x2, wd[j] & 0x7FFF7FFFu));
             }
-        };
-
-        for (int m0 = 0; m0 < cnt; m0 += 16) {            // 16 rows per pass
-            const int mreal = min(16, cnt - m0);
-            // activation rows of this pass (pad rows repeat the last real row), quantised in
-            // registers: lane (q, c16) holds k in [128 g + 32 q, +32) of row c16. The rows go
-            // out first and the first weight chunk right behind them (the memory counter
-            // completes in order, so the wait for the rows leaves the chunk in flight); the
-            // second chunk waits until the rows are quantised: with both chunks and the raw
-            // rows in registers at once the kernel spills, and a spill reload waits for every
-            // access in flight. (Staging the rows in LDS by direct loads instead frees the
-            // registers but measured slower: the rows land later, and a read of directly
-            // loaded LDS waits for every access in flight.)
-            const int my_m = min(c16, mreal - 1);
-            const int my_slot = L.slot[s0 + m0 + my_m];
-            const int arow = p.a_per_token ? my_slot / p.top_k : my_slot;
-            const uint16_t* xr = reinterpret_cast<const uint16_t*>(p.a) + (int64_t)arow * p.K + q * 32;
-            uint4 raw[GPW][4];
-#pragma unroll
-            for (int g = 0; g < GPW; ++g)
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    raw[g][i] = reinterpret_cast<const uint4*>(xr + (g0 + g) * kGroup)[i];
-            issue(0, B0{});
-            auto raw_at = [&](int g, int i) -> uint4 { return raw[g][i]; };
-            // absmax on the magnitude bits (both conversions are monotone in them; NaNs,
-            // which fmaxf skips, count as 0), then over the row's four quarter-lanes and the
-            // team's K-split waves. Two values per instruction (packed 16-bit max); a maximum
-            // above the infinity pattern means a NaN is present, and only then the exact
-            // NaN-skipping pass runs.
-            constexpr uint32_t nan_above = ABF16 ? 0x7F80u : 0x7C00u;
-            u16x2 m2 = {0, 0};
+        uint32_t mbits = max((uint32_t)m2.x, (uint32_t)m2.y);
+        if (mbits > nan_above) {
+            mbits = 0;
 #pragma unroll
             for (int g = 0; g < GPW; ++g)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const uint4 rv = raw_at(g, i);
-                    const uint32_t wd[4] = {rv.x, rv.y, rv.z, rv.w};
-#pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                        m2 = __builtin_elementwise_max(m2, __builtin_bit_cast(u16x2, wd[j] & 0x7FFF7FFFu));
-                }
-            uint32_t mbits = max((uint32_t)m2.x, (uint32_t)m2.y);
-            if (mbits > nan_above) {
-                mbits = 0;
-#pragma unroll
-                for (int g = 0; g < GPW; ++g)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const uint4 rv = raw_at(g, i);
-                        const uint32_t wd[4] = {rv.x, rv.y, rv.z, rv.w};
-#pragma unroll
-                        for (int j = 0; j < 4; ++j) {
-                            const uint32_t lo = wd[j] & 0x7FFFu, hi = (wd[j] >> 16) & 0x7FFFu;
-                            mbits = max(mbits, lo > nan_above ? 0u : lo);
-                            mbits = max(mbits, hi > nan_above ? 0u : hi);
-                        }
-                    }
-            }
-            float amax = dec_act_f32<ABF16>(mbits);
-            {
-                const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(amax), __float_as_uint(amax), false, false);
-                amax = fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
-                const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(amax), __float_as_uint(amax), false, false);
-                amax = fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
-            }
-            if constexpr (KSPLIT > 1) {
-                if (q == 0) s_amax[wave][c16] = amax;
-                lds_barrier();
-#pragma unroll
-                for (int j = 0; j < KSPLIT; ++j) amax = fmaxf(amax, s_amax[team * KSPLIT + j][c16]);
-            }
-            const float my_asc = act_scale_from_absmax(amax);
-            const float inv = 1.0f / my_asc;
-            v8i af[GPW];
-#pragma unroll
-            for (int g = 0; g < GPW; ++g)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {   // k8-interleaved bytes, as act_quant_kernel
-                    const uint4 rv = raw_at(g, i);
-                    const uint32_t wd[4] = {rv.x, rv.y, rv.z, rv.w};
-                    float f[8];
+                    const uint32_t wd[4] = {raw[g][i].x, raw[g][i].y, raw[g][i].z, raw[g][i].w};
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
-                        f[2 * j] = dec_act_f32<ABF16>(wd[j] & 0xFFFFu) * inv;
-                        f[2 * j + 1] = dec_act_f32<ABF16>(wd[j] >> 16) * inv;
-                    }
-                    af[g][2 * i] = (int)pack4_e4m3(f[0], f[2], f[4], f[6]);
-                    af[g][2 * i + 1] = (int)pack4_e4m3(f[1], f[3], f[5], f[7]);
-                }
-            v4f sa[GPW];   // 2^-9 * group sums of rows 4q .. 4q + 3 (zero-point term)
-#pragma unroll
-            for (int g = 0; g < GPW; ++g) {
-                const int one = (int)kDecOnes;
-                sa[g] = mfma_16x16x128(af[g], v8i{one, one, one, one, one, one, one, one},
-                                       v4f{0.f, 0.f, 0.f, 0.f});
-#pragma unroll
-                for (int i = 0; i < 4; ++i) sa[g][i] *= 1.0f / kNibbleScale;
-            }
-            issue(1, B1{});
-            // this pass's output rows (slot, scale) for the stores, per wave
-            if (q == 0) {
-                s_oslot[wave][c16] = c16 < mreal ? L.slot[s0 + m0 + c16] : -1;
-                s_oasc[wave][c16] = my_asc * kNibbleScale;
-            }
-
-            auto store = [&](int unit, int f0, const v4f& ra, const v4f& rb) {
-                const int col = (t0 + unit * C::CT + f0) * 16 + c16;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int m = 4 * q + i;
-                    if (m >= mreal) continue;
-                    const int sl = s_oslot[wave][m];
-                    const float a = s_oasc[wave][m];
-                    if constexpr (C::kSilu) {
-                        reinterpret_cast<__half*>(p.out)[(int64_t)sl * ncols + col] =
-                            silu_mul_h(__float2half(as_f32(ra[i] * a)), __float2half(as_f32(rb[i] * a)));
-                    } else {
-                        reinterpret_cast<float*>(p.out)[(int64_t)sl * p.N + col] = ra[i] * a;
+                        const uint32_t lo = wd[j] & 0x7FFFu, hi = (wd[j] >> 16) & 0x7FFFu;
+                        mbits = max(mbits, lo > nan_above ? 0u : lo);
+                        mbits = max(mbits, hi > nan_above ? 0u : hi);
                     }
                 }
-            };
+        }
+        float amax = dec_act_f32<ABF16>(mbits);
+        {
+            const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(amax), __float_as_uint(amax), false, false);
+            amax = fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+            const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(amax), __float_as_uint(amax), false, false);
+            amax = fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+        }
+        if constexpr (KSPLIT > 1) {
+            if (q == 0) s_amax[wave][c16] = amax;
+            lds_barrier();
+#pragma unroll
+            for (int j = 0; j < KSPLIT; ++j) amax = fmaxf(amax, s_amax[team * KSPLIT + j][c16]);
+        }
+        const float my_asc = act_scale_from_absmax(amax);
+        const float inv = 1.0f / my_asc;
+#pragma unroll
+        for (int g = 0; g < GPW; ++g)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {   // k8-interleaved bytes, as act_quant_kernel
+                const uint32_t wd[4] = {raw[g][i].x, raw[g][i].y, raw[g][i].z, raw[g][i].w};
+                float f[8];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    f[2 * j] = dec_act_f32<ABF16>(wd[j] & 0xFFFFu) * inv;
+                    f[2 * j + 1] = dec_act_f32<ABF16>(wd[j] >> 16) * inv;
+                }
+                af[g][2 * i] = (int)pack4_e4m3(f[0], f[2], f[4], f[6]);
+                af[g][2 * i + 1] = (int)pack4_e4m3(f[1], f[3], f[5], f[7]);
+            }
+#pragma unroll
+        for (int g = 0; g < GPW; ++g) {
+            const int one = (int)kDecOnes;
+            sa[g] = mfma_16x16x128(af[g], v8i{one, one, one, one, one, one, one, one},
+                                   v4f{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sa[g][i] *= 1.0f / kNibbleScale;
+        }
+        // the pass's output rows (slot, scale) for the stores
+        const int s0 = (int)L.first[c.r] + c.m0;
+        const int mreal = min(16, (int)L.first[c.r + 1] - s0);
+#pragma unroll
+        for (int i = 0; i < NRO; ++i) {
+            const int m = 4 * q + (KSPLIT > 1 ? wave % KSPLIT : i);
+            osl[i] = L.slot[s0 + min(m, mreal - 1)];
+            oasc[i] = __shfl(my_asc * kNibbleScale, m, 64);
+        }
+    };
 
-            v4f run[C::FR];
+    // column tile f0 of unit column ucol: value (ra, rb) of an output row (slot sl, scale a)
+    auto store1 = [&](int ucol, int f0, int sl, float a, float ra, float rb) __attribute__((always_inline)) {
+        const int col = (ucol * C::CT + f0) * 16 + c16;
+        if constexpr (C::kSilu) {
+            reinterpret_cast<__half*>(p.out)[(int64_t)sl * ncols + col] =
+                silu_mul_h(__float2half(as_f32(ra * a)), __float2half(as_f32(rb * a)));
+        } else {
+            reinterpret_cast<float*>(p.out)[(int64_t)sl * p.N + col] = ra * a;
+        }
+    };
+
+    // K split: the batch's completed units, per ring slot (column, and this wave's output row)
+    int bp = 0;             // batch parity (LDS buffer)
+    int bucol[C::D], bsl[C::D];
+    float basc[C::D];
+    auto part_of = [&](int parity, int slot) __attribute__((always_inline)) {
+        return s_part + (parity * C::D + slot) * (KSPLIT * C::FR * 64);
+    };
+    // sum the K-split waves' partials of slot k's unit in wave order (wave w takes row 4q + w
+    // of its lanes) and store it
+    auto flush_slot = [&](int k) __attribute__((always_inline)) {
+        const v4f* part = part_of(bp, k);
+        const int i = wave % KSPLIT;
+        float sum[C::FR];
+#pragma unroll
+        for (int f = 0; f < C::FR; ++f) {
+            const float* pf = reinterpret_cast<const float*>(part + f * 64 + lane) + i;
+            sum[f] = pf[0];
+#pragma unroll
+            for (int j = 1; j < KSPLIT; ++j) sum[f] += pf[j * C::FR * 64 * 4];
+        }
+#pragma unroll
+        for (int ct = 0; ct < C::CT; ++ct)
+            store1(bucol[k], ct, bsl[k], basc[k], sum[ct], C::kSilu ? sum[C::CT + ct] : sum[ct]);
+    };
+    auto consume = [&](const DecCursor& c, auto slot) __attribute__((always_inline)) {
+        constexpr int b = decltype(slot)::value;
+        constexpr int gb = b % C::NB;       // a pass has NB chunks per unit: slot parity == c.b
+        const int ucol = c.u - c.r * upe;
+#pragma unroll
+        for (int f = 0; f < C::FR; ++f) {
+            const int zsh = (row_of(ucol, f, c16) & 7) * 4;
+#pragma unroll
+            for (int uu = 0; uu < C::GC; ++uu) {
+                const int ga = gb * C::GC + uu;
+                v4f acc = mfma_16x16x128(af[ga], spread_nibbles(wv[b][uu * C::FR + f]),
+                                         v4f{0.f, 0.f, 0.f, 0.f});
+                const float z = p.zeros ? (float)((zw[b][f][uu] >> zsh) & 0xF) : 8.0f;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[i] = fmaf(-z, sa[ga][i], acc[i]);
+                const float s = __half2float(__ushort_as_half(
+                    (unsigned short)(uu % 2 ? sw[b][f][uu / 2] >> 16 : sw[b][f][uu / 2])));
+#pragma unroll
+                for (int i = 0; i < 4; ++i) run[f][i] = fmaf(acc[i], s, run[f][i]);
+            }
+        }
+        if constexpr (gb == C::NB - 1) {   // unit complete; every store is unconditional
+            if constexpr (KSPLIT > 1) {
+                // partials to LDS; the batch is summed and stored after the ring's last slot
+                v4f* part = part_of(bp, b);
+#pragma unroll
+                for (int f = 0; f < C::FR; ++f) part[((wave % KSPLIT) * C::FR + f) * 64 + lane] = run[f];
+                bucol[b] = ucol;
+                bsl[b] = osl[0];
+                basc[b] = oasc[0];
+            } else {
+#pragma unroll
+                for (int ct = 0; ct < C::CT; ++ct)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        store1(ucol, ct, osl[i], oasc[i], run[ct][i],
+                               C::kSilu ? run[C::CT + ct][i] : run[ct][i]);
+            }
 #pragma unroll
             for (int f = 0; f < C::FR; ++f) run[f] = v4f{0.f, 0.f, 0.f, 0.f};
-
-            // split-K partials of up to kDecBatch units, summed in wave order and stored
-            auto flush = [&](int unit_end, int nbu) {
-                lds_barrier();
-                for (int i = tid; i < nbu * 64; i += kDecThreads) {
-                    const int bu = i >> 6;              // i & 63 == lane
-                    v4f sum[C::FR];
-#pragma unroll
-                    for (int f = 0; f < C::FR; ++f) {
-                        sum[f] = s_part[((0 * kDecBatch + bu) * C::FR + f) * 64 + lane];
-#pragma unroll
-                        for (int j = 1; j < KSPLIT; ++j) {
-                            const v4f v = s_part[((j * kDecBatch + bu) * C::FR + f) * 64 + lane];
-#pragma unroll
-                            for (int k = 0; k < 4; ++k) sum[f][k] += v[k];
-                        }
-                    }
-                    const int unit = unit_end - nbu + bu;
-#pragma unroll
-                    for (int ct = 0; ct < C::CT; ++ct)
-                        store(unit, ct, sum[ct], C::kSilu ? sum[C::CT + ct] : sum[ct]);
-                }
-                lds_barrier();
-            };
-
-            auto consume = [&](int c, auto bufc) {
-                constexpr int b = decltype(bufc)::value;
-                constexpr int gb = C::NB == 2 ? b : 0;   // chunk parity == group batch when NB == 2
-                const int unit = c / C::NB;
-#pragma unroll
-                for (int f = 0; f < C::FR; ++f) {
-                    const int zsh = (row_of(c, f, c16) & 7) * 4;
-#pragma unroll
-                    for (int uu = 0; uu < C::GC; ++uu) {
-                        const int ga = gb * C::GC + uu;
-                        v4f acc = mfma_16x16x128(af[ga], spread_nibbles(wv[b][uu * C::FR + f]),
-                                                 v4f{0.f, 0.f, 0.f, 0.f});
-                        const float z = ze ? (float)((zw[b][f][uu] >> zsh) & 0xF) : 8.0f;
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) acc[i] = fmaf(-z, sa[ga][i], acc[i]);
-                        const float s = __half2float(__ushort_as_half((unsigned short)sw[b][f][uu]));
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) run[f][i] = fmaf(acc[i], s, run[f][i]);
-                    }
-                }
-                if (c % C::NB != C::NB - 1) return;
-                // unit complete
-                if constexpr (KSPLIT > 1) {
-                    const int bu = unit % kDecBatch;
-#pragma unroll
-                    for (int f = 0; f < C::FR; ++f)
-                        s_part[(((wave % KSPLIT) * kDecBatch + bu) * C::FR + f) * 64 + lane] = run[f];
-                    if (bu == kDecBatch - 1 || unit == nunits - 1) flush(unit + 1, bu + 1);
-                } else {
-#pragma unroll
-                    for (int ct = 0; ct < C::CT; ++ct)
-                        store(unit, ct, run[ct], C::kSilu ? run[C::CT + ct] : run[ct]);
-                }
-#pragma unroll
-                for (int f = 0; f < C::FR; ++f) run[f] = v4f{0.f, 0.f, 0.f, 0.f};
-            };
-
-            for (int c = 0; c < nch; c += 2) {
-                consume(c, B0{});
-                issue(c + 2, B0{});
-                if (c + 1 < nch) consume(c + 1, B1{});
-                issue(c + 3, B1{});
-            }
-            if constexpr (KSPLIT == 1) __builtin_amdgcn_wave_barrier();
         }
-        u = ue;
+        if constexpr (KSPLIT > 1 && b == C::D - 1) {   // batch complete (a full ring turn)
+            lds_barrier();
+#pragma unroll
+            for (int k = C::NB - 1; k < C::D; k += C::NB) flush_slot(k);
+            bp ^= 1;
+        }
+    };
+
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    using S2 = std::integral_constant<int, 2>;
+    using S3 = std::integral_constant<int, 3>;
+
+    // chunks of the team's work
+    int total = 0;
+    for (int r = ua / upe; r * upe < ub; ++r)
+        total += (((int)L.first[r + 1] - (int)L.first[r] + 15) >> 4) * (seg_hi(r) - seg_lo(r)) * C::NB;
+
+    // The issue cursor runs D chunks (the ring slots) ahead of the consume cursor, across experts and
+    // passes, so the next expert's weights are in flight while a pass boundary loads and
+    // quantises rows. The rows go out before the chunk issued beside them: the memory counter
+    // completes in order, so their wait leaves that chunk in flight. The compiler derives
+    // its waits for the ring from the program order of loads, so the steady-state loop has a
+    // fixed trip count (no exit inside), its steps are kept in order by scheduling barriers,
+    // and its stores are unconditional; with these, each consume waits only for its own
+    // chunk (D - 1 chunks stay in flight).
+    const int r0 = ua / upe;
+    DecCursor cc{r0, (int)L.expert[r0], 0, ua, 0};
+    DecCursor ic = cc;
+#pragma unroll
+    for (int f = 0; f < C::FR; ++f) run[f] = v4f{0.f, 0.f, 0.f, 0.f};
+    load_rows(cc);
+    __builtin_amdgcn_sched_barrier(0);
+    issue(ic, S0{}); advance(ic);
+    __builtin_amdgcn_sched_barrier(0);
+    issue(ic, S1{}); advance(ic);
+    __builtin_amdgcn_sched_barrier(0);
+    issue(ic, S2{}); advance(ic);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (C::D > 3) {
+        issue(ic, S3{}); advance(ic);
+        __builtin_amdgcn_sched_barrier(0);
     }
+    quantize(cc);
+
+    auto step = [&](auto slot) __attribute__((always_inline)) {
+        consume(cc, slot);
+        const bool np = advance(cc) && cc.u < ub;
+        if (np) load_rows(cc);
+        issue(ic, slot);
+        advance(ic);
+        if (np) quantize(cc);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    const int nq = total / C::D;
+    for (int it = 0; it < nq; ++it) {
+        step(S0{});
+        step(S1{});
+        step(S2{});
+        if constexpr (C::D > 3) step(S3{});
+    }
+    const int rem = total % C::D;
+    if (rem > 0) step(S0{});
+    if (rem > 1) step(S1{});
+    if constexpr (C::D > 3)
+        if (rem > 2) step(S2{});
+    if constexpr (KSPLIT > 1) {     // the last, partial batch (slots 0 .. rem - 1)
+        lds_barrier();
+#pragma unroll
+        for (int k = 0; k < C::D - 1; ++k)
+            if (k % C::NB == C::NB - 1 && k < rem) flush_slot(k);
+    }
+    // keeps the L2 warm-up load (its value never matches: a NaN pattern in a block that does
+    // not exist)
+    if (warm == 0x7FC00001u && blockIdx.x == 0x7FFFFFFFu) reinterpret_cast<uint32_t*>(p.out)[0] = warm;
 }
 
 struct DecSplit {
@@ -464,7 +593,7 @@ int persistent_grid() {
         hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         ncu <= 0)
         ncu = 256;
-    return 2 * ncu;   // two four-wave work-groups per CU (two waves per SIMD)
+    return ncu;   // one four-wave work-group per CU (one wave per SIMD, up to 512 registers)
 }
 
 template <Epi EPI, int GPW, int KSPLIT, bool ABF16>
