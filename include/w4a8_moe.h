@@ -250,6 +250,31 @@ W4A8_API int w4a8_moe_forward(const void* x, int x_dtype, int64_t T, int64_t H, 
                               float* topk_weights, int32_t* topk_ids, void* out,
                               void* workspace, size_t workspace_bytes, void* stream);
 
+/* Size in bytes of the library-owned scratch of w4a8_moe_forward_noalloc (one per GPU). */
+#define W4A8_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+
+/* w4a8_moe_forward with no workspace argument that allocates nothing: the intermediates live
+ * in a static device array of W4A8_NOALLOC_SCRATCH_BYTES that the library holds on every GPU
+ * it runs on until the process ends (its address is looked up once per device, on that
+ * device's first call, with the device current). Shapes whose w4a8_moe_apply_workspace_size
+ * exceeds the array are refused with W4A8_ERR_WORKSPACE (decode, T <= 96, fits at the
+ * reference's shapes; large prefill does not). Results are bit-identical to
+ * w4a8_moe_forward. Every call on a GPU uses that GPU's one array, which keeps the last
+ * call's contents (the path writes every intermediate before reading it): calls that overlap
+ * on one GPU (two streams or two threads) race and must be ordered by the caller. The stream
+ * must belong to the current device. No counterpart in the reference: it is for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid allocation). */
+W4A8_API int w4a8_moe_forward_noalloc(const void* x, int x_dtype, int64_t T, int64_t H,
+                                      int64_t inter, int64_t E, int64_t top_k, int64_t group_size,
+                                      const float* router_logits, int renormalize,
+                                      const int32_t* w13, const void* w13_scales_f16,
+                                      const int32_t* w13_zeros, const int32_t* w2,
+                                      const void* w2_scales_f16, const int32_t* w2_zeros,
+                                      int weights_layout, const int32_t* expert_map,
+                                      int64_t num_global_experts, float* topk_weights,
+                                      int32_t* topk_ids, void* out, void* stream);
+
 /* Optional per-stage timing of the whole-layer calls on the calling thread: when count >= 8,
  * the next w4a8_moe_apply / _fragments / w4a8_moe_forward calls record events[0] before the
  * first expert-path launch and events[i] after stage i (1 align, 2 act-quant x, 3 reserved

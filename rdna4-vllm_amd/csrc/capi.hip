@@ -1,6 +1,7 @@
 // C ABI entry points (include/w4a8_moe.h): argument validation mirroring the reference's
 // TORCH_CHECKs (w4a8_fp8_wmma/bindings.cpp), workspace carving, kernel-id dispatch and the
 // whole-layer composition (moe_experts.py:493-665).
+#include <mutex>
 #include <string>
 
 #include "w4a8_common.h"
@@ -387,6 +388,45 @@ int moe_apply_impl(const void* x, int x_dtype, int64_t T, int64_t H, int64_t int
 }
 }  // namespace w4a8
 
+namespace w4a8 {
+namespace {
+
+// Scratch of w4a8_moe_forward_noalloc: device data of the code object, one copy per GPU,
+// allocated when the library's code is loaded onto that GPU and held until the process
+// ends. In host code the array's name is only a stand-in for the symbol; the device address
+// of each GPU's copy comes from hipGetSymbolAddress with that GPU current.
+constexpr size_t kNoAllocScratchBytes = W4A8_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's scratch address, looked up on the device's first call.
+int noalloc_scratch(void** out) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        set_error("moe_forward_noalloc: no usable current HIP device");
+        return W4A8_ERR_HIP;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* p = nullptr;
+        const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (err != hipSuccess || p == nullptr) {
+            set_error(std::string("moe_forward_noalloc: hipGetSymbolAddress(scratch) failed: ") +
+                      hipGetErrorString(err));
+            return W4A8_ERR_HIP;
+        }
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return W4A8_OK;
+}
+
+}  // namespace
+}  // namespace w4a8
+
 extern "C" {
 
 int w4a8_abi_version(void) { return 2; }
@@ -675,6 +715,34 @@ int w4a8_moe_forward(const void* x, int x_dtype, int64_t T, int64_t H, int64_t i
                           expert_map, num_global_experts, 0, out, workspace, workspace_bytes,
                           stream, weights_layout == W4A8_WEIGHTS_FRAGMENTS, router_logits,
                           renormalize != 0);
+}
+
+int w4a8_moe_forward_noalloc(const void* x, int x_dtype, int64_t T, int64_t H, int64_t inter,
+                             int64_t E, int64_t top_k, int64_t group_size,
+                             const float* router_logits, int renormalize, const int32_t* w13,
+                             const void* w13_scales_f16, const int32_t* w13_zeros,
+                             const int32_t* w2, const void* w2_scales_f16, const int32_t* w2_zeros,
+                             int weights_layout, const int32_t* expert_map,
+                             int64_t num_global_experts, float* topk_weights, int32_t* topk_ids,
+                             void* out, void* stream) {
+    clear_error();
+    W4A8_REQUIRE(T >= 0 && H > 0 && inter > 0 && E > 0 && top_k > 0,
+                 "moe_forward_noalloc: invalid sizes");
+    const size_t need = w4a8_moe_apply_workspace_size(T, H, inter, E, top_k);
+    if (need > w4a8::kNoAllocScratchBytes) {
+        w4a8::set_error("moe_forward_noalloc: this shape needs " + std::to_string(need) +
+                        " bytes of scratch; the library's static scratch holds " +
+                        std::to_string(w4a8::kNoAllocScratchBytes) +
+                        " (W4A8_NOALLOC_SCRATCH_BYTES): call w4a8_moe_forward with a workspace");
+        return W4A8_ERR_WORKSPACE;
+    }
+    void* ws = nullptr;
+    const int rc = w4a8::noalloc_scratch(&ws);
+    if (rc != W4A8_OK) return rc;
+    return w4a8_moe_forward(x, x_dtype, T, H, inter, E, top_k, group_size, router_logits,
+                            renormalize, w13, w13_scales_f16, w13_zeros, w2, w2_scales_f16,
+                            w2_zeros, weights_layout, expert_map, num_global_experts,
+                            topk_weights, topk_ids, out, ws, w4a8::kNoAllocScratchBytes, stream);
 }
 
 int w4a8_moe_fragments_supported(int64_t H, int64_t inter, int64_t group_size) {

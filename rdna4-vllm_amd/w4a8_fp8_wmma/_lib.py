@@ -65,6 +65,10 @@ SIGNATURES = {
                                         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64,
                                         _c_void_p, _c_void_p, _size, _c_void_p]),
     "w4a8_moe_fragments_supported": (_int, [_i64, _i64, _i64]),
+    "w4a8_moe_forward_noalloc": (_int, [_c_void_p, _int, _i64, _i64, _i64, _i64, _i64, _i64,
+                                        _c_void_p, _int, _c_void_p, _c_void_p, _c_void_p,
+                                        _c_void_p, _c_void_p, _c_void_p, _int, _c_void_p, _i64,
+                                        _c_void_p, _c_void_p, _c_void_p, _c_void_p]),
 }
 
 ABI_VERSION = 2
