@@ -184,7 +184,8 @@ def gemm1_kernel_name(cfg, decode, layout):
         # persistent decode kernel (decode_gemv.hip dec_split): groups per wave, split-K
         split = {1: "1, 1", 2: "2, 1", 3: "3, 1", 4: "4, 1", 8: "2, 4", 12: "3, 4", 16: "4, 4",
                  32: "8, 4"}[H // 128]
-        return f"decode_gemv_kernel<(w4a8::Epi)1, {split}, false>"
+        # the bench's activations are bf16: the kernel's bf16 instantiation runs
+        return f"decode_gemv_kernel<(w4a8::Epi)1, {split}, true>"
     if decode:
         split = {1: "1, 1", 2: "2, 1", 3: "3, 1", 4: "4, 1", 8: "4, 2", 12: "3, 4", 16: "4, 4",
                  32: "8, 4"}[H // 128]
