@@ -1,11 +1,12 @@
 // Prefill grouped W4A8 GEMM, activation-resident schedule (gfx950 fp8 MFMA).
 //
 // Replaces the reference's tiled WMMA grouped GEMM (moe_gemm_tiled.h:29-350, dispatched at
-// moe_kernel.hip:1110-1155) for the many-token regime when K <= 2048. Arithmetic contract as
+// moe_kernel.hip:1110-1155) for the many-token regime when K <= 4096. Arithmetic contract as
 // in w4a8_common.h; the schedule is this file's own:
 //
-//   * a work-group owns 64 consecutive sorted rows (one expert) and ALL N columns: its e4m3
-//     activation tile (64 x K bytes) and the rows' per-group sums are loaded into LDS once,
+//   * a work-group owns BM consecutive sorted rows (one expert; BM = 64 for K <= 2048, 32 up
+//     to K = 4096, so the tile fits LDS) and ALL N columns: its e4m3 activation tile
+//     (BM x K bytes) and the rows' per-group sums are loaded into LDS once,
 //     then the kernel streams the expert's int4 weights past them, 256 weight rows at a time
 //     (a "range": 8 waves, two per SIMD, x 2 16-column fragments; SiLU: 128 gate + the
 //     matching 128 up columns);
@@ -23,7 +24,9 @@
 //     (moe_gemm_tiled.h:144-151) with the lane's four scales read from a per-wave LDS table;
 //   * the range's scales and zero-points are fetched one range ahead into registers; at a
 //     range boundary each wave writes the scale table and s*z (bf16 hi/lo) for its own 32
-//     weight rows, so no work-group barrier follows the prologue;
+//     weight rows, so no work-group barrier follows the prologue. The tables hold 16 K
+//     groups; for K > 2048 they are rebuilt in the middle of each range, after the first
+//     half's zero-point term;
 //   * after the last group of a range the zero-point term sum_g sum_k a * z * s is formed by
 //     bf16 MFMAs over (row group sums) x (s*z), out = asc * (512 * run - term) is stored as
 //     8-byte row pieces (fp16, or fp16 SiLU(gate) * up, bit-identical to silu_and_mul) and
@@ -40,43 +43,56 @@
 namespace w4a8 {
 namespace {
 
-constexpr int kArBM = 64;                       // rows per work-group
+constexpr int kArBM = 64;                       // rows per work-group (K <= kArMaxK)
+constexpr int kArBMWide = 32;                   // rows per work-group for kArMaxK < K <= kArMaxKWide
 constexpr int kArWaves = 8;                     // two waves per SIMD
 constexpr int kArThreads = kArWaves * 64;
 constexpr int kArNT = 2;                        // 16-column B fragments per wave and range
 constexpr int kArBN = kArWaves * kArNT * 16;    // 256 weight rows per range
 constexpr int kArD = 4;                         // B steps in flight per wave
-constexpr int kArMaxK = 2048;                   // activation tile must fit LDS
+constexpr int kArMaxK = 2048;                   // 64-row activation tile must fit LDS
+constexpr int kArMaxKWide = 4096;               // 32-row activation tile must fit LDS
 constexpr int kArMaxKAq = 1024;                 // fp16 rows quantised in the prologue
-constexpr int kArGp = 16;                       // group slots of the per-range tables
+constexpr int kArGp = 16;                       // group slots of the per-range weight tables
 constexpr int kArXcds = 8;                      // work-groups go round-robin to 8 XCDs
 
-// Activation tile in LDS, group-major: K group g of row m is 128 bytes at g * 8 KB + m * 128,
-// its eight 16-byte chunks stored at chunk ^ (m & 7), so the eight rows a ds_read_b128
-// serves per cycle hit eight different bank quads, and the rows of fragment i sit at the
-// fixed offset i * 2 KB.
-__host__ __device__ constexpr int ar_a_group_bytes() { return kArBM * kGroup; }
+template <int BM>
+__host__ __device__ constexpr int ar_max_k() { return BM == kArBM ? kArMaxK : kArMaxKWide; }
+// group slots of the row-sum table: every K group of the widest K the tile takes
+template <int BM>
+__host__ __device__ constexpr int ar_gpr() { return ar_max_k<BM>() / kGroup; }
+
+// Activation tile in LDS, group-major: K group g of row m is 128 bytes at g * BM * 128 +
+// m * 128, its eight 16-byte chunks stored at chunk ^ (m & 7), so the eight rows a
+// ds_read_b128 serves per cycle hit eight different bank quads, and the rows of fragment i
+// sit at the fixed offset i * 2 KB.
+template <int BM>
+__host__ __device__ constexpr int ar_a_group_bytes() { return BM * kGroup; }
+template <int BM>
 __device__ __forceinline__ int ar_a_off(int m, int g, int chunk) {
-    return g * ar_a_group_bytes() + m * kGroup + ((chunk ^ (m & 7)) << 4);
+    return g * ar_a_group_bytes<BM>() + m * kGroup + ((chunk ^ (m & 7)) << 4);
 }
-// Dynamic LDS layout (bytes): activation tile; row group sums (hi/lo bf16); per range:
-// s*z (hi/lo bf16) of the 256 weight rows, scales [wave][group][column / 4][fragment]
-// [column % 4] (fp16, the 16 bytes lanes (q, *) read per step) and a staging area for the
-// zero-point words
+// Dynamic LDS layout (bytes): activation tile; row group sums (hi/lo bf16, every group);
+// per range and half of K (16 groups): s*z (hi/lo bf16) of the 256 weight rows, scales
+// [wave][group][column / 4][fragment][column % 4] (fp16, the 16 bytes lanes (q, *) read
+// per step) and a staging area for the zero-point words. For K = 4096 and 32 rows this is
+// 158 KB.
+template <int BM>
 struct ArLds {
     int a, sah, sal, szh, szl, sc, zst, total;
     __host__ __device__ explicit ArLds(int K) {
         a = 0;
-        sah = (K / kGroup) * ar_a_group_bytes();
-        sal = sah + kArBM * kArGp * 2;
-        szh = sal + kArBM * kArGp * 2;
+        sah = (K / kGroup) * ar_a_group_bytes<BM>();
+        sal = sah + BM * ar_gpr<BM>() * 2;
+        szh = sal + BM * ar_gpr<BM>() * 2;
         szl = szh + kArBN * kArGp * 2;
         sc = szl + kArBN * kArGp * 2;
         zst = sc + kArBN * kArGp * 2;
         total = zst + kArBN * 8;
     }
 };
-__host__ inline size_t ar_lds_bytes(int K) { return (size_t)ArLds(K).total + kArBM * 4; }
+template <int BM>
+__host__ inline size_t ar_lds_bytes(int K) { return (size_t)ArLds<BM>(K).total + BM * 4; }
 
 // Output columns per range; output column and weight row of fragment j, column c of wave w
 // in range r (SiLU: fragment 0 holds gate rows col, fragment 1 the matching up rows
@@ -114,9 +130,10 @@ __device__ __forceinline__ uint32_t pack_bf16x2(__bf16 a, __bf16 b) {
     return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
 }
 
-template <Epi EPI, bool FRAG>
+template <Epi EPI, bool FRAG, int BM>
 __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
     constexpr bool kSilu = EPI == Epi::kSiluHalf;
+    constexpr int GPR = ar_gpr<BM>();
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
 
     const int tid = threadIdx.x;
@@ -126,31 +143,31 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
     const int c16 = lane & 15;
     const int K = p.K;
     const int G = p.G;
-    const ArLds L(K);
-    uint8_t* s_a = lds + L.a;                                         // [G][64][128] e4m3
-    __bf16* s_sah = reinterpret_cast<__bf16*>(lds + L.sah);           // [64][16] row sums hi
+    const ArLds<BM> L(K);
+    uint8_t* s_a = lds + L.a;                                         // [G][BM][128] e4m3
+    __bf16* s_sah = reinterpret_cast<__bf16*>(lds + L.sah);           // [BM][GPR] row sums hi
     __bf16* s_sal = reinterpret_cast<__bf16*>(lds + L.sal);           // ... lo
     __bf16* s_szh = reinterpret_cast<__bf16*>(lds + L.szh);           // [256][16] s*z hi
     __bf16* s_szl = reinterpret_cast<__bf16*>(lds + L.szl);           // ... lo
     uint16_t* s_sc = reinterpret_cast<uint16_t*>(lds + L.sc);         // [8][16][4][2][4] fp16
     uint32_t* s_zst = reinterpret_cast<uint32_t*>(lds + L.zst);       // [8][64] zero words
-    float* s_asc = reinterpret_cast<float*>(lds + L.total);           // [64]
+    float* s_asc = reinterpret_cast<float*>(lds + L.total);           // [BM]
 
     // ---- tile of this work-group: XCD-aware order over the live tiles ----
     const int ntp = p.ntp ? p.ntp[0] : (int)p.P;
     const int64_t live_rows = std::min<int64_t>((int64_t)ntp, p.P);
-    const int ntiles = (int)((live_rows + kArBM - 1) / kArBM);
+    const int ntiles = (int)((live_rows + BM - 1) / BM);
     const int per_xcd = (ntiles + kArXcds - 1) / kArXcds;
     const int b = blockIdx.x;
     if (b / kArXcds >= per_xcd) return;
     const int tile = (b % kArXcds) * per_xcd + b / kArXcds;
     if (tile >= ntiles) return;
-    const int64_t row0 = (int64_t)tile * kArBM;
+    const int64_t row0 = (int64_t)tile * BM;
     const int e = p.expert_ids ? p.expert_ids[row0 / p.block_m] : 0;
     if (e < 0 || e >= p.E) return;
-    // lane l of every wave resolves row l; a real row's source is its activation row
+    // lane l < BM of every wave resolves row l; a real row's source is its activation row
     int slot = -1;
-    const int src = resolve_row(p, row0 + lane, ntp, slot);
+    const int src = lane < BM ? resolve_row(p, row0 + lane, ntp, slot) : -1;
     const uint64_t vmask = __ballot(src >= 0);
     if (vmask == 0) return;
     const int maxrow = 63 - __clzll(vmask);
@@ -158,7 +175,7 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
     const int fallback = __shfl(src, __ffsll((long long)vmask) - 1, 64);
     // source row of tile row r (lane r of every wave resolved it); padding rows read a real
     // row so every load stays in bounds. Every lane must take part (shuffle).
-    auto src_of = [&](int r) {
+    auto src_of = [&](int r) __attribute__((always_inline)) {
         const int sr = __shfl(src, r, 64);
         return sr >= 0 ? sr : fallback;
     };
@@ -191,7 +208,7 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
     // range's final four groups, which this wave requested just before and are still in L2:
     // a work-group cannot retire before its loads return, so these must not go to HBM.
     const uint32_t tail_off = (uint32_t)(nranges - 1) * r_step + (uint32_t)(G - kArD) * g_step;
-    auto issue = [&](auto slotc) {
+    auto issue = [&](auto slotc) __attribute__((always_inline)) {
         constexpr int sl = decltype(slotc)::value;
         const uint8_t* base = we + i_off;
 #pragma unroll
@@ -211,29 +228,31 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
     using S2 = std::integral_constant<int, 2>;
     using S3 = std::integral_constant<int, 3>;
 
-    // ---- per-range tables. Lane l of wave w owns weight row lrow = 32 w + (l & 31), i.e.
-    //      fragment (l >> 4) & 1, column l & 15, for groups 8 (l >> 5) .. + 7: two 8-byte
-    //      scale loads. Lane l also loads zero-point word l & 15 of the wave's 8-row group
-    //      l >> 4; a row's group then reads its 8 words from the staging area ----
+    // ---- per-range tables, one half of K (16 groups) at a time: half h covers groups
+    //      16 h .. 16 h + 15. Lane l of wave w owns weight row lrow = 32 w + (l & 31), i.e.
+    //      fragment (l >> 4) & 1, column l & 15, for groups 16 h + 8 (l >> 5) .. + 7: two
+    //      8-byte scale loads. Lane l also loads zero-point word 16 h + (l & 15) of the
+    //      wave's 8-row group l >> 4; a row's group then reads its 8 words from the staging
+    //      area ----
     const int trow = lane & 31, tj = trow >> 4, tc = trow & 15, th = lane >> 5;
     const int lrow = 32 * wave + trow;
     uint2 pf_s[2];
     uint32_t pf_z;
-    auto prefetch = [&](int r) {
+    auto prefetch = [&](int r, int h) __attribute__((always_inline)) {
         const int rr = std::min(r, nranges - 1);
         const int n = ar_row<kSilu>(rr, wave, tj, tc, ncols);
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-            const int qd = std::min(2 * th + u, G / 4 - 1);
+            const int qd = std::min(4 * h + 2 * th + u, G / 4 - 1);
             pf_s[u] = *reinterpret_cast<const uint2*>(se + (uint32_t)n * G + 4 * qd);
         }
         const int rgl = lane >> 4;                     // the wave's 8-row groups: (fragment, half)
         const int nz = ar_row<kSilu>(rr, wave, rgl >> 1, 8 * (rgl & 1), ncols);
-        const int wz = std::min(lane & 15, G - 1);
+        const int wz = std::min(kArGp * h + (lane & 15), G - 1);
         // symmetric weights read (and ignore) a scale word instead: same load count
         pf_z = ze ? (uint32_t)ze[(uint32_t)(nz >> 3) * G + wz] : *reinterpret_cast<const uint32_t*>(se);
     };
-    auto build = [&](int r) {
+    auto build = [&](int r, int h) __attribute__((always_inline)) {
         const int n = ar_row<kSilu>(r, wave, tj, tc, ncols);
         s_zst[64 * wave + lane] = pf_z;
         uint32_t zw[8];
@@ -257,7 +276,7 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
                 const uint16_t hb = (tt & 1) ? (uint16_t)(w2 >> 16) : (uint16_t)(w2 & 0xFFFF);
                 const float sv = __half2float(__ushort_as_half(hb));
                 const float z = ze ? (float)((zw[tt] >> zsh) & 0xF) : 8.0f;
-                sz[v] = g < G ? sv * z : 0.f;   // exact: fp16 scale x integer <= 15
+                sz[v] = kArGp * h + g < G ? sv * z : 0.f;   // exact: fp16 scale x integer <= 15
                 s_sc[((wave * kArGp + g) * 4 + (tc >> 2)) * 8 + tj * 4 + (tc & 3)] = hb;
             }
             const __bf16 h0 = (__bf16)sz[0], h1 = (__bf16)sz[1];
@@ -271,16 +290,18 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
     // ---- prologue. Loads first, in this order: range 0's tables, the activation rows (and
     //      their scales and group sums), the first four weight steps; waiting for the rows
     //      then leaves the weights in flight behind the LDS writes and the table build ----
-    prefetch(0);
-    constexpr int kRowsPerWave = kArBM / kArWaves;
+    // table halves of K: 64-row tiles take K <= 2048 (one half), 32-row tiles 2048 < K <= 4096
+    constexpr int GH = BM == kArBM ? 1 : 2;
+    prefetch(0, 0);
+    constexpr int kRowsPerWave = BM / kArWaves;
     constexpr int kAqPass = kArMaxKAq / 512;
-    constexpr int kMaxChunks = kArMaxK / 16 * kArBM / kArThreads;   // 16-byte chunks per thread
+    constexpr int kMaxChunks = ar_max_k<BM>() / 16 * BM / kArThreads;   // 16-byte chunks per thread
     const bool self_quant = !kSilu && p.xq == nullptr;
     const int cpr = K / 16;                             // chunks per row
-    const int total = kArBM * cpr;                      // multiple of 512 (K % 128 == 0)
+    const int total = BM * cpr;                         // multiple of 512 (K % 512 == 0)
     uint4 raw[kRowsPerWave][kAqPass];                   // fp16 rows (self-quantising tiles)
     uint4 va[kMaxChunks];                               // e4m3 tile chunks (prequantised rows)
-    float asv[kArBM * kArGp / kArThreads];              // row group sums
+    float asv[BM * GPR / kArThreads];                   // row group sums
     float ascv = 0.f;
     if (self_quant) {
         // fp16 rows in (the tile owns its rows: each is read by this work-group only);
@@ -303,10 +324,10 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
             va[u] = *reinterpret_cast<const uint4*>(p.xq + (int64_t)src_of(c / cpr) * K + (c % cpr) * 16);
         }
 #pragma unroll
-        for (int j = 0; j < kArBM * kArGp / kArThreads; ++j) {   // row sums; groups >= G are 0
+        for (int j = 0; j < BM * GPR / kArThreads; ++j) {   // row sums; groups >= G are 0
             const int i = j * kArThreads + tid;
-            const int sr = src_of(i / kArGp);
-            asv[j] = i % kArGp < G ? p.asum[(int64_t)sr * G + i % kArGp] : 0.f;
+            const int sr = src_of(i / GPR);
+            asv[j] = i % GPR < G ? p.asum[(int64_t)sr * G + i % GPR] : 0.f;
         }
         if (wave == 0 && src >= 0) ascv = p.asc[src];
     }
@@ -321,7 +342,7 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
 #pragma unroll
         for (int u = 0; u < kRowsPerWave; ++u) {
             const int m = kRowsPerWave * wave + u;
-            auto val = [&](int ps, int j) {
+            auto val = [&](int ps, int j) __attribute__((always_inline)) {
                 const uint4 w4 = raw[u][ps];
                 const uint32_t wd = j < 2 ? w4.x : j < 4 ? w4.y : j < 6 ? w4.z : w4.w;
                 return __half2float(__ushort_as_half((uint16_t)((j & 1) ? wd >> 16 : wd & 0xFFFF)));
@@ -346,19 +367,19 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
                 const uint32_t lo = pack4_e4m3(v[0], v[2], v[4], v[6]);
                 const uint32_t hi = pack4_e4m3(v[1], v[3], v[5], v[7]);
                 const int k = ps * 512 + lane * 8;
-                *reinterpret_cast<uint2*>(s_a + ar_a_off(m, k / kGroup, (k % kGroup) / 16) + 8 * (lane & 1)) =
+                *reinterpret_cast<uint2*>(s_a + ar_a_off<BM>(m, k / kGroup, (k % kGroup) / 16) + 8 * (lane & 1)) =
                     make_uint2(lo, hi);
                 float t = e4m3_pair_sum(0.f, lo, hi);
                 t = lane_allreduce<4>(t, SumOp{});
                 if ((lane & 15) == 0) {
                     const __bf16 h = (__bf16)t;
-                    s_sah[m * kArGp + k / kGroup] = h;
-                    s_sal[m * kArGp + k / kGroup] = (__bf16)(t - (float)h);
+                    s_sah[m * GPR + k / kGroup] = h;
+                    s_sal[m * GPR + k / kGroup] = (__bf16)(t - (float)h);
                 }
             }
         }
-        for (int i = tid; i < kArBM * kArGp; i += kArThreads) {   // groups >= G are 0
-            if (i % kArGp >= G) {
+        for (int i = tid; i < BM * GPR; i += kArThreads) {   // groups >= G are 0
+            if (i % GPR >= G) {
                 s_sah[i] = (__bf16)0.f;
                 s_sal[i] = (__bf16)0.f;
             }
@@ -368,22 +389,27 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
         for (int u = 0; u < kMaxChunks; ++u) {
             const int c = u * kArThreads + tid;
             if (c < total)
-                *reinterpret_cast<uint4*>(s_a + ar_a_off(c / cpr, (c % cpr) >> 3, c & 7)) = va[u];
+                *reinterpret_cast<uint4*>(s_a + ar_a_off<BM>(c / cpr, (c % cpr) >> 3, c & 7)) = va[u];
         }
 #pragma unroll
-        for (int j = 0; j < kArBM * kArGp / kArThreads; ++j) {
+        for (int j = 0; j < BM * GPR / kArThreads; ++j) {
             const int i = j * kArThreads + tid;
             const __bf16 h = (__bf16)asv[j];
             s_sah[i] = h;
             s_sal[i] = (__bf16)(asv[j] - (float)h);
         }
-        if (wave == 0) s_asc[lane] = ascv;
+        if (wave == 0 && lane < BM) s_asc[lane] = ascv;
     }
-    build(0);
-    if (nranges > 1) prefetch(1);
+    build(0, 0);
+    // the tables' next (range, half), prefetched right after each build
+    auto prefetch_after = [&](int r, int h) __attribute__((always_inline)) {
+        if (h + 1 < GH) prefetch(r, h + 1);
+        else if (r + 1 < nranges) prefetch(r + 1, 0);
+    };
+    prefetch_after(0, 0);
     lds_barrier();
 
-    auto main_loop = [&](auto nflc) {
+    auto main_loop = [&](auto nflc) __attribute__((always_inline)) {
         constexpr int NF = decltype(nflc)::value;
         // Operands go in swapped (weights first), so the MFMAs produce the transposed block:
         // lane (q, c16) of fragment (i, j) holds tile row 16 i + c16, columns 4 q .. 4 q + 3
@@ -396,10 +422,10 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
         // first step has nothing to fold and its second starts the accumulators
         // (run = acc * scale).
         v4f pend[NF][kArNT];
-        auto scales_of = [&](int g) {      // fp16 scales [fragment][column 0..3] of group g
-            return *reinterpret_cast<const uint4*>(s_sc + ((wave * kArGp + g) * 4 + q) * 8);
+        auto scales_of = [&](int g) __attribute__((always_inline)) {      // fp16 scales [fragment][column 0..3] of group g
+            return *reinterpret_cast<const uint4*>(s_sc + ((wave * kArGp + (g & (kArGp - 1))) * 4 + q) * 8);
         };
-        auto fold_one = [&](int i, int j, const uint4& sc, auto modec) {
+        auto fold_one = [&](int i, int j, const uint4& sc, auto modec) __attribute__((always_inline)) {
             constexpr int mode = decltype(modec)::value;
 #pragma unroll
             for (int rr = 0; rr < 4; ++rr) {
@@ -412,7 +438,7 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
         using M0 = std::integral_constant<int, 0>;
         using M1 = std::integral_constant<int, 1>;
         using M2 = std::integral_constant<int, 2>;
-        auto consume = [&](int g, auto slotc, auto modec) {
+        auto consume = [&](int g, auto slotc, auto modec) __attribute__((always_inline)) {
             constexpr int sl = decltype(slotc)::value;
             constexpr int mode = decltype(modec)::value;
             const uint4 sc = mode ? scales_of(g - 1) : make_uint4(0u, 0u, 0u, 0u);
@@ -420,8 +446,8 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
 #pragma unroll
             for (int j = 0; j < kArNT; ++j) bf[j] = spread_nibbles(bw[sl][j]);
             // fragment i's rows are 16 i + c16: same swizzle as row c16, offset i * 2 KB
-            const uint8_t* A0 = s_a + ar_a_off(c16, g, 2 * q);
-            const uint8_t* A1 = s_a + ar_a_off(c16, g, 2 * q + 1);
+            const uint8_t* A0 = s_a + ar_a_off<BM>(c16, g, 2 * q);
+            const uint8_t* A1 = s_a + ar_a_off<BM>(c16, g, 2 * q + 1);
 #pragma unroll
             for (int i = 0; i < NF; ++i) {
                 const uint4 lo = *reinterpret_cast<const uint4*>(A0 + i * 16 * kGroup);
@@ -436,18 +462,15 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
             }
         };
 
-        // Range epilogue: zero-point term of every (row, column) as bf16 MFMAs over the
-        // groups (lane (q, c16), K slot 8q + t <-> group 8 (q & 1) + t: the row operand is
-        // the hi (q < 2) or lo (q >= 2) half of the row's group sum; the column operand the
-        // hi, then lo, half of s*z with slots 16..31 repeating 0..15, so the two MFMAs add
-        // (sa_hi + sa_lo)(sz_hi + sz_lo)); operands swapped as in the main MFMAs), then
-        // out = asc * (512 * run - zero term), stored.
-        auto epilogue = [&](int r) {
-            const uint4 sc = scales_of(G - 1);
-#pragma unroll
-            for (int i = 0; i < NF; ++i)
-#pragma unroll
-                for (int j = 0; j < kArNT; ++j) fold_one(i, j, sc, M2{});
+        // Zero-point term of every (row, column) of a range as bf16 MFMAs over the 16 groups
+        // of table half h (lane (q, c16), K slot 8q + t <-> group 16 h + 8 (q & 1) + t: the
+        // row operand is the hi (q < 2) or lo (q >= 2) half of the row's group sum; the column
+        // operand the hi, then lo, half of s*z with slots 16..31 repeating 0..15, so the two
+        // MFMAs add (sa_hi + sa_lo)(sz_hi + sz_lo)); operands swapped as in the main MFMAs. The
+        // second half of K adds to the first half's result.
+        v4f za[NF], zb[NF];
+        auto zterm = [&](int h, auto firstc) __attribute__((always_inline)) {
+            constexpr bool first = decltype(firstc)::value;
             const __bf16* sa_tab = q < 2 ? s_sah : s_sal;
             const int go = 8 * (q & 1);
             const int lra = 32 * wave + c16, lrb = lra + 16;
@@ -455,22 +478,37 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
             const bf16x8 zal = lds_bf16x8(s_szl + lra * kArGp + go);
             const bf16x8 zbh = lds_bf16x8(s_szh + lrb * kArGp + go);
             const bf16x8 zbl = lds_bf16x8(s_szl + lrb * kArGp + go);
+#pragma unroll
+            for (int i = 0; i < NF; ++i) {
+                const int m = 16 * i + c16;
+                const bf16x8 sa = lds_bf16x8(sa_tab + m * GPR + kArGp * h + go);
+                za[i] = mfma_bf16_16x16x32(zah, sa, first ? v4f{0.f, 0.f, 0.f, 0.f} : za[i]);
+                za[i] = mfma_bf16_16x16x32(zal, sa, za[i]);
+                zb[i] = mfma_bf16_16x16x32(zbh, sa, first ? v4f{0.f, 0.f, 0.f, 0.f} : zb[i]);
+                zb[i] = mfma_bf16_16x16x32(zbl, sa, zb[i]);
+            }
+        };
+        // fold of the last step's MFMA results (group g) into the accumulators
+        auto fold_last = [&](int g) __attribute__((always_inline)) {
+            const uint4 sc = scales_of(g);
+#pragma unroll
+            for (int i = 0; i < NF; ++i)
+#pragma unroll
+                for (int j = 0; j < kArNT; ++j) fold_one(i, j, sc, M2{});
+        };
+        // Range output: out = asc * (512 * run - zero term), stored.
+        auto store_range = [&](int r) __attribute__((always_inline)) {
             const int64_t ldo = kSilu ? ncols : p.N;
             __half* outp = reinterpret_cast<__half*>(p.out) + ar_col<kSilu>(r, wave, 0, 0) + 4 * q;
 #pragma unroll
             for (int i = 0; i < NF; ++i) {
                 const int m = 16 * i + c16;
-                const bf16x8 sa = lds_bf16x8(sa_tab + m * kArGp + go);
-                v4f za = mfma_bf16_16x16x32(zah, sa, v4f{0.f, 0.f, 0.f, 0.f});
-                za = mfma_bf16_16x16x32(zal, sa, za);
-                v4f zb = mfma_bf16_16x16x32(zbh, sa, v4f{0.f, 0.f, 0.f, 0.f});
-                zb = mfma_bf16_16x16x32(zbl, sa, zb);
                 const float av = s_asc[m];
                 float va[4], vb[4];
 #pragma unroll
                 for (int rr = 0; rr < 4; ++rr) {
-                    va[rr] = as_f32(av * (kNibbleScale * run[i][0][rr] - za[rr]));
-                    vb[rr] = as_f32(av * (kNibbleScale * run[i][1][rr] - zb[rr]));
+                    va[rr] = as_f32(av * (kNibbleScale * run[i][0][rr] - za[i][rr]));
+                    vb[rr] = as_f32(av * (kNibbleScale * run[i][1][rr] - zb[i][rr]));
                 }
                 __half* rowp = outp + (row0 + m) * ldo;
                 const bool live = (vmask >> m) & 1;
@@ -493,31 +531,27 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
             }
         };
 
-        // Four steps per pass of the ring (G % 4 == 0), so every pass issues the same loads
-        // and the wait counts stay exact; a range's first pass is written out on its own (its
-        // first two steps fold differently). The next range's tables are requested once per
-        // range, before its loop. The scheduling barriers keep each step's MFMAs next to the
-        // fold that frees their registers instead of hoisting later steps' MFMAs.
-        for (int r = 0; r < nranges; ++r) {
-            // Waves w and w + 4 share a SIMD and the issue arbiter favours one of them; the
-            // higher priority alternates between the two every range, so neither falls a
-            // whole tile behind (the work-group ends with its slowest wave).
-            if (((wave >> 2) ^ r) & 1) __builtin_amdgcn_s_setprio(1);
-            else __builtin_amdgcn_s_setprio(0);
-            if (r > 0 && r + 1 < nranges) prefetch(r + 1);
-            consume(0, S0{}, M0{});
+        // The steps of groups [g0, g1): four per pass of the ring (the halves hold multiples of
+        // 4 groups, G % 4 == 0), so every pass issues the same loads and the wait counts stay
+        // exact; a half's first pass is written out on its own (its first steps fold
+        // differently: the range's first step folds nothing and its second starts the
+        // accumulators; the second half's first step folds nothing, the middle of the range
+        // having folded its predecessor). The scheduling barriers keep each step's MFMAs next
+        // to the fold that frees their registers instead of hoisting later steps' MFMAs.
+        auto run_steps = [&](int g0, int g1, auto second_mode) __attribute__((always_inline)) {
+            consume(g0, S0{}, M0{});
             issue(S0{});
             __builtin_amdgcn_sched_barrier(0);
-            consume(1, S1{}, M1{});
+            consume(g0 + 1, S1{}, second_mode);
             issue(S1{});
             __builtin_amdgcn_sched_barrier(0);
-            consume(2, S2{}, M2{});
+            consume(g0 + 2, S2{}, M2{});
             issue(S2{});
             __builtin_amdgcn_sched_barrier(0);
-            consume(3, S3{}, M2{});
+            consume(g0 + 3, S3{}, M2{});
             issue(S3{});
             __builtin_amdgcn_sched_barrier(0);
-            for (int g = 4; g < G; g += 4) {
+            for (int g = g0 + 4; g < g1; g += 4) {
                 consume(g, S0{}, M2{});
                 issue(S0{});
                 __builtin_amdgcn_sched_barrier(0);
@@ -531,43 +565,84 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
                 issue(S3{});
                 __builtin_amdgcn_sched_barrier(0);
             }
-            epilogue(r);
-            if (r + 1 < nranges) build(r + 1);
+        };
+        using F0 = std::false_type;
+        using F1 = std::true_type;
+        for (int r = 0; r < nranges; ++r) {
+            // Waves w and w + 4 share a SIMD and the issue arbiter favours one of them; the
+            // higher priority alternates between the two every range, so neither falls a
+            // whole tile behind (the work-group ends with its slowest wave).
+            if (((wave >> 2) ^ r) & 1) __builtin_amdgcn_s_setprio(1);
+            else __builtin_amdgcn_s_setprio(0);
+            if constexpr (GH == 1) {
+                run_steps(0, G, M1{});
+                fold_last(G - 1);
+                zterm(0, F1{});
+            } else {
+                // K > 2048: the tables hold one half of K; the middle of the range folds the
+                // first half's last step, takes its zero-point term and rebuilds the tables
+                run_steps(0, kArGp, M1{});
+                fold_last(kArGp - 1);
+                zterm(0, F1{});
+                build(r, 1);
+                prefetch_after(r, 1);
+                run_steps(kArGp, G, M2{});
+                fold_last(G - 1);
+                zterm(1, F0{});
+            }
+            store_range(r);
+            if (r + 1 < nranges) {
+                build(r + 1, 0);
+                prefetch_after(r + 1, 0);
+            }
         }
     };
-    switch (nfl) {
-        case 1: main_loop(std::integral_constant<int, 1>{}); break;
-        case 2: main_loop(std::integral_constant<int, 2>{}); break;
-        case 3: main_loop(std::integral_constant<int, 3>{}); break;
-        default: main_loop(std::integral_constant<int, 4>{}); break;
+    if constexpr (BM == kArBM) {
+        switch (nfl) {
+            case 1: main_loop(std::integral_constant<int, 1>{}); break;
+            case 2: main_loop(std::integral_constant<int, 2>{}); break;
+            case 3: main_loop(std::integral_constant<int, 3>{}); break;
+            default: main_loop(std::integral_constant<int, 4>{}); break;
+        }
+    } else {
+        if (nfl == 1) main_loop(std::integral_constant<int, 1>{});
+        else main_loop(std::integral_constant<int, 2>{});
     }
 }
 
-template <Epi EPI, bool FRAG>
-int launch_ares_t(const Params& p, hipStream_t s) {
-    const size_t lds = ar_lds_bytes(p.K);
+template <Epi EPI, bool FRAG, int BM>
+int launch_ares_bm(const Params& p, hipStream_t s) {
+    const size_t lds = ar_lds_bytes<BM>(p.K);
     static bool attr_set = false;
     if (!attr_set) {   // > 64 KB of dynamic LDS needs an explicit opt-in
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_ares_kernel<EPI, FRAG>),
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_ares_kernel<EPI, FRAG, BM>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)ar_lds_bytes(kArMaxK)) != hipSuccess) {
+                                (int)ar_lds_bytes<BM>(ar_max_k<BM>())) != hipSuccess) {
             set_error("prefill_ares_kernel: cannot reserve dynamic LDS");
             return W4A8_ERR_HIP;
         }
         attr_set = true;
     }
     // a multiple of 8 work-groups covers every tile under the XCD-aware order
-    const int64_t tiles = (p.P + kArBM - 1) / kArBM;
+    const int64_t tiles = (p.P + BM - 1) / BM;
     const unsigned grid = (unsigned)((tiles + kArXcds - 1) / kArXcds * kArXcds);
-    launch_kernel(&prefill_ares_kernel<EPI, FRAG>, dim3(grid), dim3(kArThreads), lds, s, p);
+    launch_kernel(&prefill_ares_kernel<EPI, FRAG, BM>, dim3(grid), dim3(kArThreads), lds, s, p);
     return check_launch("prefill_ares_kernel");
+}
+
+// 64-row tiles up to K = 2048; 32-row tiles (the activation tile halves) up to K = 4096
+template <Epi EPI, bool FRAG>
+int launch_ares_t(const Params& p, hipStream_t s) {
+    return p.K <= kArMaxK ? launch_ares_bm<EPI, FRAG, kArBM>(p, s)       // one table half
+                          : launch_ares_bm<EPI, FRAG, kArBMWide>(p, s);  // two (2048 < K <= 4096)
 }
 
 }  // namespace
 
 bool prefill_ares_supported(int64_t K, int64_t N, int64_t group_size, bool e2m1, int64_t block_m,
                             Epi epi) {
-    if (e2m1 || group_size != kGroup || K % (4 * kGroup) != 0 || K > kArMaxK || block_m % kArBM != 0)
+    if (e2m1 || group_size != kGroup || K % (4 * kGroup) != 0 || K > kArMaxKWide ||
+        block_m % (K <= kArMaxK ? kArBM : kArBMWide) != 0)
         return false;
     if (epi == Epi::kSiluHalf) return N % (2 * ar_range_cols<true>()) == 0;
     if (epi == Epi::kHalf) return N % ar_range_cols<false>() == 0;
@@ -589,8 +664,9 @@ int launch_grouped_prefill_ares(const GroupedArgs& a, hipStream_t s) {
     if (!prefill_ares_supported(a.K, a.N, a.group_size, a.e2m1, a.block_m, a.epi) ||
         !(prequant || self_quant) || a.x_rows * a.K >= ((int64_t)1 << 31)) {
         set_error("prefill (activation-resident): needs g128 int4 weights, K % 512 == 0 and "
-                  "K <= 2048, output columns in whole 256-row ranges, block_m % 64 == 0, fp16 "
-                  "out, and prequantised rows with group sums (or fp16 rows, fp16 out, K <= 1024)");
+                  "K <= 4096, output columns in whole 256-row ranges, block_m % 64 == 0 (32 for "
+                  "K > 2048), fp16 out, and prequantised rows with group sums (or fp16 rows, fp16 "
+                  "out, K <= 1024)");
         return W4A8_ERR_INVALID;
     }
     if (a.w_frag && (a.N % 16 != 0 || (a.epi == Epi::kSiluHalf && (a.N / 2) % 16 != 0))) {

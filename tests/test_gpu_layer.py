@@ -181,6 +181,30 @@ def test_prefill_layer_equals_op_composition(T, frag):
     assert torch.equal(fused, unfused)
 
 
+@pytest.mark.parametrize("H,T,frag", [(4096, 200, True), (3072, 130, False)])
+def test_prefill_wide_k_tiles(H, T, frag):
+    """Hidden sizes above 2048 run gemm1 on the 32-row activation tiles, whose per-range
+    tables are rebuilt in the middle of K (H = 3072: a partial second half of 8 groups):
+    against the oracle, and equal to the op-by-op composition bit for bit."""
+    cfg = dict(T=T, H=H, E=16, k=4, I=512, g=128, routing="uniform")
+    ws = bench.make_weights(cfg, 600 + H, DEV)
+    x, logits = bench.make_inputs(cfg, 601 + H, DEV)
+    tw, ids = W.fused_topk(None, logits, cfg["k"], True)
+    w13, w2 = ws["w13"], ws["w2"]
+    if frag:
+        w13, w2 = W.repack_fragments(w13), W.repack_fragments(w2)
+    out = W.moe_apply(x, w13, w2, ws["s13"], ws["s2"], ws["z13"], ws["z2"], tw, ids)
+    ref = oracle_layer(cfg, ws, x, tw, ids)
+    err = maxrel(out.float().cpu().numpy(), ref)
+    print(f"  H={H} T={T} frag={frag} max rel err {err:.2e}")
+    assert err <= REL_TOL
+    unfused = moe_experts._run_unfused(
+        x.to(torch.float16), ws["w13"], ws["w2"], ws["s13"], ws["s2"], ws["z13"], ws["z2"],
+        tw.reshape(-1).contiguous(), ids, cfg["k"], cfg["E"], None, "wmma", False, None, None,
+        64).to(x.dtype)
+    assert torch.equal(out, unfused)
+
+
 @pytest.mark.parametrize("name", ["c2", "c3", "c4", "c5"])
 def test_baseline_configs_sampled_tokens(name):
     """Full-size BASELINE.json layers; the oracle checks 3 tokens (first, middle, last)."""
