@@ -52,7 +52,7 @@ int check_grouped(int64_t rows, int64_t K, int64_t E, int64_t N, int64_t gs, int
 }
 
 int run_grouped(GroupedArgs& a, int64_t kernel, void* ws, size_t ws_bytes, hipStream_t s) {
-    const bool mfma = mfma_supported(a.K, a.group_size);
+    const bool mfma = mfma_supported(a.K, a.group_size, a.e2m1);
     // E2M1 codebook weights take the matrix-core tiles (the GEMV feeds raw nibbles)
     const bool gemv = gemv_supported(a.K, a.group_size) && !a.e2m1;
     Workspace w(ws, ws_bytes);
@@ -82,9 +82,12 @@ int run_grouped(GroupedArgs& a, int64_t kernel, void* ws, size_t ws_bytes, hipSt
     }
     // gemv for K-group counts outside its split-K table runs the matrix-core tiles
     const bool tiles = (kernel == W4A8_MOE_KERNEL_WMMA || kernel == W4A8_MOE_KERNEL_GEMV) && mfma;
+    // E2M1 tiles take fp4 operands against activations in natural k order; every other
+    // kernel (the scalar one included) takes k8-interleaved activations
+    const bool k8 = !(a.e2m1 && tiles);
     const bool prefill = tiles && prefill_supported(a.K, a.group_size, a.e2m1);
     a.act_group_sums = prefill ? gsum : nullptr;
-    if (int rc = launch_act_quant(a.x, a.x_bf16, a.x_rows, a.K, a.x_fp8, a.act_scales, true, s,
+    if (int rc = launch_act_quant(a.x, a.x_bf16, a.x_rows, a.K, a.x_fp8, a.act_scales, k8, s,
                                   filter ? a.sorted_ids : nullptr, filter ? a.ntp : nullptr,
                                   a.num_valid, a.act_group_sums))
         return rc;
@@ -258,14 +261,17 @@ int moe_apply_impl(const void* x, int x_dtype, int64_t T, int64_t H, int64_t int
     const bool bf16 = x_dtype == W4A8_DTYPE_BF16;
     const bool e2m1 = weight_is_e2m1 != 0;
     const int64_t numel = T * top_k;
-    const bool mfma = mfma_supported(H, group_size) && mfma_supported(inter, group_size);
+    const bool mfma = mfma_supported(H, group_size, e2m1) && mfma_supported(inter, group_size, e2m1);
+    // E2M1 tiles take fp4 operands against activations in natural k order; the scalar
+    // kernel takes k8-interleaved ones
+    const bool k8 = !(e2m1 && mfma);
     // prefill tiles need the per-group sums of the quantised rows (zero-point term)
     const bool pf1 = !pl.decode && mfma && prefill_supported(H, group_size, e2m1);
     const bool pf2 = !pl.decode && mfma && prefill_supported(inter, group_size, e2m1);
     // router: one wave per token over the whole grid (folding it into the align launch
     // would serialise the tokens on the align work-group)
     // many-token schedule: the routing waves also quantise x (one launch less)
-    const bool route_quant = logits != nullptr && !(pl.decode && numel <= kAlignSmallMax);
+    const bool route_quant = logits != nullptr && !(pl.decode && numel <= kAlignSmallMax) && k8;
     if (logits != nullptr)
         if (int rc = launch_topk_softmax(logits, T, n_global, top_k, renormalize,
                                          const_cast<float*>(topk_weights),
@@ -306,7 +312,7 @@ int moe_apply_impl(const void* x, int x_dtype, int64_t T, int64_t H, int64_t int
         stage_mark(7, s);
         return rc;
     }
-    if (pl.decode && numel <= kAlignSmallMax) {
+    if (pl.decode && numel <= kAlignSmallMax && k8) {
         // one launch: align in work-group 0, act-quant of x in the others
         if (int rc = launch_align_quant(topk_ids, numel, E, pl.block_m, expert_map, n_global, sti,
                                         pl.P, eid, ntp, s2r, x, bf16, T, H, xq, s1, nullptr, s))
@@ -318,7 +324,7 @@ int moe_apply_impl(const void* x, int x_dtype, int64_t T, int64_t H, int64_t int
             return rc;
         stage_mark(1, s);
         if (!route_quant)
-            if (int rc = launch_act_quant(x, bf16, T, H, xq, s1, true, s, nullptr, nullptr, 0,
+            if (int rc = launch_act_quant(x, bf16, T, H, xq, s1, k8, s, nullptr, nullptr, 0,
                                           pf1 ? gs1 : nullptr))
                 return rc;
     }
@@ -351,7 +357,7 @@ int moe_apply_impl(const void* x, int x_dtype, int64_t T, int64_t H, int64_t int
     const bool gemv2 = pl.decode && !e2m1 && gemv_supported(inter, group_size);
     const bool ares2 = pf2 && prefill_ares_supported(inter, H, group_size, e2m1, pl.block_m, Epi::kHalf);
     const bool ares2_quant = ares2 && prefill_ares_quantises_rows(inter, Epi::kHalf);
-    if (!ares2_quant && (rc = launch_act_quant(h, false, pl.P, inter, hq, s2, true, s, sti, ntp,
+    if (!ares2_quant && (rc = launch_act_quant(h, false, pl.P, inter, hq, s2, k8, s, sti, ntp,
                                                numel, pf2 ? gs2 : nullptr)))
         return rc;
     stage_mark(5, s);

@@ -135,7 +135,13 @@ struct TileCfg {
     static_assert(MT >= 1 && NT >= 1 && A_CHUNKS >= 1 && B_CHUNKS >= 1, "tile too small");
 };
 
-template <Epi EPI, int BM, int BN>
+// FP4: E2M1 weights enter the MFMA as fp4 operands (raw codes, the f8f6f4 MFMA's e2m1
+// format decodes them), against activations quantised in natural k order; one MFMA per
+// K group of 32, 64 or 128 (the lanes holding other groups' 32-wide K blocks pass zero codes),
+// each folded with its own scale, so a group's partial sum is the same exact sum the scalar
+// kernel forms. Otherwise int4 / E2M1 words are decoded to e4m3 through the tables
+// (k8-interleaved, against k8-interleaved activations).
+template <Epi EPI, int BM, int BN, bool FP4>
 __global__ void __launch_bounds__(256) grouped_mfma_kernel(Params p) {
     using C = TileCfg<EPI, BM, BN>;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -212,7 +218,7 @@ __global__ void __launch_bounds__(256) grouped_mfma_kernel(Params p) {
             const int n = b_n[i];
             b_reg[i] = *reinterpret_cast<const uint4*>(
                 we + (int64_t)n * kw_row + g * (kGroup / 8) + ((tid + i * 256) & 3) * 4);
-            b_tab[i] = table_index(ze, n, g, p.G, p.e2m1);
+            if constexpr (!FP4) b_tab[i] = table_index(ze, n, g, p.G, p.e2m1);
         }
     };
     auto store_group = [&](int buf) {
@@ -228,9 +234,13 @@ __global__ void __launch_bounds__(256) grouped_mfma_kernel(Params p) {
         for (int i = 0; i < C::B_CHUNKS; ++i) {
             const int c = tid + i * 256;
             uint8_t* dst = B + b_row[i] * kLdsStride + (c & 3) * 32;
-            const v8i d = decode_frag(b_reg[i], load_table(b_tab[i]));
-            *reinterpret_cast<uint4*>(dst) = make_uint4(d[0], d[1], d[2], d[3]);
-            *reinterpret_cast<uint4*>(dst + 16) = make_uint4(d[4], d[5], d[6], d[7]);
+            if constexpr (FP4) {
+                *reinterpret_cast<uint4*>(dst) = b_reg[i];   // 32 codes, first half of the slot
+            } else {
+                const v8i d = decode_frag(b_reg[i], load_table(b_tab[i]));
+                *reinterpret_cast<uint4*>(dst) = make_uint4(d[0], d[1], d[2], d[3]);
+                *reinterpret_cast<uint4*>(dst + 16) = make_uint4(d[4], d[5], d[6], d[7]);
+            }
         }
     };
 
@@ -252,16 +262,19 @@ __global__ void __launch_bounds__(256) grouped_mfma_kernel(Params p) {
 #pragma unroll
         for (int j = 0; j < C::NTT; ++j) run[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
+    // K steps of 128; FP4 takes groups of 32, 64 or 128 (gps groups per step)
+    const int nsteps = p.K / kGroup;
+    const int gps = p.G / nsteps;
+    // this lane's 32-wide K block within a step, and the group of the step it belongs to
+    const int lane_grp = FP4 ? (lane >> 4) * gps / 4 : 0;
+
     load_group(0);
     store_group(0);
     __syncthreads();
 
-    for (int g = 0; g < p.G; ++g) {
+    for (int g = 0; g < nsteps; ++g) {
         const int buf = g & 1;
-        if (g + 1 < p.G) load_group(g + 1);
-        float sc[C::NTT];
-#pragma unroll
-        for (int j = 0; j < C::NTT; ++j) sc[j] = __half2float(se[(int64_t)t_srow[j] * p.G + g]);
+        if (g + 1 < nsteps) load_group(g + 1);
 
         const uint8_t* A = lds + buf * (C::LDS_A + C::LDS_B);
         const uint8_t* B = A + C::LDS_A;
@@ -272,26 +285,54 @@ __global__ void __launch_bounds__(256) grouped_mfma_kernel(Params p) {
             const int brow = (C::kSilu && j >= C::NT ? BN : 0) + wn * C::NWC + jj * 16 + (lane & 15);
             const uint8_t* src = B + brow * kLdsStride + (lane >> 4) * 32;
             const uint4 lo = *reinterpret_cast<const uint4*>(src);
-            const uint4 hi = *reinterpret_cast<const uint4*>(src + 16);
-            bf[j] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w,
-                        (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+            if constexpr (FP4) {
+                bf[j] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, 0, 0, 0, 0};
+            } else {
+                const uint4 hi = *reinterpret_cast<const uint4*>(src + 16);
+                bf[j] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w,
+                            (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+            }
         }
+        v8i af[C::MT];
 #pragma unroll
         for (int i = 0; i < C::MT; ++i) {
             const int arow = wm * C::MW + i * 16 + (lane & 15);
-            const uint8_t* src = A + arow * kLdsStride + (lane >> 4) * 32;
+            // against an fp4 operand (lane kb: k 32kb..32kb+31) an fp8 lane kb holds
+            // k 16kb..16kb+15 and 64+16kb..64+16kb+15; fp8 against fp8 pairs element for element
+            const uint8_t* src = A + arow * kLdsStride + (lane >> 4) * (FP4 ? 16 : 32);
             const uint4 lo = *reinterpret_cast<const uint4*>(src);
-            const uint4 hi = *reinterpret_cast<const uint4*>(src + 16);
-            const v8i af = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w,
-                               (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+            const uint4 hi = *reinterpret_cast<const uint4*>(src + (FP4 ? 64 : 16));
+            af[i] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w,
+                        (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+        }
+        for (int sg = 0; sg < gps; ++sg) {   // gps == 1 without FP4
+            const int gi = g * gps + sg;
+            float sc[C::NTT];
+#pragma unroll
+            for (int j = 0; j < C::NTT; ++j) sc[j] = __half2float(se[(int64_t)t_srow[j] * p.G + gi]);
+            v8i bm[C::NTT];
 #pragma unroll
             for (int j = 0; j < C::NTT; ++j) {
-                const v4f acc = mfma_16x16x128(af, bf[j], v4f{0.f, 0.f, 0.f, 0.f});
+                const bool mine = !FP4 || gps == 1 || lane_grp == sg;
 #pragma unroll
-                for (int r = 0; r < 4; ++r) run[i][j][r] = fmaf(acc[r], sc[j], run[i][j][r]);
+                for (int t = 0; t < 8; ++t) bm[j][t] = mine ? bf[j][t] : 0;
+            }
+#pragma unroll
+            for (int i = 0; i < C::MT; ++i) {
+#pragma unroll
+                for (int j = 0; j < C::NTT; ++j) {
+                    v4f acc;
+                    if constexpr (FP4)
+                        acc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                            af[i], bm[j], v4f{0.f, 0.f, 0.f, 0.f}, 0, 4, 0, 0, 0, 0);
+                    else
+                        acc = mfma_16x16x128(af[i], bm[j], v4f{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) run[i][j][r] = fmaf(acc[r], sc[j], run[i][j][r]);
+                }
             }
         }
-        if (g + 1 < p.G) store_group(buf ^ 1);
+        if (g + 1 < nsteps) store_group(buf ^ 1);
         __syncthreads();
     }
 
@@ -792,12 +833,12 @@ int launch_scalar_t(const Params& p, hipStream_t s) {
     return check_launch("grouped_scalar_kernel");
 }
 
-template <Epi EPI, int BM, int BN>
+template <Epi EPI, int BM, int BN, bool FP4>
 int launch_mfma_t(const Params& p, hipStream_t s) {
     using C = TileCfg<EPI, BM, BN>;
     static bool attr_set = false;   // > 64 KB dynamic LDS needs an explicit opt-in
     if (!attr_set) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&grouped_mfma_kernel<EPI, BM, BN>),
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&grouped_mfma_kernel<EPI, BM, BN, FP4>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize,
                                 C::LDS_BYTES) != hipSuccess) {
             set_error("grouped_mfma_kernel: cannot reserve dynamic LDS");
@@ -807,19 +848,30 @@ int launch_mfma_t(const Params& p, hipStream_t s) {
     }
     const int ncols = EPI == Epi::kSiluHalf ? p.N / 2 : p.N;
     dim3 grid((unsigned)((ncols + BN - 1) / BN), (unsigned)((p.P + BM - 1) / BM));
-    grouped_mfma_kernel<EPI, BM, BN><<<grid, 256, C::LDS_BYTES, s>>>(p);
+    grouped_mfma_kernel<EPI, BM, BN, FP4><<<grid, 256, C::LDS_BYTES, s>>>(p);
     return check_launch("grouped_mfma_kernel");
 }
 
 // The work-group tile height must divide block_m so every tile lies in one expert block.
 template <Epi EPI>
-int launch_mfma_e(const Params& p, hipStream_t s) {
-    if (p.block_m % 128 == 0) return launch_mfma_t<EPI, 128, 64>(p, s);
-    if (p.block_m % 64 == 0) return launch_mfma_t<EPI, 64, 64>(p, s);
-    if (p.block_m % 32 == 0) return launch_mfma_t<EPI, 32, 64>(p, s);
-    if (p.block_m % 16 == 0) return launch_mfma_t<EPI, 16, 64>(p, s);
+int launch_mfma_b(const Params& p, hipStream_t s) {
+    if (p.e2m1) {
+        if (p.block_m % 128 == 0) return launch_mfma_t<EPI, 128, 64, true>(p, s);
+        if (p.block_m % 64 == 0) return launch_mfma_t<EPI, 64, 64, true>(p, s);
+        if (p.block_m % 32 == 0) return launch_mfma_t<EPI, 32, 64, true>(p, s);
+        if (p.block_m % 16 == 0) return launch_mfma_t<EPI, 16, 64, true>(p, s);
+    } else {
+        if (p.block_m % 128 == 0) return launch_mfma_t<EPI, 128, 64, false>(p, s);
+        if (p.block_m % 64 == 0) return launch_mfma_t<EPI, 64, 64, false>(p, s);
+        if (p.block_m % 32 == 0) return launch_mfma_t<EPI, 32, 64, false>(p, s);
+        if (p.block_m % 16 == 0) return launch_mfma_t<EPI, 16, 64, false>(p, s);
+    }
     set_error("wmma grouped GEMM: block_m must be a multiple of 16");
     return W4A8_ERR_INVALID;
+}
+template <Epi EPI>
+int launch_mfma_e(const Params& p, hipStream_t s) {
+    return launch_mfma_b<EPI>(p, s);
 }
 
 // Split of the K groups over waves: G == GPW * KSPLIT for the shapes below; others run
@@ -915,7 +967,9 @@ bool gemv_supported(int64_t K, int64_t group_size) {
     return mfma_supported(K, group_size) && gemv_split((int)(K / group_size)).gpw > 0;
 }
 
-bool mfma_supported(int64_t K, int64_t group_size) {
+bool mfma_supported(int64_t K, int64_t group_size, bool e2m1) {
+    // E2M1 runs fp4 operands with one MFMA per group of 32, 64 or 128
+    if (e2m1) return (group_size == 32 || group_size == 64 || group_size == kGroup) && K % kGroup == 0;
     return group_size == kGroup && K % kGroup == 0;
 }
 

@@ -169,7 +169,8 @@ int launch_grouped_prefill(const GroupedArgs& a, hipStream_t stream);
 bool prefill_supported(int64_t K, int64_t group_size, bool e2m1);   // g128, K <= 4096, no E2M1
 // Same, with an explicit column-tile count per wave team (0 = default heuristic).
 int launch_grouped_gemv_tpt(const GroupedArgs& a, int tiles_per_team, hipStream_t stream);
-bool mfma_supported(int64_t K, int64_t group_size);
+// the matrix-core tiles take the shape (int4: group 128; E2M1: groups of 32, 64 or 128)
+bool mfma_supported(int64_t K, int64_t group_size, bool e2m1 = false);
 // mfma_supported and K / group_size in {1,2,3,4,8,12,16,32} (split-K table of the GEMV)
 bool gemv_supported(int64_t K, int64_t group_size);
 

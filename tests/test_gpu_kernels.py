@@ -210,6 +210,41 @@ def test_moe_gemm_vs_oracle(kernel, asym, case):
     assert maxrel(got, ref[valid]) <= REL_TOL
 
 
+E2M1_CASES = [
+    # (T, E, N, K, top_k, block_m, g): mxfp4's block of 32, 64 and 128-wide groups
+    (64, 8, 128, 256, 2, 16, 32),
+    (40, 8, 256, 1024, 4, 64, 32),
+    (32, 4, 256, 512, 2, 32, 64),
+    (128, 8, 512, 1024, 2, 128, 128),
+]
+
+
+@pytest.mark.parametrize("case", E2M1_CASES)
+def test_e2m1_fp4_tiles_equal_scalar(case):
+    """E2M1 weights on the matrix-core tiles take fp4 MFMA operands (the f8f6f4 MFMA decodes
+    the raw codes; one MFMA per K group of 32, 64 or 128, each folded with its scale). Both
+    the tiles and the scalar golden kernel match the oracle's E2M1 codebook GEMM
+    (tile_config.h:59-71), and each other to fp32 summation order: e4m3 x e2m1 products
+    span more than fp32's 24 bits, so the MFMA's internal sum and the scalar fmaf chain may
+    round differently, within 2e-3 of the output's range."""
+    T, E, N, K, k, bm, g = case
+    r = rng(sum(case) + 7)
+    codes = r.integers(0, 16, (E, N, K))
+    w = O.pack_nibbles(codes)
+    sc = r.uniform(0.005, 0.02, (E, N, K // g)).astype(np.float16)
+    x = r.standard_normal((T, K)).astype(np.float16)
+    ids = np.stack([r.permutation(E)[:k] for _ in range(T)]).astype(np.int32)
+    sti, eid, ntp = O.moe_align(ids, bm, E)
+    xd, wd, scd, stid, eidd, ntpd = to_dev(x, w, sc, sti, eid, ntp)
+    outs = {kern: W.mmq_fp8_moe_gemm(xd, wd, scd, stid, eidd, ntpd, k, bm, kernel=kern,
+                                     weight_is_e2m1=True) for kern in ("scalar", "wmma")}
+    ref, valid = O.grouped_gemm_padded(x, w, sc, None, sti, eid, ntp, k, bm, e2m1=True)
+    got = outs["wmma"].cpu().numpy()[valid]
+    assert maxrel(outs["scalar"].cpu().numpy()[valid], ref[valid]) <= REL_TOL
+    assert maxrel(got, ref[valid]) <= REL_TOL
+    assert maxrel(got, outs["scalar"].cpu().numpy()[valid]) <= 2e-3
+
+
 @pytest.mark.parametrize("case", [(32, 8, 512, 2048, 8, 16, 128), (24, 16, 256, 512, 4, 16, 128),
                                   (9, 8, 384, 1024, 2, 32, 128), (40, 8, 256, 1536, 2, 64, 128)])
 def test_gemv_in_kernel_quant_matches_prequant(case):
