@@ -1,6 +1,8 @@
 // C ABI entry points (include/w4a8_moe.h): argument validation mirroring the reference's
 // TORCH_CHECKs (w4a8_fp8_wmma/bindings.cpp), workspace carving, kernel-id dispatch and the
 // whole-layer composition (moe_experts.py:493-665).
+#include <atomic>
+#include <cstdlib>
 #include <mutex>
 #include <string>
 
@@ -151,7 +153,7 @@ void carve_apply(WS& w, const ApplyPlan& pl, int64_t T, int64_t H, int64_t inter
                  int64_t top_k, int32_t** sti, int32_t** eid, int32_t** ntp, void** align_ws,
                  size_t* align_bytes, uint8_t** xq, float** s1, __half** h, uint8_t** hq,
                  float** s2, float** acc, float** gs1, float** gs2, __half** y,
-                 int32_t** s2r) {
+                 int32_t** s2r, uint64_t** dflags) {
     *sti = w.template take<int32_t>((size_t)pl.P);
     *eid = w.template take<int32_t>((size_t)pl.nblk);
     *ntp = w.template take<int32_t>(1);
@@ -170,6 +172,24 @@ void carve_apply(WS& w, const ApplyPlan& pl, int64_t T, int64_t H, int64_t inter
     // prefill: per-group sums of the quantised rows (zero-point term of the tiles)
     *gs1 = pl.decode ? nullptr : w.template take<float>((size_t)(T * ((H + 127) / 128)));
     *gs2 = pl.decode ? nullptr : w.template take<float>((size_t)(pl.P * ((inter + 127) / 128)));
+    // decode: completion flags of the fused layer's work-groups and its timeout marker
+    *dflags = pl.decode ? w.template take<uint64_t>((size_t)(kDecodeFlagSlots + 1)) : nullptr;
+}
+
+// Per-call value of the fused decode layer's completion flags (never 0).
+uint64_t next_decode_nonce() {
+    static std::atomic<uint64_t> counter{0x9E3779B97F4A7C15ull};
+    uint64_t v = counter.fetch_add(1, std::memory_order_relaxed);
+    return v == 0 ? counter.fetch_add(1, std::memory_order_relaxed) : v;
+}
+
+// W4A8_DECODE_FUSED=1 runs the decode layer's two GEMVs as one launch (decode_layer_kernel).
+// Off by default: on MI355X it measures slower than the two launches (the in-kernel wait for
+// h through agent-coherent loads costs more than the launch boundary it removes). Read on
+// every call, so a process can switch it.
+bool decode_fused_enabled() {
+    const char* v = std::getenv("W4A8_DECODE_FUSED");
+    return v != nullptr && v[0] == '1';
 }
 
 constexpr int kStageEvents = 8;
@@ -252,8 +272,9 @@ int moe_apply_impl(const void* x, int x_dtype, int64_t T, int64_t H, int64_t int
     Workspace w(workspace, workspace_bytes);
     int32_t *sti, *eid, *ntp; void* aws; size_t abytes; uint8_t* xq; float* s1; __half* h;
     uint8_t* hq; float* s2; float* acc; float* gs1; float* gs2; __half* y; int32_t* s2r;
+    uint64_t* dflags;
     carve_apply(w, pl, T, H, inter, E, top_k, &sti, &eid, &ntp, &aws, &abytes, &xq, &s1, &h, &hq,
-                &s2, &acc, &gs1, &gs2, &y, &s2r);
+                &s2, &acc, &gs1, &gs2, &y, &s2r, &dflags);
     if (workspace == nullptr || !w.ok()) {
         set_error("moe_apply: workspace smaller than w4a8_moe_apply_workspace_size()");
         return W4A8_ERR_WORKSPACE;
@@ -293,22 +314,39 @@ int moe_apply_impl(const void* x, int x_dtype, int64_t T, int64_t H, int64_t int
         d.a = x; d.a_bf16 = bf16; d.silu = true;
         d.w = w13; d.scales = w13_scales_f16; d.zeros = w13_zeros; d.out = h;
         d.K = H; d.N = 2 * inter;
-        stamp_gemm(0);
-        int rc = launch_decode_gemv(d, s);
-        stamp_gemm(-1);
-        if (rc) return rc;
-        stage_mark(4, s);
-        stage_mark(5, s);
-        d.a = h; d.a_bf16 = false; d.silu = false;
-        d.w = w2; d.scales = w2_scales_f16; d.zeros = w2_zeros; d.out = acc;
-        d.K = inter; d.N = H;
-        stamp_gemm(1);
-        rc = launch_decode_gemv(d, s);
-        stamp_gemm(-1);
-        if (rc) return rc;
+        DecodeLaunch d2 = d;
+        d2.a = h; d2.a_bf16 = false; d2.silu = false;
+        d2.w = w2; d2.scales = w2_scales_f16; d2.zeros = w2_zeros; d2.out = acc;
+        d2.K = inter; d2.N = H;
+        SlotReduceSync sync;
+        int rc;
+        if (decode_fused_enabled() && decode_layer_fused_supported(H, inter)) {
+            // one launch for both GEMVs; the slot reduce resets the completion flags
+            sync.flags = dflags;
+            sync.nflags = (int)kDecodeFlagSlots;
+            sync.timeout = dflags + kDecodeFlagSlots;
+            sync.nonce = next_decode_nonce();
+            stamp_gemm(0);
+            rc = launch_decode_layer(d, d2, dflags, sync.nonce, dflags + kDecodeFlagSlots, s);
+            stamp_gemm(-1);
+            if (rc) return rc;
+            stage_mark(4, s);
+            stage_mark(5, s);
+        } else {
+            stamp_gemm(0);
+            rc = launch_decode_gemv(d, s);
+            stamp_gemm(-1);
+            if (rc) return rc;
+            stage_mark(4, s);
+            stage_mark(5, s);
+            stamp_gemm(1);
+            rc = launch_decode_gemv(d2, s);
+            stamp_gemm(-1);
+            if (rc) return rc;
+        }
         stage_mark(6, s);
         rc = launch_slot_reduce(acc, topk_weights, topk_ids, expert_map, n_global, E, T, H, top_k,
-                                out, bf16, s);
+                                out, bf16, s, sync);
         stage_mark(7, s);
         return rc;
     }
@@ -670,9 +708,9 @@ size_t w4a8_moe_apply_workspace_size(int64_t T, int64_t H, int64_t inter, int64_
     const ApplyPlan pl = plan_apply(T, E, top_k);
     SizeProbe sp;
     int32_t *a, *b, *c; void* d; size_t db; uint8_t* e; float* f; __half* g; uint8_t* h;
-    float *i, *j, *k, *l; __half* m; int32_t* n;
+    float *i, *j, *k, *l; __half* m; int32_t* n; uint64_t* o;
     carve_apply(sp, pl, T, H, inter, E, top_k, &a, &b, &c, &d, &db, &e, &f, &g, &h, &i, &j, &k,
-                &l, &m, &n);
+                &l, &m, &n, &o);
     return sp.s.used;
 }
 

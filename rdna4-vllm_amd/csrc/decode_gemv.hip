@@ -58,15 +58,20 @@ struct DecodeLists {
     int16_t first[kDecMaxExperts + 1];     // its slots are slot[first[r] .. first[r + 1])
     int16_t slot[kDecMaxSlots];
     int cnt[kDecMaxExperts];
-    int cost[kDecMaxExperts + 1];          // work before touched expert r (partition units)
+    int pp[kDecMaxExperts + 1];            // 16-row passes of the touched experts before r
     int wtot[3][kDecThreads / 64];
 };
 
+// Partition cost of the work before touched expert r for a GEMM with upe column units per
+// expert: every 16-row pass streams the upe units once and starts with a row load charged
+// as kDecPassCost units.
+__device__ __forceinline__ int dec_cost(const DecodeLists& L, int r, int upe) {
+    return L.pp[r] * (upe + kDecPassCost);
+}
+
 // Touched experts and their slot lists (the align's grouping, without padding) in LDS, and
-// the work of each touched expert for the partition: every 16-row pass over the expert's
-// upe column units streams their weights once and starts with an activation-row load,
-// charged as kDecPassCost units.
-__device__ void build_lists(const DecodeParams& p, int upe, DecodeLists& L) {
+// the number of 16-row passes before each touched expert (the partition cost, dec_cost).
+__device__ void build_lists(const DecodeParams& p, DecodeLists& L) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     constexpr int kPer = kDecMaxSlots / kDecThreads;
     for (int e = tid; e < p.E; e += kDecThreads) L.cnt[e] = 0;
@@ -83,7 +88,7 @@ __device__ void build_lists(const DecodeParams& p, int upe, DecodeLists& L) {
     for (int i = 0; i < kPer; ++i)
         if (es[i] >= 0) atomicAdd(&L.cnt[es[i]], 1);
     __syncthreads();
-    // exclusive scans of (slots, touched, work) over experts; thread t owns experts 4t .. 4t + 3
+    // exclusive scans of (slots, touched, passes) over experts; thread t owns experts 4t .. 4t + 3
     int c[4], tot = 0, tch = 0, twk = 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -91,7 +96,7 @@ __device__ void build_lists(const DecodeParams& p, int upe, DecodeLists& L) {
         c[j] = e < p.E ? L.cnt[e] : 0;
         tot += c[j];
         tch += c[j] > 0 ? 1 : 0;
-        twk += ((c[j] + 15) >> 4) * (upe + kDecPassCost);
+        twk += (c[j] + 15) >> 4;
     }
     int it = tot, ic = tch, iw = twk;
 #pragma unroll
@@ -121,8 +126,8 @@ __device__ void build_lists(const DecodeParams& p, int upe, DecodeLists& L) {
         if (c[j] > 0) {
             L.expert[r] = (int16_t)e;
             L.first[r] = (int16_t)off;
-            L.cost[r] = wk;
-            wk += ((c[j] + 15) >> 4) * (upe + kDecPassCost);
+            L.pp[r] = wk;
+            wk += (c[j] + 15) >> 4;
             ++r;
         }
         if (e < p.E) L.cnt[e] = off;     // becomes the fill cursor of expert e
@@ -131,7 +136,7 @@ __device__ void build_lists(const DecodeParams& p, int upe, DecodeLists& L) {
     if (tid == kDecThreads - 1) {
         L.n_touched = r;
         L.first[r] = (int16_t)off;
-        L.cost[r] = wk;
+        L.pp[r] = wk;
     }
     __syncthreads();
 #pragma unroll
@@ -146,14 +151,14 @@ __device__ int unit_at_cost(const DecodeLists& L, int n_t, int upe, int X) {
     const int lane = threadIdx.x & 63;
     const int step = (n_t + 64) / 64;       // candidates cost[0], cost[step], ... cover [0, n_t]
     int cand = lane * step;
-    uint64_t m = __ballot(cand <= n_t && L.cost[cand] <= X);    // bit 0: cost[0] = 0 <= X
+    uint64_t m = __ballot(cand <= n_t && dec_cost(L, cand, upe) <= X);   // bit 0: cost 0 <= X
     const int base = (63 - __clzll(m)) * step;
     cand = base + lane;
-    m = __ballot(lane < step && cand <= n_t && L.cost[cand] <= X);
+    m = __ballot(lane < step && cand <= n_t && dec_cost(L, cand, upe) <= X);
     const int r = base + 63 - __clzll(m);    // largest r with cost[r] <= X
     if (r >= n_t) return n_t * upe;
     const int np = ((int)L.first[r + 1] - (int)L.first[r] + 15) >> 4;
-    const int d = X - L.cost[r] - np * kDecPassCost;
+    const int d = X - dec_cost(L, r, upe) - np * kDecPassCost;
     const int k = d <= 0 ? 0 : (d + np - 1) / np;
     return r * upe + min(k, upe);
 }
@@ -215,27 +220,72 @@ struct DecCursor {
     int r, e, m0, u, b;
 };
 
-template <Epi EPI, int GPW, int KSPLIT, bool ABF16>
-__global__ void __launch_bounds__(kDecThreads, 1) decode_gemv_kernel(DecodeParams p) {
-    using C = DecCfg<EPI, GPW, KSPLIT>;
-    __shared__ DecodeLists L;
-    __shared__ float s_amax[4][16];
-    extern __shared__ __attribute__((aligned(16))) uint8_t s_dyn[];
-    v4f* s_part = reinterpret_cast<v4f*>(s_dyn);
+// In-kernel dependency of the fused layer's second GEMM on its first (decode_layer_kernel),
+// on the agent-scope operations of the memory model only. Work-group w of the first GEMM
+// stores `nonce` to flags[w] with release semantics at agent scope (its L2 written back)
+// once every h row it writes is stored. A team of the second GEMM reads its rows only after
+// every work-group that wrote a unit of the touched experts in its range has published, and
+// reads flags and rows with agent-coherent loads (sc1, the loads of agent-scope atomics),
+// which do not return lines another XCD's L2 may hold stale. The first GEMM's partition is
+// a pure function of the lists, so its writers of an expert are computed, not recorded.
+struct DecDep {
+    const uint64_t* flags;    // one per work-group of the first GEMM
+    uint64_t nonce;           // this call's value (never 0; the slot reduce resets flags to 0)
+    int upe1;                 // column units per expert of the first GEMM
+    int teams1;               // teams per work-group of the first GEMM
+    uint64_t* timeout;        // set to nonce when a wait gave up (bounded spin; not expected)
+};
+constexpr int kDecSpinLimit = 1 << 20;   // polls before a wait gives up (~1 s)
 
+// Last team of a GEMM partition (n teams over W cost units, team t starting at
+// floor(W t / n)) whose start is at or before cost S: the team that runs the unit starting at S.
+__device__ __forceinline__ int dec_owner(int S, int W, int n) {
+    const int t = (int)((((int64_t)S + 1) * n - 1) / W);
+    return min(t, n - 1);
+}
+
+// 8 bytes of a completion flag, agent-coherent
+__device__ __forceinline__ uint64_t dec_flag(const uint64_t* flags, int w) {
+    return __hip_atomic_load(flags + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// 16 bytes of activation row: plain, or (DEP) agent-coherent (buffer load with sc1) for rows
+// written earlier in the same kernel by other work-groups
+template <bool DEP>
+__device__ __forceinline__ uint4 dec_row16(const uint16_t* base, int64_t elem) {
+    if constexpr (DEP) {
+        using u32x4 = unsigned __attribute__((ext_vector_type(4)));
+        const auto rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), (short)0,
+                                                            0x7FFFFFFF, 0x00020000);
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, (int)(elem * 2), 0, kCpolSc1);
+        return make_uint4(v.x, v.y, v.z, v.w);
+    } else {
+        return *reinterpret_cast<const uint4*>(base + elem);
+    }
+}
+
+// L2 warm-up of the activation rows (one 128-byte line per lane; work-group b runs on XCD
+// b % 8): they are cold (h was just written on other XCDs) and the row loads of a pass start
+// are on the critical path. The value is only kept alive (dec_keep), never used.
+__device__ __forceinline__ uint32_t dec_warm(const DecodeParams& p) {
+    const int nrows = p.a_per_token ? p.numel / p.top_k : p.numel;
+    const int lines = (int)(((int64_t)nrows * p.K * 2 + 127) / 128);
+    const int idx = ((int)(blockIdx.x / 8) * 4 + (int)(threadIdx.x >> 6)) * 64 + (int)(threadIdx.x & 63);
+    return lines > 0 ? reinterpret_cast<const uint32_t*>(p.a)[(int64_t)min(idx, lines - 1) * 32] : 0u;
+}
+// keeps the warm-up load (its value never matches: a NaN pattern in a block that does not exist)
+__device__ __forceinline__ void dec_keep(uint32_t warm, void* out) {
+    if (warm == 0x7FC00001u && blockIdx.x == 0x7FFFFFFFu) reinterpret_cast<uint32_t*>(out)[0] = warm;
+}
+
+// One GEMM of the layer over the lists L by the whole grid (the body of decode_gemv_kernel).
+// DEP: the activation rows are h written by the first GEMM of the same kernel (DecDep).
+template <Epi EPI, int GPW, int KSPLIT, bool ABF16, bool DEP>
+__device__ __forceinline__ void dec_run(const DecodeParams& p, const DecodeLists& L,
+                                        float (&s_amax)[4][16], v4f* s_part, const DecDep& dep) {
+    using C = DecCfg<EPI, GPW, KSPLIT>;
     const int ncols = C::kSilu ? p.N / 2 : p.N;
     const int upe = ncols / (16 * C::CT);                 // units per expert
-    // Warm this XCD's L2 with the activation rows (one 128-byte line per lane; work-group b
-    // runs on XCD b % 8): they are cold (h was just written on other XCDs) and the row loads
-    // of a pass start are on the critical path. The value is only kept alive, never used.
-    uint32_t warm;
-    {
-        const int nrows = p.a_per_token ? p.numel / p.top_k : p.numel;
-        const int lines = (int)(((int64_t)nrows * p.K * 2 + 127) / 128);
-        const int idx = ((int)(blockIdx.x / 8) * 4 + (int)(threadIdx.x >> 6)) * 64 + (int)(threadIdx.x & 63);
-        warm = lines > 0 ? reinterpret_cast<const uint32_t*>(p.a)[(int64_t)min(idx, lines - 1) * 32] : 0u;
-    }
-    build_lists(p, upe, L);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -248,7 +298,7 @@ __global__ void __launch_bounds__(kDecThreads, 1) decode_gemv_kernel(DecodeParam
     const int nteams = (int)gridDim.x * C::TEAMS;
     const int tm = (int)blockIdx.x * C::TEAMS + team;
     // team tm starts at work floor(W tm / nteams), in 32-bit arithmetic (W < 2^25)
-    const int work = L.cost[n_t];
+    const int work = dec_cost(L, n_t, upe);
     const int wq = work / nteams, wr = work % nteams;
     auto work_at = [&](int t) { return wq * t + wr * t / nteams; };
     const int ua = __builtin_amdgcn_readfirstlane(unit_at_cost(L, n_t, upe, work_at(tm)));
@@ -328,12 +378,43 @@ __global__ void __launch_bounds__(kDecThreads, 1) decode_gemv_kernel(DecodeParam
         const int mreal = min(16, (int)L.first[c.r + 1] - s0);
         const int my_slot = L.slot[s0 + min(c16, mreal - 1)];
         const int arow = p.a_per_token ? my_slot / p.top_k : my_slot;
-        const uint16_t* xr = reinterpret_cast<const uint16_t*>(p.a) + (int64_t)arow * p.K + q * 32;
+        const int64_t xr = (int64_t)arow * p.K + q * 32;
 #pragma unroll
         for (int g = 0; g < GPW; ++g)
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                raw[g][i] = reinterpret_cast<const uint4*>(xr + (g0 + g) * kGroup)[i];
+                raw[g][i] = dec_row16<DEP>(reinterpret_cast<const uint16_t*>(p.a),
+                                           xr + (g0 + g) * kGroup + i * 8);
+    };
+    // DEP: wait until every work-group of the first GEMM that wrote a unit of the touched
+    // experts in this team's range has published its rows. Lane i polls work-group
+    // w_lo + i (+ 64 j); the partition is the first GEMM's (same lists, upe1 units).
+    // work-groups [w_lo, w_hi] of the first GEMM that wrote units of the touched experts in
+    // this team's range (its partition over the same lists, upe1 units an expert)
+    auto producers = [&](int& w_lo, int& w_hi) __attribute__((always_inline)) {
+        const int r_a = ua / upe, r_b = (ub - 1) / upe;
+        const int n1 = (int)gridDim.x * dep.teams1;
+        const int w1 = dec_cost(L, n_t, dep.upe1);
+        // start costs of the first unit of r_a and the last unit of r_b in the first GEMM
+        const int np_a = ((int)L.first[r_a + 1] - (int)L.first[r_a] + 15) >> 4;
+        const int np_b = ((int)L.first[r_b + 1] - (int)L.first[r_b] + 15) >> 4;
+        const int s_lo = dec_cost(L, r_a, dep.upe1) + np_a * kDecPassCost;
+        const int s_hi = dec_cost(L, r_b, dep.upe1) + np_b * (kDecPassCost + dep.upe1 - 1);
+        w_lo = dec_owner(s_lo, w1, n1) / dep.teams1;
+        w_hi = dec_owner(s_hi, w1, n1) / dep.teams1;
+    };
+    // wait until work-groups w_lo .. w_hi (lane i: w_lo + i + 64 j) have published
+    auto wait_rows = [&](int w_lo, int w_hi) __attribute__((always_inline)) {
+        for (int w0 = w_lo; w0 <= w_hi; w0 += 64) {
+            const int w = w0 + lane;
+            bool ok = w > w_hi;
+            for (int spin = 0; spin < kDecSpinLimit; ++spin) {
+                if (!ok) ok = dec_flag(dep.flags, w) == dep.nonce;
+                if (__ballot(!ok) == 0) break;
+                __builtin_amdgcn_s_sleep(2);
+            }
+            if (__ballot(!ok) != 0 && lane == 0) *dep.timeout = dep.nonce;
+        }
     };
     // quantise the pass's rows, bit-identical to act_quant_kernel: absmax on the magnitude
     // bits (both conversions are monotone in them; NaNs, which fmaxf skips, count as 0), then
@@ -523,7 +604,18 @@ __global__ void __launch_bounds__(kDecThreads, 1) decode_gemv_kernel(DecodeParam
     DecCursor ic = cc;
 #pragma unroll
     for (int f = 0; f < C::FR; ++f) run[f] = v4f{0.f, 0.f, 0.f, 0.f};
-    load_rows(cc);
+    // DEP: the first poll of the producers' flags goes out, then the weight ring (weights do
+    // not depend on the first GEMM), then the wait and the rows. The memory counter completes
+    // in order, so reading the poll's result leaves the ring's loads in flight.
+    int w_lo = 0, w_hi = -1;
+    uint64_t fl0 = 0;
+    if constexpr (DEP) {
+        producers(w_lo, w_hi);
+        // unconditional (a clamped address): a load under a branch gets its wait at the join
+        fl0 = dec_flag(dep.flags, w_lo + min(lane, w_hi - w_lo));
+    } else {
+        load_rows(cc);
+    }
     __builtin_amdgcn_sched_barrier(0);
     issue(ic, S0{}); advance(ic);
     __builtin_amdgcn_sched_barrier(0);
@@ -534,6 +626,11 @@ __global__ void __launch_bounds__(kDecThreads, 1) decode_gemv_kernel(DecodeParam
     if constexpr (C::D > 3) {
         issue(ic, S3{}); advance(ic);
         __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (DEP) {
+        if (w_hi - w_lo >= 64 || __ballot(lane <= w_hi - w_lo && fl0 != dep.nonce) != 0)
+            wait_rows(w_lo, w_hi);
+        load_rows(cc);
     }
     quantize(cc);
 
@@ -564,9 +661,41 @@ __global__ void __launch_bounds__(kDecThreads, 1) decode_gemv_kernel(DecodeParam
         for (int k = 0; k < C::D - 1; ++k)
             if (k % C::NB == C::NB - 1 && k < rem) flush_slot(k);
     }
-    // keeps the L2 warm-up load (its value never matches: a NaN pattern in a block that does
-    // not exist)
-    if (warm == 0x7FC00001u && blockIdx.x == 0x7FFFFFFFu) reinterpret_cast<uint32_t*>(p.out)[0] = warm;
+}
+
+template <Epi EPI, int GPW, int KSPLIT, bool ABF16>
+__global__ void __launch_bounds__(kDecThreads, 1) decode_gemv_kernel(DecodeParams p) {
+    __shared__ DecodeLists L;
+    __shared__ float s_amax[4][16];
+    extern __shared__ __attribute__((aligned(16))) uint8_t s_dyn[];
+    const uint32_t warm = dec_warm(p);
+    build_lists(p, L);
+    dec_run<EPI, GPW, KSPLIT, ABF16, false>(p, L, s_amax, reinterpret_cast<v4f*>(s_dyn), DecDep{});
+    dec_keep(warm, p.out);
+}
+
+// The decode layer's two GEMVs in one launch: gemm1 + SiLU*mul over x (h rows per slot),
+// then gemm2 over h (fp32 rows per slot), on the same lists. Each work-group publishes its
+// gemm1 rows (flags[blockIdx.x] = nonce) before its gemm2 part, whose weight ring fills
+// while it waits for the rows it reads (DecDep). Every wait is bounded, so every wave
+// reaches the end; one work-group per CU, all resident.
+template <int GPW1, int KS1, int GPW2, int KS2, bool ABF16>
+__global__ void __launch_bounds__(kDecThreads, 1) decode_layer_kernel(DecodeParams p1, DecodeParams p2,
+                                                                      DecDep dep) {
+    __shared__ DecodeLists L;
+    __shared__ float s_amax[4][16];
+    extern __shared__ __attribute__((aligned(16))) uint8_t s_dyn[];
+    const uint32_t warm = dec_warm(p1);
+    build_lists(p1, L);
+    dec_run<Epi::kSiluHalf, GPW1, KS1, ABF16, false>(p1, L, s_amax, reinterpret_cast<v4f*>(s_dyn), dep);
+    // every wave's h stores complete (vmcnt(0)), then one release at agent scope publishes them
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __syncthreads();
+    if (threadIdx.x == 0)
+        __hip_atomic_store(const_cast<uint64_t*>(dep.flags) + blockIdx.x, dep.nonce,
+                           __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    dec_run<Epi::kSlotF32, GPW2, KS2, false, true>(p2, L, s_amax, reinterpret_cast<v4f*>(s_dyn), dep);
+    dec_keep(warm, p2.out);
 }
 
 struct DecSplit {
@@ -641,16 +770,55 @@ int launch_dec_e(const DecodeParams& p, hipStream_t s) {
     return W4A8_ERR_INVALID;
 }
 
-}  // namespace
-
-bool decode_layer_supported(int64_t numel, int64_t E, int64_t H, int64_t inter, int64_t gs) {
-    return numel <= kDecMaxSlots && E <= kDecMaxExperts && gs == kGroup && H % kGroup == 0 &&
-           inter % kGroup == 0 && dec_split((int)(H / kGroup)).gpw > 0 &&
-           dec_split((int)(inter / kGroup)).gpw > 0;
+// The fused layer for the K-group counts of the common shapes (gemm1 K = H, gemm2 K = I);
+// other shapes run the two GEMVs as separate launches.
+template <int GPW1, int KS1, int GPW2, int KS2, bool ABF16>
+int launch_layer_a(const DecodeParams& p1, const DecodeParams& p2, const DecDep& dep, hipStream_t s) {
+    constexpr size_t l1 = DecCfg<Epi::kSiluHalf, GPW1, KS1>::LDS_BYTES;
+    constexpr size_t l2 = DecCfg<Epi::kSlotF32, GPW2, KS2>::LDS_BYTES;
+    constexpr size_t lds = l1 > l2 ? l1 : l2;
+    auto* kern = &decode_layer_kernel<GPW1, KS1, GPW2, KS2, ABF16>;
+    static bool attr_set = false;
+    if (!attr_set) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
+            set_error("decode_layer_kernel: cannot reserve dynamic LDS");
+            return W4A8_ERR_HIP;
+        }
+        attr_set = true;
+    }
+    static int grid = 0;
+    if (grid == 0) grid = persistent_grid();
+    launch_kernel(kern, dim3(grid), dim3(kDecThreads), lds, s, p1, p2, dep);
+    return check_launch("decode_layer_kernel");
 }
 
-int launch_decode_gemv(const DecodeLaunch& d, hipStream_t s) {
-    if (d.numel == 0) return W4A8_OK;
+template <int GPW1, int KS1, int GPW2, int KS2>
+int launch_layer_t(const DecodeParams& p1, const DecodeParams& p2, const DecDep& dep, hipStream_t s) {
+    if (p1.a_bf16) return launch_layer_a<GPW1, KS1, GPW2, KS2, true>(p1, p2, dep, s);
+    return launch_layer_a<GPW1, KS1, GPW2, KS2, false>(p1, p2, dep, s);
+}
+
+// (K groups of gemm1, K groups of gemm2) with a fused instantiation
+bool dec_fused_shape(int g1, int g2) {
+    return (g1 == 16 && g2 == 4) || (g1 == 32 && g2 == 12) || (g1 == 4 && g2 == 2) ||
+           (g1 == 2 && g2 == 1) || (g1 == 16 && g2 == 16) || (g1 == 8 && g2 == 4);
+}
+
+int launch_layer_e(const DecodeParams& p1, const DecodeParams& p2, const DecDep& dep, hipStream_t s) {
+    switch (p1.G * 64 + p2.G) {
+        case 16 * 64 + 4: return launch_layer_t<4, 4, 4, 1>(p1, p2, dep, s);
+        case 32 * 64 + 12: return launch_layer_t<8, 4, 3, 4>(p1, p2, dep, s);
+        case 4 * 64 + 2: return launch_layer_t<4, 1, 2, 1>(p1, p2, dep, s);
+        case 2 * 64 + 1: return launch_layer_t<2, 1, 1, 1>(p1, p2, dep, s);
+        case 16 * 64 + 16: return launch_layer_t<4, 4, 4, 4>(p1, p2, dep, s);
+        case 8 * 64 + 4: return launch_layer_t<2, 4, 4, 1>(p1, p2, dep, s);
+    }
+    set_error("decode layer: no fused instantiation for these K-group counts");
+    return W4A8_ERR_INVALID;
+}
+
+DecodeParams dec_params(const DecodeLaunch& d) {
     DecodeParams p;
     p.ids = d.topk_ids;
     p.emap = d.expert_map;
@@ -668,6 +836,41 @@ int launch_decode_gemv(const DecodeLaunch& d, hipStream_t s) {
     p.K = (int)d.K;
     p.N = (int)d.N;
     p.G = (int)(d.K / kGroup);
+    return p;
+}
+
+}  // namespace
+
+bool decode_layer_fused_supported(int64_t H, int64_t inter) {
+    return dec_fused_shape((int)(H / kGroup), (int)(inter / kGroup));
+}
+
+int launch_decode_layer(const DecodeLaunch& d1, const DecodeLaunch& d2, uint64_t* flags,
+                        uint64_t nonce, uint64_t* timeout, hipStream_t s) {
+    if (d1.numel == 0) return W4A8_OK;
+    if (persistent_grid() > kDecodeFlagSlots) {
+        set_error("decode layer: more compute units than completion flags");
+        return W4A8_ERR_INVALID;
+    }
+    const DecodeParams p1 = dec_params(d1), p2 = dec_params(d2);
+    DecDep dep;
+    dep.flags = flags;
+    dep.nonce = nonce;
+    dep.upe1 = (int)(d1.N / 2 / 16);                 // gemm1: 16 gate + 16 up columns a unit
+    dep.teams1 = dec_split(p1.G).ksplit > 1 ? 1 : 4;
+    dep.timeout = timeout;
+    return launch_layer_e(p1, p2, dep, s);
+}
+
+bool decode_layer_supported(int64_t numel, int64_t E, int64_t H, int64_t inter, int64_t gs) {
+    return numel <= kDecMaxSlots && E <= kDecMaxExperts && gs == kGroup && H % kGroup == 0 &&
+           inter % kGroup == 0 && dec_split((int)(H / kGroup)).gpw > 0 &&
+           dec_split((int)(inter / kGroup)).gpw > 0;
+}
+
+int launch_decode_gemv(const DecodeLaunch& d, hipStream_t s) {
+    if (d.numel == 0) return W4A8_OK;
+    const DecodeParams p = dec_params(d);
     return d.silu ? launch_dec_e<Epi::kSiluHalf>(p, s) : launch_dec_e<Epi::kSlotF32>(p, s);
 }
 

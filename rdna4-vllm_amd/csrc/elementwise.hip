@@ -90,9 +90,16 @@ template <bool BF16>
 __global__ void slot_reduce_kernel(const float* __restrict__ y, const float* __restrict__ tw,
                                    const int32_t* __restrict__ ids,
                                    const int32_t* __restrict__ emap, int emap_len, int E,
-                                   int64_t T, int N, int top_k, void* __restrict__ out) {
+                                   int64_t T, int N, int top_k, void* __restrict__ out,
+                                   SlotReduceSync sync) {
     const int64_t t = blockIdx.y;
     const int n = (blockIdx.x * blockDim.x + threadIdx.x) * 4;
+    // after the fused decode layer: its completion flags go back to 0 for the next call, and
+    // a wait of this call that gave up (never expected) turns the whole output into NaN
+    // instead of leaving rows that may have read unpublished h
+    const bool failed = sync.timeout != nullptr && *sync.timeout == sync.nonce;
+    if (sync.flags != nullptr && blockIdx.x == 0 && blockIdx.y == 0)
+        for (int i = threadIdx.x; i < sync.nflags; i += blockDim.x) sync.flags[i] = 0;
     if (n >= N || t >= T) return;
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll 8
@@ -107,6 +114,9 @@ __global__ void slot_reduce_kernel(const float* __restrict__ y, const float* __r
         acc[2] = fmaf(w, v.z, acc[2]);
         acc[3] = fmaf(w, v.w, acc[3]);
     }
+    if (failed)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] = __builtin_nanf("");
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         if constexpr (BF16)
@@ -255,15 +265,16 @@ int launch_gather_reduce(const void* out2, int64_t P, int64_t N, const int32_t* 
 
 int launch_slot_reduce(const float* y, const float* tw, const int32_t* ids,
                        const int32_t* emap, int64_t emap_len, int64_t E, int64_t T, int64_t N,
-                       int64_t top_k, void* out, bool out_bf16, hipStream_t stream) {
+                       int64_t top_k, void* out, bool out_bf16, hipStream_t stream,
+                       SlotReduceSync sync) {
     if (T == 0 || N == 0) return W4A8_OK;
     dim3 grid(blocks_for(N / 4, 256), (unsigned)T);
     if (out_bf16)
         slot_reduce_kernel<true><<<grid, 256, 0, stream>>>(y, tw, ids, emap, (int)emap_len,
-                                                          (int)E, T, (int)N, (int)top_k, out);
+                                                          (int)E, T, (int)N, (int)top_k, out, sync);
     else
         slot_reduce_kernel<false><<<grid, 256, 0, stream>>>(y, tw, ids, emap, (int)emap_len,
-                                                           (int)E, T, (int)N, (int)top_k, out);
+                                                           (int)E, T, (int)N, (int)top_k, out, sync);
     return check_launch("slot_reduce_kernel");
 }
 

@@ -39,6 +39,9 @@ __device__ __forceinline__ uint4 load_stream16(const void* p) {
     const v4i v = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(p));
     return make_uint4((uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w);
 }
+// cache-policy operand of the buffer intrinsics on gfx950: sc1 (agent coherence, the bit
+// agent-scope atomics carry)
+constexpr int kCpolSc1 = 16;
 using v4f = float __attribute__((ext_vector_type(4)));
 using v16f = float __attribute__((ext_vector_type(16)));
 

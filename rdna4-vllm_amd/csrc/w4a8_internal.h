@@ -102,9 +102,18 @@ int launch_gather_reduce(const void* out2, int64_t P, int64_t N, const int32_t* 
                          float* out, int32_t* slot_to_row, hipStream_t stream);
 // out[t, n] = cast(sum_{j asc} w[t*k+j] * y[(t*k+j), n]) with y fp32 (rows = T*k);
 // slots whose (mapped) expert is outside [0, E) are skipped (map as launch_align_quant).
+// sync (after the fused decode layer): flags[0..nflags) are reset to 0, and the output is
+// NaN when *timeout == nonce (an in-kernel wait of this call gave up).
+struct SlotReduceSync {
+    uint64_t* flags = nullptr;
+    int nflags = 0;
+    const uint64_t* timeout = nullptr;
+    uint64_t nonce = 0;
+};
 int launch_slot_reduce(const float* y, const float* tw, const int32_t* topk_ids,
                        const int32_t* expert_map, int64_t emap_len, int64_t E, int64_t T,
-                       int64_t N, int64_t top_k, void* out, bool out_bf16, hipStream_t stream);
+                       int64_t N, int64_t top_k, void* out, bool out_bf16, hipStream_t stream,
+                       SlotReduceSync sync = SlotReduceSync{});
 int launch_cast_f32(const float* in, int64_t n, void* out, bool out_bf16, hipStream_t stream);
 // out[t, n] = cast(sum_{j asc} w[t*k+j] * f32(y[slot_to_row[t*k+j], n])), y fp16 (rows, N);
 // rows < 0 (slots dropped by expert_map) contribute nothing. N % 8 == 0.
@@ -193,5 +202,12 @@ struct DecodeLaunch {
 };
 bool decode_layer_supported(int64_t numel, int64_t E, int64_t H, int64_t inter, int64_t gs);
 int launch_decode_gemv(const DecodeLaunch& d, hipStream_t stream);
+// Both GEMVs in one launch (gemm2 waits in-kernel for the gemm1 rows it reads): d1 is gemm1,
+// d2 gemm2. flags: kDecodeFlagSlots words, 0 or a value other than nonce on entry (the slot
+// reduce resets them to 0); timeout: set to nonce if an in-kernel wait gave up.
+constexpr int64_t kDecodeFlagSlots = 1024;
+bool decode_layer_fused_supported(int64_t H, int64_t inter);
+int launch_decode_layer(const DecodeLaunch& d1, const DecodeLaunch& d2, uint64_t* flags,
+                        uint64_t nonce, uint64_t* timeout, hipStream_t stream);
 
 }  // namespace w4a8

@@ -1,0 +1,95 @@
+"""The decode layer's two GEMVs fused into one launch (decode_layer_kernel, opt-in with
+W4A8_DECODE_FUSED=1): gemm2 waits in the kernel for the gemm1 rows it reads. Same arithmetic
+and partition as the two launches, so the outputs are bit-identical to them; the oracle
+checks the fused output too. Graph replays with fresh inputs check that the completion
+flags are reset between calls (the slot reduce clears them)."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import bench
+import oracle as O
+import w4a8_fp8_wmma as W
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+@pytest.fixture
+def fused_env():
+    old = os.environ.get("W4A8_DECODE_FUSED")
+    yield
+    if old is None:
+        os.environ.pop("W4A8_DECODE_FUSED", None)
+    else:
+        os.environ["W4A8_DECODE_FUSED"] = old
+
+
+def run(cfg, ws, x, logits, fused):
+    os.environ["W4A8_DECODE_FUSED"] = "1" if fused else "0"
+    out, tw, ids = W.moe_forward(x, logits, cfg["k"], ws["f13"], ws["f2"], ws["s13"], ws["s2"],
+                                 ws["z13"], ws["z2"])
+    torch.cuda.synchronize()
+    return out, tw, ids
+
+
+def layer(name, T, seed):
+    cfg = dict(bench.CONFIGS[name]) if isinstance(name, str) else dict(name)
+    cfg["T"] = T
+    ws = bench.make_weights(cfg, seed, DEV)
+    ws["f13"], ws["f2"] = W.repack_fragments(ws["w13"]), W.repack_fragments(ws["w2"])
+    x, logits = bench.make_inputs(cfg, seed + 1, DEV)
+    return cfg, ws, x, logits
+
+
+SMALL = dict(H=512, E=16, k=4, I=256, g=128, routing="uniform")
+
+
+@pytest.mark.parametrize("name,T", [("c3", 32), ("c3", 1), ("c3", 96), ("c5", 32), ("c5", 1),
+                                    (SMALL, 7), (SMALL, 64)])
+def test_fused_decode_equals_two_launches(fused_env, name, T):
+    cfg, ws, x, logits = layer(name, T, 6100 + T)
+    out2, tw, ids = run(cfg, ws, x, logits, fused=False)
+    out1, tw1, ids1 = run(cfg, ws, x, logits, fused=True)
+    assert torch.equal(ids1, ids) and torch.equal(tw1, tw)
+    assert not torch.isnan(out1.float()).any()
+    assert torch.equal(out1, out2)
+    # the oracle on a few tokens (the fused path's own check)
+    sel = np.arange(min(T, 4))
+    h = {kk: v.cpu().numpy() for kk, v in ws.items() if kk in ("w13", "s13", "z13", "w2", "s2", "z2")}
+    ref = O.moe_layer(x.float().cpu().numpy()[sel], h["w13"], h["s13"], h["z13"], h["w2"],
+                      h["s2"], h["z2"], tw.cpu().numpy()[sel], ids.cpu().numpy()[sel], cfg["g"],
+                      round_y_fp16=False)
+    got = out1.float().cpu().numpy()[sel]
+    assert np.abs(got - ref).max() / np.abs(ref).max() <= 1e-2
+
+
+def test_fused_decode_graph_replays(fused_env):
+    """Five replays of one captured fused layer, each after new inputs are copied in, against
+    eager two-launch calls on the same inputs (the flags are cleared by each replay's slot
+    reduce; a stale flag would let gemm2 read the previous replay's rows)."""
+    cfg, ws, x, logits = layer("c3", 32, 6200)
+    os.environ["W4A8_DECODE_FUSED"] = "1"
+    xs, ls = x.clone(), logits.clone()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        W.moe_forward(xs, ls, cfg["k"], ws["f13"], ws["f2"], ws["s13"], ws["s2"], ws["z13"], ws["z2"])
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out_g, _, _ = W.moe_forward(xs, ls, cfg["k"], ws["f13"], ws["f2"], ws["s13"], ws["s2"],
+                                    ws["z13"], ws["z2"])
+    for r in range(5):
+        x_r, l_r = bench.make_inputs(cfg, 6300 + r, DEV)
+        xs.copy_(x_r)
+        ls.copy_(l_r)
+        g.replay()
+        torch.cuda.synchronize()
+        got = out_g.clone()
+        ref, _, _ = run(cfg, ws, x_r, l_r, fused=False)
+        os.environ["W4A8_DECODE_FUSED"] = "1"
+        assert torch.equal(got, ref), r
