@@ -293,7 +293,12 @@ int moe_apply_impl(const void* x, int x_dtype, int64_t T, int64_t H, int64_t int
     // would serialise the tokens on the align work-group)
     // many-token schedule: the routing waves also quantise x (one launch less)
     const bool route_quant = logits != nullptr && !(pl.decode && numel <= kAlignSmallMax) && k8;
-    if (logits != nullptr)
+    const bool frag_decode =
+        frag && pl.decode && !e2m1 && decode_layer_supported(numel, E, H, inter, group_size);
+    // few tokens: the decode gemm1 launch routes them itself (no router launch)
+    const bool route_in_gemm1 = logits != nullptr && frag_decode &&
+                                decode_routes_in_kernel(T, n_global, top_k);
+    if (logits != nullptr && !route_in_gemm1)
         if (int rc = launch_topk_softmax(logits, T, n_global, top_k, renormalize,
                                          const_cast<float*>(topk_weights),
                                          const_cast<int32_t*>(topk_ids), s,
@@ -301,7 +306,7 @@ int moe_apply_impl(const void* x, int x_dtype, int64_t T, int64_t H, int64_t int
                                          pf1 ? gs1 : nullptr))
             return rc;
     stage_mark(0, s);
-    if (frag && pl.decode && !e2m1 && decode_layer_supported(numel, E, H, inter, group_size)) {
+    if (frag_decode) {
         // decode on fragment-layout weights: two GEMVs that group the slots by expert
         // themselves (no align launch) and quantise their rows in registers (no act-quant
         // launches), then the slot reduce
@@ -315,6 +320,11 @@ int moe_apply_impl(const void* x, int x_dtype, int64_t T, int64_t H, int64_t int
         d.w = w13; d.scales = w13_scales_f16; d.zeros = w13_zeros; d.out = h;
         d.K = H; d.N = 2 * inter;
         DecodeLaunch d2 = d;
+        if (route_in_gemm1) {
+            d.logits = logits; d.n_router = n_global; d.renormalize = renormalize;
+            d.topk_weights_out = const_cast<float*>(topk_weights);
+            d.topk_ids_out = const_cast<int32_t*>(topk_ids);
+        }
         d2.a = h; d2.a_bf16 = false; d2.silu = false;
         d2.w = w2; d2.scales = w2_scales_f16; d2.zeros = w2_zeros; d2.out = acc;
         d2.K = inter; d2.N = H;

@@ -26,6 +26,7 @@
 #include <type_traits>
 
 #include "grouped_params.h"
+#include "router.h"
 
 namespace w4a8 {
 namespace {
@@ -39,7 +40,13 @@ constexpr uint32_t kDecOnes = 0x38383838u;   // four e4m3 bytes of 1.0
 using u16x2 = unsigned short __attribute__((ext_vector_type(2)));
 
 struct DecodeParams {
-    const int32_t* ids;      // (numel) routed expert ids
+    const int32_t* ids;      // (numel) routed expert ids (unused with logits)
+    // router in the kernel (gemm1 only): every work-group routes the T tokens itself and
+    // work-group 0 writes the weights and ids; null: ids come from an earlier launch
+    const float* logits;     // (T, n_router) fp32
+    int n_router, renorm;
+    float* tw_out;           // (numel) fp32
+    int32_t* ids_out;        // (numel)
     const int32_t* emap;     // global -> local expert map or null
     int emap_len, numel, top_k, E;
     const void* a;           // activation rows, fp16 / bf16
@@ -71,7 +78,7 @@ __device__ __forceinline__ int dec_cost(const DecodeLists& L, int r, int upe) {
 
 // Touched experts and their slot lists (the align's grouping, without padding) in LDS, and
 // the number of 16-row passes before each touched expert (the partition cost, dec_cost).
-__device__ void build_lists(const DecodeParams& p, DecodeLists& L) {
+__device__ void build_lists(const DecodeParams& p, const int32_t* ids, DecodeLists& L) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     constexpr int kPer = kDecMaxSlots / kDecThreads;
     for (int e = tid; e < p.E; e += kDecThreads) L.cnt[e] = 0;
@@ -79,7 +86,7 @@ __device__ void build_lists(const DecodeParams& p, DecodeLists& L) {
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
         const int s = tid + kDecThreads * i;
-        int e = s < p.numel ? p.ids[s] : -1;
+        int e = s < p.numel ? ids[s] : -1;
         if (p.emap != nullptr) e = (e >= 0 && e < p.emap_len) ? p.emap[e] : -1;
         es[i] = (e >= 0 && e < p.E) ? e : -1;
     }
@@ -142,6 +149,41 @@ __device__ void build_lists(const DecodeParams& p, DecodeLists& L) {
 #pragma unroll
     for (int i = 0; i < kPer; ++i)
         if (es[i] >= 0) L.slot[atomicAdd(&L.cnt[es[i]], 1)] = (int16_t)(tid + kDecThreads * i);
+    __syncthreads();
+}
+
+// In-kernel router (DecodeParams::logits): every work-group selects the top-k of all T
+// tokens itself (wave w takes tokens w, w + 4, ..., eight logit rows in flight at a time),
+// with the router kernel's selection (router.h), so the ids are the same bits; work-group 0
+// also writes the weights and ids out. No other work-group's result is read, so there is
+// no synchronisation between work-groups. One selection takes a wave ~2 us, so this pays
+// only while each wave routes one token: T <= 4 (c2, T = 1: 32.4 -> 30.7 us per layer; at
+// T = 32, eight tokens a wave, gemm1 grew by 17 us against the 4.7 us router launch it
+// replaced). n_router <= 256.
+constexpr int kDecRouteMaxT = 4;
+constexpr int kDecRouteMaxE = 256;
+__device__ void dec_route(const DecodeParams& p, int32_t* s_ids) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int T = p.numel / p.top_k;
+    const bool writer = blockIdx.x == 0;
+    constexpr int kRows = 8;
+    for (int t0 = wave; t0 < T; t0 += 4 * kRows) {
+        float v[kRows][4];
+#pragma unroll
+        for (int i = 0; i < kRows; ++i) {
+            const int t = min(t0 + 4 * i, T - 1);
+            topk_load<4>(p.logits + (int64_t)t * p.n_router, p.n_router, lane, v[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < kRows; ++i) {
+            const int t = t0 + 4 * i;
+            if (t < T)
+                topk_select<4>(v[i], p.n_router, p.top_k, p.renorm != 0,
+                               writer ? p.tw_out + (int64_t)t * p.top_k : nullptr,
+                               writer ? p.ids_out + (int64_t)t * p.top_k : nullptr,
+                               s_ids + t * p.top_k, lane);
+        }
+    }
     __syncthreads();
 }
 
@@ -668,8 +710,14 @@ __global__ void __launch_bounds__(kDecThreads, 1) decode_gemv_kernel(DecodeParam
     __shared__ DecodeLists L;
     __shared__ float s_amax[4][16];
     extern __shared__ __attribute__((aligned(16))) uint8_t s_dyn[];
+    __shared__ int32_t s_ids[kDecMaxSlots];
     const uint32_t warm = dec_warm(p);
-    build_lists(p, L);
+    const int32_t* ids = p.ids;
+    if (p.logits != nullptr) {
+        dec_route(p, s_ids);
+        ids = s_ids;
+    }
+    build_lists(p, ids, L);
     dec_run<EPI, GPW, KSPLIT, ABF16, false>(p, L, s_amax, reinterpret_cast<v4f*>(s_dyn), DecDep{});
     dec_keep(warm, p.out);
 }
@@ -685,8 +733,14 @@ __global__ void __launch_bounds__(kDecThreads, 1) decode_layer_kernel(DecodePara
     __shared__ DecodeLists L;
     __shared__ float s_amax[4][16];
     extern __shared__ __attribute__((aligned(16))) uint8_t s_dyn[];
+    __shared__ int32_t s_ids[kDecMaxSlots];
     const uint32_t warm = dec_warm(p1);
-    build_lists(p1, L);
+    const int32_t* ids = p1.ids;
+    if (p1.logits != nullptr) {
+        dec_route(p1, s_ids);
+        ids = s_ids;
+    }
+    build_lists(p1, ids, L);
     dec_run<Epi::kSiluHalf, GPW1, KS1, ABF16, false>(p1, L, s_amax, reinterpret_cast<v4f*>(s_dyn), dep);
     // every wave's h stores complete (vmcnt(0)), then one release at agent scope publishes them
     __builtin_amdgcn_s_waitcnt(0x0F70);
@@ -821,6 +875,11 @@ int launch_layer_e(const DecodeParams& p1, const DecodeParams& p2, const DecDep&
 DecodeParams dec_params(const DecodeLaunch& d) {
     DecodeParams p;
     p.ids = d.topk_ids;
+    p.logits = d.logits;
+    p.n_router = (int)d.n_router;
+    p.renorm = d.renormalize ? 1 : 0;
+    p.tw_out = d.topk_weights_out;
+    p.ids_out = d.topk_ids_out;
     p.emap = d.expert_map;
     p.emap_len = (int)d.emap_len;
     p.numel = (int)d.numel;
@@ -860,6 +919,10 @@ int launch_decode_layer(const DecodeLaunch& d1, const DecodeLaunch& d2, uint64_t
     dep.teams1 = dec_split(p1.G).ksplit > 1 ? 1 : 4;
     dep.timeout = timeout;
     return launch_layer_e(p1, p2, dep, s);
+}
+
+bool decode_routes_in_kernel(int64_t T, int64_t n_router, int64_t top_k) {
+    return T <= kDecRouteMaxT && n_router <= kDecRouteMaxE && top_k <= n_router && top_k <= 64;
 }
 
 bool decode_layer_supported(int64_t numel, int64_t E, int64_t H, int64_t inter, int64_t gs) {

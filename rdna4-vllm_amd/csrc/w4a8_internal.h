@@ -189,6 +189,13 @@ bool gemv_supported(int64_t K, int64_t group_size);
 // else gemm2 (a = h (numel, K) fp16 by slot, out = y (numel, N) fp32).
 struct DecodeLaunch {
     const int32_t* topk_ids;
+    // gemm1 only: route in the kernel from these logits (decode_routes_in_kernel), writing
+    // topk_weights_out / topk_ids_out; null: topk_ids come from an earlier launch
+    const float* logits = nullptr;
+    int64_t n_router = 0;
+    bool renormalize = true;
+    float* topk_weights_out = nullptr;
+    int32_t* topk_ids_out = nullptr;
     const int32_t* expert_map;
     int64_t emap_len, numel, top_k, E;
     const void* a;
@@ -201,6 +208,8 @@ struct DecodeLaunch {
     int64_t K, N;
 };
 bool decode_layer_supported(int64_t numel, int64_t E, int64_t H, int64_t inter, int64_t gs);
+// T tokens over n_router experts: the decode gemm1 launch can route them itself
+bool decode_routes_in_kernel(int64_t T, int64_t n_router, int64_t top_k);
 int launch_decode_gemv(const DecodeLaunch& d, hipStream_t stream);
 // Both GEMVs in one launch (gemm2 waits in-kernel for the gemm1 rows it reads): d1 is gemm1,
 // d2 gemm2. flags: kDecodeFlagSlots words, 0 or a value other than nonce on entry (the slot

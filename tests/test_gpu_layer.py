@@ -291,11 +291,15 @@ def test_fragment_layout_full_size(name, T):
     assert torch.equal(a, b)
 
 
-@pytest.mark.parametrize("T,frag", [(1, True), (32, True), (32, False), (96, True), (300, True)])
-def test_moe_forward_equals_router_then_apply(T, frag):
+@pytest.mark.parametrize("T,frag,E", [(1, True, 64), (32, True, 64), (32, False, 64),
+                                      (96, True, 64), (300, True, 64), (4, True, 256),
+                                      (5, True, 256), (3, True, 16), (2, True, 512)])
+def test_moe_forward_equals_router_then_apply(T, frag, E):
     """moe_forward (router + expert path in one call) gives the fused_topk ids / weights and
-    the moe_apply output bit for bit."""
-    cfg = dict(T=T, H=512, E=64, k=8, I=256, g=128, routing="uniform")
+    the moe_apply output bit for bit. On fragment weights with T <= 4 and E <= 256 the decode
+    gemm1 launch routes the tokens itself (same selection code, every work-group); T = 5 and
+    E = 512 go through the router kernel."""
+    cfg = dict(T=T, H=512, E=E, k=8, I=256, g=128, routing="uniform")
     ws = bench.make_weights(cfg, 700 + T, DEV)
     x, logits = bench.make_inputs(cfg, 701 + T, DEV)
     x = x.to(torch.bfloat16)
