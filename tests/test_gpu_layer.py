@@ -362,3 +362,40 @@ def test_graph_replay_matches_eager():
         assert torch.equal(out, eager)
         W.moe_apply(x, ws["w13"], ws["w2"], ws["s13"], ws["s2"], ws["z13"], ws["z2"], tw, ids)
         torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("T", [1, 4, 32, 300])
+def test_graph_replay_forward_fragments_fresh_inputs(T):
+    """moe_forward on fragment weights captured once and replayed with new hidden states and
+    router logits copied in before each replay (how a serving loop uses the graph): every
+    replay equals an eager call on the same inputs. T = 1 and 4 route inside the decode
+    gemm1 launch, 32 has the router launch, 300 is the prefill schedule."""
+    cfg = dict(T=T, H=512, E=64, k=8, I=256, g=128, routing="uniform")
+    ws = bench.make_weights(cfg, 900 + T, DEV)
+    f13, f2 = W.repack_fragments(ws["w13"]), W.repack_fragments(ws["w2"])
+    x, logits = bench.make_inputs(cfg, 901 + T, DEV)
+    xs, ls = x.clone(), logits.clone()
+
+    def fwd(a, b):
+        return W.moe_forward(a, b, cfg["k"], f13, f2, ws["s13"], ws["s2"], ws["z13"], ws["z2"])
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fwd(xs, ls)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out_g, tw_g, ids_g = fwd(xs, ls)
+    for r in range(4):
+        x_r, l_r = bench.make_inputs(cfg, 950 + 10 * T + r, DEV)
+        xs.copy_(x_r)
+        ls.copy_(l_r)
+        g.replay()
+        torch.cuda.synchronize()
+        got = (out_g.clone(), tw_g.clone(), ids_g.clone())
+        ref = fwd(x_r, l_r)
+        torch.cuda.synchronize()
+        assert torch.equal(got[2], ref[2]) and torch.equal(got[1], ref[1]), r
+        assert torch.equal(got[0], ref[0]), r
