@@ -94,8 +94,12 @@ int run_grouped(GroupedArgs& a, int64_t kernel, void* ws, size_t ws_bytes, hipSt
                                   a.num_valid, a.act_group_sums))
         return rc;
     // activation-resident tiles where the shape allows (the whole-layer prefill kernel, so
-    // the op API and moe_apply share it), the streamed-K tiles otherwise
-    if (prefill && prefill_ares_supported(a.K, a.N, a.group_size, a.e2m1, a.block_m, a.epi) &&
+    // the op API and moe_apply share it), the streamed-K tiles otherwise. An ares work-group
+    // owns all N columns of its rows, so one expert (the dense GEMM) fills the chip only with
+    // >= 512 row tiles; below that the streamed-K tiles also split N.
+    const bool ares_fills = a.E > 1 || a.P >= 512 * 64;
+    if (prefill && ares_fills &&
+        prefill_ares_supported(a.K, a.N, a.group_size, a.e2m1, a.block_m, a.epi) &&
         a.x_rows * a.K < ((int64_t)1 << 31))
         return launch_grouped_prefill_ares(a, s);
     if (prefill) return launch_grouped_prefill(a, s);

@@ -116,6 +116,8 @@ def mmq_fp8_moe_gather_reduce(out2, sorted_token_ids, topk_weights, num_tokens_p
         out2, sorted_token_ids, topk_weights, num_tokens_post_padded, top_k)
 
 
+from . import linear  # noqa: E402,F401  defines torch.ops.vllm.w4a8_dense_apply
+
 __all__ = [
     "mmq_fp8_gemm", "mmq_fp8_moe_gemm", "mmq_fp8_moe_gemm1_silu", "mmq_fp8_moe_gemm_scatter",
     "mmq_fp8_moe_gather_reduce", "act_quant_fp8", "dequant_fp8", "fragments_supported",

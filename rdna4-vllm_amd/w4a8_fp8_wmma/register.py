@@ -1,8 +1,10 @@
 """vLLM general-plugin entry point (w4a8_fp8_wmma/w4a8_fp8_wmma/register.py:42-175).
 
-``register()`` installs the MoeWNA16 MoE hook. The dense-linear and other MoE hooks of
-the reference are outside this package's scope (the W4A8 MoE expert path only).
-Removed env knobs raise at boot, like the reference (register.py:29-39).
+``register()`` prepends the dense W4A8 linear kernel to vLLM's ROCm linear-kernel list and
+installs the MoeWNA16 MoE hook, each best-effort so one failing leaves the other in place.
+The reference's other hooks (mxfp4 dense registry, compressed-tensors and mxfp4 MoE) are
+outside this package's scope. Removed env knobs raise at boot, like the reference
+(register.py:29-39).
 """
 from __future__ import annotations
 
@@ -22,6 +24,11 @@ def register() -> None:
         print("[w4a8_fp8_wmma] disabled via VLLM_ROCM_USE_W4A8_FP8_WMMA")
         return
     _check_removed_w4a8_env()
+    from .linear import register_dense_linear
+    try:
+        register_dense_linear()
+    except ImportError as e:
+        print(f"[w4a8_fp8_wmma] dense linear kernel not registered: {e}")
     from .moe_experts import register_moe_wna16
     try:
         register_moe_wna16()

@@ -304,3 +304,94 @@ def test_layer_args_rejections(bad, match):
         W.moe_apply(t["x"], t["w13"], t["w2"], t["w13_s"], t["w2_s"], t["w13_z"], t["w2_z"],
                     t["topk_weights"], t["topk_ids"], extra.get("expert_map"),
                     global_num_experts=extra.get("global_num_experts"))
+
+
+# --- dense linear (vllm::w4a8_dense_apply and its adapter) ---------------------------------
+def test_dense_ladder_and_env(monkeypatch):
+    from w4a8_fp8_wmma import linear
+    monkeypatch.delenv("VLLM_ROCM_W4A8_DECODE_MAX_M", raising=False)
+    d = linear.DECODE_MAX_M_DEFAULT
+    assert linear.dense_kernel_for(1, 2048, 128) == "decode_gemv"
+    assert linear.dense_kernel_for(d, 2048, 128) == "decode_gemv"
+    assert linear.dense_kernel_for(d + 1, 2048, 128) == "prefill_wmma_ashuffle"
+    assert linear.dense_kernel_for(1, 2048, 64) == "prefill_wmma"
+    assert linear.dense_kernel_for(1, 2048, 32) == "prefill_wmma_ashuffle"
+    monkeypatch.setenv("VLLM_ROCM_W4A8_DECODE_MAX_M", "2")
+    assert linear.dense_kernel_for(3, 2048, 128) == "prefill_wmma_ashuffle"
+    for name in ("decode_gemv", "prefill_wmma_ashuffle", "prefill_wmma"):
+        assert name in W._DENSE_KERNELS
+
+
+def test_gptq_to_op_layout_from_the_format_definition():
+    """AutoGPTQ qweight (K/8, N): word [k8, n] holds k = 8 k8 + j of column n in nibble j.
+    Built element by element here, then converted and compared with the oracle's op-layout
+    pack of the same matrix."""
+    from w4a8_fp8_wmma import linear
+    r = np.random.default_rng(5)
+    N, K, g = 24, 64, 32
+    nib = r.integers(0, 16, (N, K))
+    gq = np.zeros((K // 8, N), np.int64)
+    for k in range(K):
+        for n in range(N):
+            gq[k // 8, n] |= int(nib[n, k]) << (4 * (k % 8))
+    gq = gq.astype(np.uint32).view(np.int32)
+    sc = r.uniform(0.005, 0.02, (K // g, N)).astype(np.float32)
+    wq, ws = linear.gptq_to_op_layout(torch.from_numpy(gq), torch.from_numpy(sc), K, N)
+    assert np.array_equal(wq.numpy(), O.pack_nibbles(nib))
+    assert ws.dtype == torch.float16 and np.array_equal(ws.numpy(), sc.T.astype(np.float16))
+    with pytest.raises(ValueError, match="GPTQ qweight"):
+        linear.gptq_to_op_layout(torch.from_numpy(gq).t(), torch.from_numpy(sc), K, N)
+
+
+def test_dense_apply_rejections(monkeypatch):
+    from w4a8_fp8_wmma import linear
+    x = torch.zeros(2, 256, dtype=torch.bfloat16)
+    wq = torch.zeros(64, 32, dtype=torch.int32)
+    ws = torch.zeros(64, 2, dtype=torch.float16)
+    args = (None, None, None, None, 64, 256, 128)
+    with pytest.raises(ValueError, match="bias 8"):
+        linear.w4a8_dense_apply(x, wq, ws, *args, False, 0, 0)
+    with pytest.raises(ValueError, match="w_q must be"):
+        linear.w4a8_dense_apply(x, wq[:, :16], ws, *args, False, 8, 0)
+    with pytest.raises(ValueError, match="x must be"):
+        linear.w4a8_dense_apply(x[:, :128], wq, ws, *args, False, 8, 0)
+    monkeypatch.setenv("VLLM_ROCM_W4A8_FORCE", "off")
+    with pytest.raises(RuntimeError, match="Triton"):
+        linear.w4a8_dense_apply(x, wq, ws, *args, False, 8, 0)
+
+
+def test_dense_apply_op_registered_with_fake():
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    from w4a8_fp8_wmma import linear  # noqa: F401  (defines torch.ops.vllm.w4a8_dense_apply)
+    with FakeTensorMode():
+        x = torch.empty(5, 256, dtype=torch.bfloat16)
+        wq = torch.empty(64, 32, dtype=torch.int32)
+        ws = torch.empty(64, 2, dtype=torch.float16)
+        o = torch.ops.vllm.w4a8_dense_apply(x, wq, ws, None, None, None, None, 64, 256, 128,
+                                            False, 8, 0)
+        assert o.shape == (5, 64) and o.dtype == torch.float16
+
+
+def test_linear_kernel_can_implement():
+    from w4a8_fp8_wmma import linear
+
+    class Base:
+        def __init__(self, c):
+            self.config = c
+
+    class T:
+        uint4b8, uint4 = object(), object()
+
+    class C:
+        partition_weight_shape = (2048, 1024)
+        group_size = 128
+        weight_type = T.uint4
+        act_type = torch.bfloat16
+        has_g_idx = False
+
+    Cls = linear.make_linear_kernel(Base, T, lambda: True)
+    ok, why = Cls.can_implement(C)
+    assert not ok and "gfx950" in why          # no device in this container
+    ok, why = linear.make_linear_kernel(Base, T, lambda: False).can_implement(C)
+    assert not ok and why == "ROCm only"
+    assert linear.register_dense_linear(verbose=False) is False   # vLLM absent
