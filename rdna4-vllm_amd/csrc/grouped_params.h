@@ -31,6 +31,7 @@ struct Params {
     int xbf16;                  // xh holds bf16 (else fp16)
     int w_frag;                 // w in fragment layout (16-row tile, group, lane)
     const float* asum;          // (x_rows, K/128) sums of the e4m3 values per group, or null
+    int xcd_slots;              // activation-resident tiles: work-groups one XCD runs at once
 };
 
 // Row resolution shared by all schedules. Returns the activation row (or -1).
@@ -70,6 +71,7 @@ inline Params make_params(const GroupedArgs& a) {
     p.xbf16 = a.x_bf16 ? 1 : 0;
     p.asum = a.act_group_sums;
     p.w_frag = a.w_frag ? 1 : 0;
+    p.xcd_slots = 0;
     return p;
 }
 

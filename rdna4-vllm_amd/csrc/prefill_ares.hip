@@ -153,15 +153,37 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
     uint32_t* s_zst = reinterpret_cast<uint32_t*>(lds + L.zst);       // [8][64] zero words
     float* s_asc = reinterpret_cast<float*>(lds + L.total);           // [BM]
 
-    // ---- tile of this work-group: XCD-aware order over the live tiles ----
+    const int ncols = kSilu ? p.N / 2 : p.N;
+    const int nranges = ncols / ar_range_cols<kSilu>();
+
+    // ---- piece of this work-group: XCD-aware order over the live tiles. XCD x (work-groups
+    //      b with b % 8 == x) owns a contiguous run of tiles and takes its work-groups in the
+    //      order b / 8. Whole tiles fill the XCD's slots in rounds; when the last round would
+    //      hold at most half the slots, its tiles are split into pieces of consecutive
+    //      ranges instead (each piece reloads the tile's rows), so that round ends after a
+    //      fraction of a tile. The results do not depend on the split. ----
     const int ntp = p.ntp ? p.ntp[0] : (int)p.P;
     const int64_t live_rows = std::min<int64_t>((int64_t)ntp, p.P);
     const int ntiles = (int)((live_rows + BM - 1) / BM);
     const int per_xcd = (ntiles + kArXcds - 1) / kArXcds;
     const int b = blockIdx.x;
-    if (b / kArXcds >= per_xcd) return;
-    const int tile = (b % kArXcds) * per_xcd + b / kArXcds;
-    if (tile >= ntiles) return;
+    const int t0 = (b % kArXcds) * per_xcd;
+    const int jx = b / kArXcds;
+    const int nx = std::max(0, std::min(per_xcd, ntiles - t0));
+    const int slots = std::max(p.xcd_slots, 1);
+    const int tail = nx % slots;
+    const int split = tail > 0 && 2 * tail <= slots ? std::min(slots / tail, nranges) : 1;
+    const int whole = split > 1 ? nx - tail : nx;
+    int tile, r_begin = 0, r_end = nranges;
+    if (jx < whole) {
+        tile = t0 + jx;
+    } else {
+        const int i = jx - whole;
+        if (split == 1 || i >= tail * split) return;
+        tile = t0 + whole + i / split;
+        r_begin = (i % split) * nranges / split;
+        r_end = (i % split + 1) * nranges / split;
+    }
     const int64_t row0 = (int64_t)tile * BM;
     const int e = p.expert_ids ? p.expert_ids[row0 / p.block_m] : 0;
     if (e < 0 || e >= p.E) return;
@@ -180,8 +202,6 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
         return sr >= 0 ? sr : fallback;
     };
 
-    const int ncols = kSilu ? p.N / 2 : p.N;
-    const int nranges = ncols / ar_range_cols<kSilu>();
     const uint32_t half_k = (uint32_t)K / 2;           // bytes per op-layout weight row
     const uint8_t* we = reinterpret_cast<const uint8_t*>(p.w) + (int64_t)e * p.N * half_k;
     const uint16_t* se = reinterpret_cast<const uint16_t*>(p.scales) + (int64_t)e * p.N * G;
@@ -202,25 +222,28 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
         frag_off[j] = FRAG ? (n0 / 16) * G * 1024u : n0 * half_k;
     }
     uint4 bw[kArD][kArNT];
-    uint32_t i_off = 0;          // step_off of the next issue
-    int i_g = 0, i_r = 0;        // its group and range
-    // Steps past the last range (at most the ring's four, never consumed) reload the last
+    uint32_t i_off = (uint32_t)r_begin * r_step;   // step_off of the next issue
+    int i_g = 0, i_r = r_begin;                     // its group and range
+    // Steps past the piece's last range (at most the ring's four, never consumed) reload that
     // range's final four groups, which this wave requested just before and are still in L2:
     // a work-group cannot retire before its loads return, so these must not go to HBM.
-    const uint32_t tail_off = (uint32_t)(nranges - 1) * r_step + (uint32_t)(G - kArD) * g_step;
+    const uint32_t tail_off = (uint32_t)(r_end - 1) * r_step + (uint32_t)(G - kArD) * g_step;
     auto issue = [&](auto slotc) __attribute__((always_inline)) {
         constexpr int sl = decltype(slotc)::value;
         const uint8_t* base = we + i_off;
 #pragma unroll
         for (int j = 0; j < kArNT; ++j) {
             const uint8_t* ptr = base + frag_off[j] + lane_off;
-            bw[sl][j] = FRAG ? load_stream16(ptr) : *reinterpret_cast<const uint4*>(ptr);
+            // ordinary (L2-allocating) loads: the tiles of one expert run at the same time
+            // on one XCD and read the same weights, so the lines must stay in L2 for the
+            // later ones (non-temporal loads cost c5 gemm1 467 against 361 us)
+            bw[sl][j] = *reinterpret_cast<const uint4*>(ptr);
         }
         i_off += g_step;
         if (++i_g == G) {
             i_g = 0;
             i_off += r_step - (uint32_t)G * g_step;
-            if (++i_r >= nranges) i_off = tail_off;
+            if (++i_r >= r_end) i_off = tail_off;
         }
     };
     using S0 = std::integral_constant<int, 0>;
@@ -239,7 +262,7 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
     uint2 pf_s[2];
     uint32_t pf_z;
     auto prefetch = [&](int r, int h) __attribute__((always_inline)) {
-        const int rr = std::min(r, nranges - 1);
+        const int rr = std::min(r, r_end - 1);
         const int n = ar_row<kSilu>(rr, wave, tj, tc, ncols);
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
@@ -292,7 +315,7 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
     //      then leaves the weights in flight behind the LDS writes and the table build ----
     // table halves of K: 64-row tiles take K <= 2048 (one half), 32-row tiles 2048 < K <= 4096
     constexpr int GH = BM == kArBM ? 1 : 2;
-    prefetch(0, 0);
+    prefetch(r_begin, 0);
     constexpr int kRowsPerWave = BM / kArWaves;
     constexpr int kAqPass = kArMaxKAq / 512;
     constexpr int kMaxChunks = ar_max_k<BM>() / 16 * BM / kArThreads;   // 16-byte chunks per thread
@@ -400,13 +423,13 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
         }
         if (wave == 0 && lane < BM) s_asc[lane] = ascv;
     }
-    build(0, 0);
+    build(r_begin, 0);
     // the tables' next (range, half), prefetched right after each build
     auto prefetch_after = [&](int r, int h) __attribute__((always_inline)) {
         if (h + 1 < GH) prefetch(r, h + 1);
-        else if (r + 1 < nranges) prefetch(r + 1, 0);
+        else if (r + 1 < r_end) prefetch(r + 1, 0);
     };
-    prefetch_after(0, 0);
+    prefetch_after(r_begin, 0);
     lds_barrier();
 
     auto main_loop = [&](auto nflc) __attribute__((always_inline)) {
@@ -568,7 +591,7 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
         };
         using F0 = std::false_type;
         using F1 = std::true_type;
-        for (int r = 0; r < nranges; ++r) {
+        for (int r = r_begin; r < r_end; ++r) {
             // Waves w and w + 4 share a SIMD and the issue arbiter favours one of them; the
             // higher priority alternates between the two every range, so neither falls a
             // whole tile behind (the work-group ends with its slowest wave).
@@ -591,7 +614,7 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
                 zterm(1, F0{});
             }
             store_range(r);
-            if (r + 1 < nranges) {
+            if (r + 1 < r_end) {
                 build(r + 1, 0);
                 prefetch_after(r + 1, 0);
             }
@@ -623,10 +646,36 @@ int launch_ares_bm(const Params& p, hipStream_t s) {
         }
         attr_set = true;
     }
-    // a multiple of 8 work-groups covers every tile under the XCD-aware order
+    // work-groups one XCD holds at once (the split of the last round is sized to it)
+    static int occ_lds[4] = {-1, -1, -1, -1}, occ_val[4] = {0, 0, 0, 0};
+    static int ncu = 0;
+    if (ncu == 0) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            ncu <= 0)
+            ncu = 256;
+    }
+    int occ = 0;
+    for (int i = 0; i < 4 && occ == 0; ++i) {
+        if (occ_lds[i] == (int)lds) occ = occ_val[i];
+        else if (occ_lds[i] < 0) {
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                    &occ, reinterpret_cast<const void*>(&prefill_ares_kernel<EPI, FRAG, BM>),
+                    kArThreads, lds) != hipSuccess || occ <= 0)
+                occ = 1;
+            occ_lds[i] = (int)lds;
+            occ_val[i] = occ;
+        }
+    }
+    if (occ == 0) occ = 1;
+    Params q = p;
+    q.xcd_slots = std::max(1, ncu * occ / kArXcds);
+    // a multiple of 8 work-groups covers every tile under the XCD-aware order, plus one more
+    // slot's worth per XCD for the pieces of a split last round
     const int64_t tiles = (p.P + BM - 1) / BM;
-    const unsigned grid = (unsigned)((tiles + kArXcds - 1) / kArXcds * kArXcds);
-    launch_kernel(&prefill_ares_kernel<EPI, FRAG, BM>, dim3(grid), dim3(kArThreads), lds, s, p);
+    const unsigned grid = (unsigned)(((tiles + kArXcds - 1) / kArXcds + q.xcd_slots) * kArXcds);
+    launch_kernel(&prefill_ares_kernel<EPI, FRAG, BM>, dim3(grid), dim3(kArThreads), lds, s, q);
     return check_launch("prefill_ares_kernel");
 }
 
