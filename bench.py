@@ -204,11 +204,12 @@ def gemm1_kernel_name(cfg, decode, layout, fused=False):
         split = {1: "1, 1", 2: "2, 1", 3: "3, 1", 4: "4, 1", 8: "4, 2", 12: "3, 4", 16: "4, 4",
                  32: "8, 4"}[H // 128]
         return f"grouped_gemv_kernel<kSiluHalf, {split}, false, {frag}>"
-    # activation-resident tiles: 64 rows up to K = 2048, 32 rows up to K = 4096
+    # activation-resident tiles: 64 rows up to K = 2048, 32 rows up to K = 4096; gemm1 takes
+    # prequantised rows (the last template argument, SQ, is false)
     if H % 512 == 0 and H <= 2048:
-        return f"prefill_ares_kernel<kSiluHalf, {frag}, 64>"
+        return f"prefill_ares_kernel<kSiluHalf, {frag}, 64, false>"
     if H % 512 == 0 and H <= 4096:
-        return f"prefill_ares_kernel<kSiluHalf, {frag}, 32>"
+        return f"prefill_ares_kernel<kSiluHalf, {frag}, 32, false>"
     return f"prefill_mfma_kernel<kSiluHalf, 4, {frag}>"
 
 

@@ -130,9 +130,13 @@ __device__ __forceinline__ uint32_t pack_bf16x2(__bf16 a, __bf16 b) {
     return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
 }
 
-template <Epi EPI, bool FRAG, int BM>
+// SQ: the tile quantises fp16 rows itself (fp16 output, K <= kArMaxKAq); otherwise it loads
+// prequantised rows. A compile-time choice: with both prologues in one kernel the compiler
+// kept the 16-chunk row staging array in scratch, each store waiting for its load.
+template <Epi EPI, bool FRAG, int BM, bool SQ>
 __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
     constexpr bool kSilu = EPI == Epi::kSiluHalf;
+    static_assert(!(SQ && kSilu), "gemm1 tiles take prequantised rows");
     constexpr int GPR = ar_gpr<BM>();
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
 
@@ -258,10 +262,17 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
     //      wave's 8-row group l >> 4; a row's group then reads its 8 words from the staging
     //      area ----
     const int trow = lane & 31, tj = trow >> 4, tc = trow & 15, th = lane >> 5;
+    // The range-boundary code (prefetch, build) recomputes its lane-derived indices from an
+    // opaque copy of the lane id: hoisted out of the range loop, they stayed live across the
+    // main loop and were spilled, and each range start then reloaded them from scratch behind
+    // a wait that drained the weight ring.
+    auto lane_now = [&]() __attribute__((always_inline)) { int l = lane; asm volatile("" : "+v"(l)); return l; };
     const int lrow = 32 * wave + trow;
     uint2 pf_s[2];
     uint32_t pf_z;
     auto prefetch = [&](int r, int h) __attribute__((always_inline)) {
+        const int lane = lane_now();
+        const int tj = (lane & 31) >> 4, tc = lane & 15, th = lane >> 5;
         const int rr = std::min(r, r_end - 1);
         const int n = ar_row<kSilu>(rr, wave, tj, tc, ncols);
 #pragma unroll
@@ -276,6 +287,8 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
         pf_z = ze ? (uint32_t)ze[(uint32_t)(nz >> 3) * G + wz] : *reinterpret_cast<const uint32_t*>(se);
     };
     auto build = [&](int r, int h) __attribute__((always_inline)) {
+        const int lane = lane_now();
+        const int tj = (lane & 31) >> 4, tc = lane & 15, th = lane >> 5, lrow = 32 * wave + (lane & 31);
         const int n = ar_row<kSilu>(r, wave, tj, tc, ncols);
         s_zst[64 * wave + lane] = pf_z;
         uint32_t zw[8];
@@ -319,14 +332,14 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
     constexpr int kRowsPerWave = BM / kArWaves;
     constexpr int kAqPass = kArMaxKAq / 512;
     constexpr int kMaxChunks = ar_max_k<BM>() / 16 * BM / kArThreads;   // 16-byte chunks per thread
-    const bool self_quant = !kSilu && p.xq == nullptr;
+    constexpr bool self_quant = SQ;
     const int cpr = K / 16;                             // chunks per row
     const int total = BM * cpr;                         // multiple of 512 (K % 512 == 0)
-    uint4 raw[kRowsPerWave][kAqPass];                   // fp16 rows (self-quantising tiles)
-    uint4 va[kMaxChunks];                               // e4m3 tile chunks (prequantised rows)
+    uint4 raw[SQ ? kRowsPerWave : 1][SQ ? kAqPass : 1]; // fp16 rows (self-quantising tiles)
+    uint4 va[SQ ? 1 : kMaxChunks];                      // e4m3 tile chunks (prequantised rows)
     float asv[BM * GPR / kArThreads];                   // row group sums
     float ascv = 0.f;
-    if (self_quant) {
+    if constexpr (self_quant) {
         // fp16 rows in (the tile owns its rows: each is read by this work-group only);
         // wave w quantises tile rows 8w .. 8w + 7 below
         const int npass = K / 512;                      // 1 or 2 (K <= kArMaxKAq)
@@ -358,7 +371,7 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
     issue(S1{});
     issue(S2{});
     issue(S3{});
-    if (self_quant) {
+    if constexpr (self_quant) {
         // as act_quant_kernel: s = max(absmax / 448, 1e-8), e4m3 RNE of x / s in k8-interleaved
         // order, per-group sums of the e4m3 values by the same lane tree; straight into LDS
         const int npass = K / 512;
@@ -633,12 +646,12 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
     }
 }
 
-template <Epi EPI, bool FRAG, int BM>
+template <Epi EPI, bool FRAG, int BM, bool SQ>
 int launch_ares_bm(const Params& p, hipStream_t s) {
     const size_t lds = ar_lds_bytes<BM>(p.K);
     static bool attr_set = false;
     if (!attr_set) {   // > 64 KB of dynamic LDS needs an explicit opt-in
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_ares_kernel<EPI, FRAG, BM>),
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_ares_kernel<EPI, FRAG, BM, SQ>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)ar_lds_bytes<BM>(ar_max_k<BM>())) != hipSuccess) {
             set_error("prefill_ares_kernel: cannot reserve dynamic LDS");
@@ -661,7 +674,7 @@ int launch_ares_bm(const Params& p, hipStream_t s) {
         if (occ_lds[i] == (int)lds) occ = occ_val[i];
         else if (occ_lds[i] < 0) {
             if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                    &occ, reinterpret_cast<const void*>(&prefill_ares_kernel<EPI, FRAG, BM>),
+                    &occ, reinterpret_cast<const void*>(&prefill_ares_kernel<EPI, FRAG, BM, SQ>),
                     kArThreads, lds) != hipSuccess || occ <= 0)
                 occ = 1;
             occ_lds[i] = (int)lds;
@@ -675,15 +688,19 @@ int launch_ares_bm(const Params& p, hipStream_t s) {
     // slot's worth per XCD for the pieces of a split last round
     const int64_t tiles = (p.P + BM - 1) / BM;
     const unsigned grid = (unsigned)(((tiles + kArXcds - 1) / kArXcds + q.xcd_slots) * kArXcds);
-    launch_kernel(&prefill_ares_kernel<EPI, FRAG, BM>, dim3(grid), dim3(kArThreads), lds, s, q);
+    launch_kernel(&prefill_ares_kernel<EPI, FRAG, BM, SQ>, dim3(grid), dim3(kArThreads), lds, s, q);
     return check_launch("prefill_ares_kernel");
 }
 
 // 64-row tiles up to K = 2048; 32-row tiles (the activation tile halves) up to K = 4096
 template <Epi EPI, bool FRAG>
 int launch_ares_t(const Params& p, hipStream_t s) {
-    return p.K <= kArMaxK ? launch_ares_bm<EPI, FRAG, kArBM>(p, s)       // one table half
-                          : launch_ares_bm<EPI, FRAG, kArBMWide>(p, s);  // two (2048 < K <= 4096)
+    if constexpr (EPI == Epi::kHalf) {
+        if (p.xq == nullptr)   // self-quantising tiles: K <= kArMaxKAq, so 64 rows
+            return launch_ares_bm<EPI, FRAG, kArBM, true>(p, s);
+    }
+    return p.K <= kArMaxK ? launch_ares_bm<EPI, FRAG, kArBM, false>(p, s)       // one table half
+                          : launch_ares_bm<EPI, FRAG, kArBMWide, false>(p, s);  // two (K <= 4096)
 }
 
 }  // namespace
