@@ -116,6 +116,12 @@ __device__ __forceinline__ __half silu_mul_tile(float gate, float up) {
 }
 
 using bf16x8 = __bf16 __attribute__((ext_vector_type(8)));
+using lds_void_ptr = __attribute__((address_space(3))) void*;
+using global_cvoid_ptr = const __attribute__((address_space(1))) void*;
+
+// s_waitcnt operand waiting for at most n outstanding vector memory operations only
+// (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt 6:4 and lgkmcnt 11:8 at their maxima)
+constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
 __device__ __forceinline__ v4f mfma_bf16_16x16x32(const bf16x8& a, const bf16x8& b, const v4f& c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -323,21 +329,33 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
         *reinterpret_cast<uint4*>(s_szl + lrow * kArGp + 8 * th) = make_uint4(szl[0], szl[1], szl[2], szl[3]);
     };
 
-    // ---- prologue. Loads first, in this order: range 0's tables, the activation rows (and
-    //      their scales and group sums), the first four weight steps; waiting for the rows
-    //      then leaves the weights in flight behind the LDS writes and the table build ----
+    // ---- prologue. Loads first, in this order: the first range's tables, the activation rows
+    //      (self-quantising tiles: fp16 rows into registers; otherwise the row scales and group
+    //      sums, then the e4m3 tile straight into LDS), the first four weight steps; the
+    //      weights stay in flight behind the table build ----
     // table halves of K: 64-row tiles take K <= 2048 (one half), 32-row tiles 2048 < K <= 4096
     constexpr int GH = BM == kArBM ? 1 : 2;
     prefetch(r_begin, 0);
     constexpr int kRowsPerWave = BM / kArWaves;
     constexpr int kAqPass = kArMaxKAq / 512;
-    constexpr int kMaxChunks = ar_max_k<BM>() / 16 * BM / kArThreads;   // 16-byte chunks per thread
     constexpr bool self_quant = SQ;
-    const int cpr = K / 16;                             // chunks per row
-    const int total = BM * cpr;                         // multiple of 512 (K % 512 == 0)
     uint4 raw[SQ ? kRowsPerWave : 1][SQ ? kAqPass : 1]; // fp16 rows (self-quantising tiles)
-    uint4 va[SQ ? 1 : kMaxChunks];                      // e4m3 tile chunks (prequantised rows)
     float asv[BM * GPR / kArThreads];                   // row group sums
+    // Prequantised rows go straight into the LDS tile (global_load_lds, 16 bytes per lane; no
+    // registers, no LDS writes): a wave instruction fills one contiguous KB, rows
+    // 8 rb .. 8 rb + 7 of one K group, lane l writing row 8 rb + l / 8 at 16-byte slot l % 8,
+    // which holds the row's chunk (l % 8) ^ (row & 7) (the tile's swizzle). Instruction i,
+    // issued by wave i % 8, covers group i / (BM / 8), row block i % (BM / 8), so a wave
+    // always fills the same row block and each lane's source row and chunk are fixed: one
+    // 32-bit offset (x_rows * K < 2^31, checked at launch). The whole tile goes out before
+    // the first weight steps. (Loading the first range's later groups behind its first
+    // passes was tried: the compiler cannot tell the tile reads from the DMA writes still in
+    // flight and waits for all of them, vmcnt(0), before each read, draining the ring.)
+    constexpr int kRB = BM / 8;                         // row blocks per K group
+    const int act_row = (wave % kRB) * 8 + (lane >> 3);
+    const uint32_t act_off = SQ ? 0u : (uint32_t)src_of(act_row) * (uint32_t)K +
+                                           ((uint32_t)((lane & 7) ^ (act_row & 7)) << 4);
+    uint8_t* const act_dst = s_a + (wave % kRB) * 8 * kGroup;   // + group offset; wave-uniform
     float ascv = 0.f;
     if constexpr (self_quant) {
         // fp16 rows in (the tile owns its rows: each is read by this work-group only);
@@ -353,12 +371,6 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
                     xh + (int64_t)sr * K + std::min(ps, npass - 1) * 512 + lane * 8);
         }
     } else {
-        // chunk c: row c / cpr, bytes (c % cpr) * 16; chunks past the tile repeat the last
-#pragma unroll
-        for (int u = 0; u < kMaxChunks; ++u) {
-            const int c = min(u * kArThreads + tid, total - 1);
-            va[u] = *reinterpret_cast<const uint4*>(p.xq + (int64_t)src_of(c / cpr) * K + (c % cpr) * 16);
-        }
 #pragma unroll
         for (int j = 0; j < BM * GPR / kArThreads; ++j) {   // row sums; groups >= G are 0
             const int i = j * kArThreads + tid;
@@ -366,6 +378,12 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
             asv[j] = i % GPR < G ? p.asum[(int64_t)sr * G + i % GPR] : 0.f;
         }
         if (wave == 0 && src >= 0) ascv = p.asc[src];
+        for (int i = wave; i < G * kRB; i += kArWaves) {     // instruction i: group i / kRB
+            const int g = i / kRB;
+            __builtin_amdgcn_global_load_lds((global_cvoid_ptr)(p.xq + act_off + (uint32_t)g * kGroup),
+                                             (lds_void_ptr)(act_dst + g * ar_a_group_bytes<BM>()),
+                                             16, 0, 0);
+        }
     }
     issue(S0{});
     issue(S1{});
@@ -422,12 +440,6 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
         }
     } else {
 #pragma unroll
-        for (int u = 0; u < kMaxChunks; ++u) {
-            const int c = u * kArThreads + tid;
-            if (c < total)
-                *reinterpret_cast<uint4*>(s_a + ar_a_off<BM>(c / cpr, (c % cpr) >> 3, c & 7)) = va[u];
-        }
-#pragma unroll
         for (int j = 0; j < BM * GPR / kArThreads; ++j) {
             const int i = j * kArThreads + tid;
             const __bf16 h = (__bf16)asv[j];
@@ -443,6 +455,11 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
         else if (r + 1 < r_end) prefetch(r + 1, 0);
     };
     prefetch_after(r_begin, 0);
+    if constexpr (!self_quant) {
+        // the tile's DMA done: at most the weight steps issued after it still pending (and
+        // the tables' prefetch when issued, so this may wait for a little more)
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm(4 * kArNT));
+    }
     lds_barrier();
 
     auto main_loop = [&](auto nflc) __attribute__((always_inline)) {
