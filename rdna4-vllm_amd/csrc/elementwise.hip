@@ -86,7 +86,7 @@ __global__ void gather_reduce_kernel(const __half* __restrict__ out2,
     out[t * N + n] = acc;
 }
 
-template <bool BF16>
+template <bool BF16, int KMAX>
 __global__ void slot_reduce_kernel(const float* __restrict__ y, const float* __restrict__ tw,
                                    const int32_t* __restrict__ ids,
                                    const int32_t* __restrict__ emap, int emap_len, int E,
@@ -102,17 +102,46 @@ __global__ void slot_reduce_kernel(const float* __restrict__ y, const float* __r
         for (int i = threadIdx.x; i < sync.nflags; i += blockDim.x) sync.flags[i] = 0;
     if (n >= N || t >= T) return;
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 8
-    for (int j = 0; j < top_k; ++j) {
+    auto expert_of = [&](int j) {
         int e = ids[t * top_k + j];
         if (emap != nullptr) e = (e >= 0 && e < emap_len) ? emap[e] : -1;
-        if (e < 0 || e >= E) continue;
-        const float w = tw[t * top_k + j];
-        const float4 v = *reinterpret_cast<const float4*>(y + (t * top_k + j) * N + n);
-        acc[0] = fmaf(w, v.x, acc[0]);
-        acc[1] = fmaf(w, v.y, acc[1]);
-        acc[2] = fmaf(w, v.z, acc[2]);
-        acc[3] = fmaf(w, v.w, acc[3]);
+        return e;
+    };
+    if constexpr (KMAX > 0) {
+        // the token's ids, weights and all its slot rows requested together (every slot row
+        // exists; a slot without a local expert is read and left out), then summed over j
+        // ascending: one memory round trip instead of one per slot
+        int e[KMAX];
+        float w[KMAX];
+        float4 v[KMAX];
+#pragma unroll
+        for (int j = 0; j < KMAX; ++j) {
+            if (j < top_k) {
+                e[j] = expert_of(j);
+                w[j] = tw[t * top_k + j];
+                v[j] = *reinterpret_cast<const float4*>(y + (t * top_k + j) * N + n);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < KMAX; ++j) {
+            if (j < top_k && e[j] >= 0 && e[j] < E) {
+                acc[0] = fmaf(w[j], v[j].x, acc[0]);
+                acc[1] = fmaf(w[j], v[j].y, acc[1]);
+                acc[2] = fmaf(w[j], v[j].z, acc[2]);
+                acc[3] = fmaf(w[j], v[j].w, acc[3]);
+            }
+        }
+    } else {
+        for (int j = 0; j < top_k; ++j) {
+            const int e = expert_of(j);
+            if (e < 0 || e >= E) continue;
+            const float w = tw[t * top_k + j];
+            const float4 v = *reinterpret_cast<const float4*>(y + (t * top_k + j) * N + n);
+            acc[0] = fmaf(w, v.x, acc[0]);
+            acc[1] = fmaf(w, v.y, acc[1]);
+            acc[2] = fmaf(w, v.z, acc[2]);
+            acc[3] = fmaf(w, v.w, acc[3]);
+        }
     }
     if (failed)
 #pragma unroll
@@ -268,13 +297,20 @@ int launch_slot_reduce(const float* y, const float* tw, const int32_t* ids,
                        int64_t top_k, void* out, bool out_bf16, hipStream_t stream,
                        SlotReduceSync sync) {
     if (T == 0 || N == 0) return W4A8_OK;
-    dim3 grid(blocks_for(N / 4, 256), (unsigned)T);
-    if (out_bf16)
-        slot_reduce_kernel<true><<<grid, 256, 0, stream>>>(y, tw, ids, emap, (int)emap_len,
-                                                          (int)E, T, (int)N, (int)top_k, out, sync);
-    else
-        slot_reduce_kernel<false><<<grid, 256, 0, stream>>>(y, tw, ids, emap, (int)emap_len,
-                                                           (int)E, T, (int)N, (int)top_k, out, sync);
+    // 128 threads of four columns per work-group: a decode batch spreads over more CUs
+    dim3 grid(blocks_for(N / 4, 128), (unsigned)T);
+    auto go = [&](auto kernel) {
+        kernel<<<grid, 128, 0, stream>>>(y, tw, ids, emap, (int)emap_len, (int)E, T, (int)N,
+                                         (int)top_k, out, sync);
+    };
+    if (top_k <= 8) {
+        if (out_bf16) go(slot_reduce_kernel<true, 8>);
+        else go(slot_reduce_kernel<false, 8>);
+    } else if (out_bf16) {
+        go(slot_reduce_kernel<true, 0>);
+    } else {
+        go(slot_reduce_kernel<false, 0>);
+    }
     return check_launch("slot_reduce_kernel");
 }
 
