@@ -211,7 +211,7 @@ W4A8_API int w4a8_repack_int4_fragments(const int32_t* w_packed, int64_t E, int6
  * and zero-points stay in the op layout. Same workspace (w4a8_moe_apply_workspace_size) and
  * bit-identical results. Needs group_size 128 and int4 weights (no E2M1); hidden and
  * intermediate sizes must be multiples of 128 that the schedule chosen for T takes: the
- * decode GEMV (T <= 96) needs K/128 in {1,2,3,4,8,12,16,32}, the prefill tiles K <= 4096.
+ * decode GEMV (T <= 96) needs K/128 in {1,2,3,4,6,8,12,16,32}, the prefill tiles K <= 4096.
  * No reference counterpart (the reference's composition, moe_experts.py:493-665, runs on
  * the op layout). */
 W4A8_API int w4a8_moe_apply_fragments(const void* x, int x_dtype, int64_t T, int64_t H,

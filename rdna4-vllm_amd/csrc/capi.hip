@@ -265,7 +265,7 @@ int moe_apply_impl(const void* x, int x_dtype, int64_t T, int64_t H, int64_t int
     const ApplyPlan pl = plan_apply(T, E, top_k);
     W4A8_REQUIRE(!frag || (!weight_is_e2m1 && fragments_schedule_ok(pl.decode, H, inter, group_size)),
                  "fragment-layout weights need int4 g128 with hidden and intermediate sizes the "
-                 "chosen schedule takes (decode GEMV: K/128 in {1,2,3,4,8,12,16,32}; prefill "
+                 "chosen schedule takes (decode GEMV: K/128 in {1,2,3,4,6,8,12,16,32}; prefill "
                  "tiles: K <= 4096)");
     if (T == 0) return W4A8_OK;
     W4A8_REQUIRE(x && w13 && w13_scales_f16 && w2 && w2_scales_f16 && topk_weights && topk_ids && out,

@@ -885,6 +885,7 @@ GemvSplit gemv_split(int G) {
         case 2: return {2, 1};
         case 3: return {3, 1};
         case 4: return {4, 1};
+        case 6: return {3, 2};
         case 8: return {4, 2};
         case 12: return {3, 4};
         case 16: return {4, 4};
@@ -951,6 +952,7 @@ int launch_gemv_e(const Params& p, int tpt, hipStream_t s) {
         case 1 * 8 + 1: return launch_gemv_t<EPI, 1, 1>(p, tpt, s);
         case 2 * 8 + 1: return launch_gemv_t<EPI, 2, 1>(p, tpt, s);
         case 3 * 8 + 1: return launch_gemv_t<EPI, 3, 1>(p, tpt, s);
+        case 3 * 8 + 2: return launch_gemv_t<EPI, 3, 2>(p, tpt, s);
         case 4 * 8 + 1: return launch_gemv_t<EPI, 4, 1>(p, tpt, s);
         case 4 * 8 + 2: return launch_gemv_t<EPI, 4, 2>(p, tpt, s);
         case 3 * 8 + 4: return launch_gemv_t<EPI, 3, 4>(p, tpt, s);
@@ -1013,7 +1015,7 @@ int launch_grouped_gemv_tpt(const GroupedArgs& a, int tpt, hipStream_t s) {
         return W4A8_ERR_INVALID;
     }
     if (!gemv_supported(a.K, a.group_size)) {
-        set_error("gemv grouped GEMM: K / group_size must be one of 1,2,3,4,8,12,16,32");
+        set_error("gemv grouped GEMM: K / group_size must be one of 1,2,3,4,6,8,12,16,32");
         return W4A8_ERR_INVALID;
     }
     if (a.e2m1) {

@@ -180,7 +180,7 @@ bool prefill_supported(int64_t K, int64_t group_size, bool e2m1);   // g128, K <
 int launch_grouped_gemv_tpt(const GroupedArgs& a, int tiles_per_team, hipStream_t stream);
 // the matrix-core tiles take the shape (int4: group 128; E2M1: groups of 32, 64 or 128)
 bool mfma_supported(int64_t K, int64_t group_size, bool e2m1 = false);
-// mfma_supported and K / group_size in {1,2,3,4,8,12,16,32} (split-K table of the GEMV)
+// mfma_supported and K / group_size in {1,2,3,4,6,8,12,16,32} (split-K table of the GEMV)
 bool gemv_supported(int64_t K, int64_t group_size);
 
 // Whole-layer decode GEMV on fragment-layout weights (decode_gemv.hip): each work-group

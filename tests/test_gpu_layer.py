@@ -399,3 +399,22 @@ def test_graph_replay_forward_fragments_fresh_inputs(T):
         torch.cuda.synchronize()
         assert torch.equal(got[2], ref[2]) and torch.equal(got[1], ref[1]), r
         assert torch.equal(got[0], ref[0]), r
+
+
+@pytest.mark.parametrize("T", [1, 8, 32, 96])
+@pytest.mark.parametrize("frag", [False, True])
+def test_decode_six_group_intermediate(T, frag):
+    """An intermediate size of 768 (K/128 = 6 for gemm2, Qwen3-30B-A3B-shaped) runs the decode
+    GEMV (split table entry 6 = 3 groups per wave, two waves per team) against the oracle, on
+    op-layout and fragment weights, and the two layouts agree bit for bit."""
+    cfg, ws, x, tw, ids = small_layer(800 + T, T, 32, 512, 768, 4)
+    assert W.fragments_supported(512, 768, 128)
+    w13, w2 = ws["w13"], ws["w2"]
+    if frag:
+        w13, w2 = W.repack_fragments(w13), W.repack_fragments(w2)
+    out = W.moe_apply(x, w13, w2, ws["s13"], ws["s2"], ws["z13"], ws["z2"], tw, ids)
+    ref = oracle_layer(cfg, ws, x, tw, ids)
+    assert maxrel(out.float().cpu().numpy(), ref) <= REL_TOL
+    if frag:
+        op = W.moe_apply(x, ws["w13"], ws["w2"], ws["s13"], ws["s2"], ws["z13"], ws["z2"], tw, ids)
+        assert torch.equal(out, op)
