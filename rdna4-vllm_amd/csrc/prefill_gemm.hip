@@ -56,31 +56,45 @@ __device__ __forceinline__ bool prefill_item(int nblocks, int ntiles, int& m_blo
     return true;
 }
 
+// Loads take a wave-uniform base plus a 32-bit per-lane byte offset, so they issue in the
+// scalar-base form (one offset register per load, no 64-bit address arithmetic per lane).
+// The offset passes through an opaque copy: otherwise loop strength reduction turns each
+// address into a 64-bit per-lane induction variable (two registers per load stream), which
+// pushed the 64- and 128-row tiles into scratch.
+__device__ __forceinline__ uint32_t pf_opaque(uint32_t v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+// A staging pieces as native 4 x u32 vectors (an array of the uint4 wrapper struct was kept
+// in scratch, each piece stored there as soon as its load returned)
+using u32x4 = uint32_t __attribute__((ext_vector_type(4)));
 template <int A_CHUNKS>
-__device__ __forceinline__ void pf_load_a(uint4 (&reg)[A_CHUNKS], const uint8_t* __restrict__ xq,
+__device__ __forceinline__ void pf_load_a(u32x4 (&reg)[A_CHUNKS], const uint8_t* __restrict__ xq,
                                           const uint32_t (&src)[A_CHUNKS], int gg) {
+    const uint8_t* base = xq + (uint32_t)gg * kGroup;
 #pragma unroll
-    for (int i = 0; i < A_CHUNKS; ++i)
-        reg[i] = *reinterpret_cast<const uint4*>(xq + src[i] + gg * kGroup);
+    for (int i = 0; i < A_CHUNKS; ++i) reg[i] = *reinterpret_cast<const u32x4*>(base + pf_opaque(src[i]));
 }
 template <int A_CHUNKS>
-__device__ __forceinline__ void pf_store_a(const uint4 (&reg)[A_CHUNKS], uint8_t* dst,
+__device__ __forceinline__ void pf_store_a(const u32x4 (&reg)[A_CHUNKS], uint8_t* dst,
                                            const int (&off)[A_CHUNKS]) {
 #pragma unroll
-    for (int i = 0; i < A_CHUNKS; ++i) *reinterpret_cast<uint4*>(dst + off[i]) = reg[i];
+    for (int i = 0; i < A_CHUNKS; ++i) *reinterpret_cast<u32x4*>(dst + off[i]) = reg[i];
 }
-// FRAG: fragment-layout weights (repack.hip), lane l's 16 bytes of block (row / 16, group)
-// at offset 16 l; otherwise op layout, row wrow, words 16 gg + 4 q.
-template <bool FRAG>
+// B fragments of group gg: weight bytes at wb + gg * gstep + woff[j] (fragment layout:
+// lane l's 16 bytes of block (row / 16, group) at ((row / 16) * G + group) * 1 KB + 16 l, so
+// gstep = 1 KB; op layout: row * K / 2 + 64 group + 16 q, gstep = 64), the fp16 scale at
+// sb + 2 gg + soff[j] (soff = 2 row G).
 __device__ __forceinline__ void pf_load_b(uint4 (&w)[kPfNT], uint32_t (&sc)[kPfNT],
-                                          const int32_t* __restrict__ we, const uint16_t* __restrict__ se,
-                                          const int (&wrow)[kPfNT], int kw_row, int G, int gg, int lane) {
+                                          const uint8_t* __restrict__ wb, uint32_t gstep,
+                                          const uint32_t (&woff)[kPfNT], const uint8_t* __restrict__ sb,
+                                          const uint32_t (&soff)[kPfNT], int gg) {
+    const uint8_t* wg = wb + (uint32_t)gg * gstep;
+    const uint8_t* sg = sb + (uint32_t)gg * 2u;
 #pragma unroll
     for (int j = 0; j < kPfNT; ++j) {
-        const int32_t* src = FRAG ? we + ((int64_t)(wrow[j] >> 4) * G + gg) * 256 + lane * 4
-                                  : we + (int64_t)wrow[j] * kw_row + gg * (kGroup / 8) + (lane >> 4) * 4;
-        w[j] = *reinterpret_cast<const uint4*>(src);
-        sc[j] = se[(int64_t)wrow[j] * G + gg];
+        w[j] = *reinterpret_cast<const uint4*>(wg + pf_opaque(woff[j]));
+        sc[j] = *reinterpret_cast<const uint16_t*>(sg + pf_opaque(soff[j]));
     }
 }
 
@@ -113,7 +127,8 @@ __global__ void __launch_bounds__(256, 1) prefill_mfma_kernel(Params p, int nblo
     if (!prefill_item(live_blocks, ntiles, m_block, n_tile)) return;
     const int64_t row0 = (int64_t)m_block * BM;
     if (row0 >= ntp || row0 >= p.P) return;
-    const int e = p.expert_ids ? p.expert_ids[row0 / p.block_m] : 0;
+    // wave-uniform in a scalar register, so weight addresses are a scalar base + lane offset
+    const int e = __builtin_amdgcn_readfirstlane(p.expert_ids ? p.expert_ids[row0 / p.block_m] : 0);
     if (e < 0 || e >= p.E) return;
 
     const int tid = threadIdx.x;
@@ -142,7 +157,7 @@ __global__ void __launch_bounds__(256, 1) prefill_mfma_kernel(Params p, int nblo
         if (src >= 0) atomicMax(&s_maxrow, tid);
     }
     __syncthreads();
-    const int maxrow = s_maxrow;
+    const int maxrow = __builtin_amdgcn_readfirstlane(s_maxrow);
     if (maxrow < 0) return;                       // uniform: no real row in this tile
     const int nfl = maxrow / 16 + 1;              // live 16-row fragments
     const int fallback_src = s_src[maxrow];       // a real row: padding rows read it
@@ -236,7 +251,17 @@ __global__ void __launch_bounds__(256, 1) prefill_mfma_kernel(Params p, int nblo
     // alternate with the group parity (compile-time indices: the loop is unrolled by 2).
     uint4 wv0[kPfNT], wv1[kPfNT];
     uint32_t sv0[kPfNT], sv1[kPfNT];
-    const uint16_t* se16 = reinterpret_cast<const uint16_t*>(se);
+    // per-lane byte offsets of the B fragments and scales (an expert's slice is < 2^31 bytes)
+    const uint8_t* wb = reinterpret_cast<const uint8_t*>(we);
+    const uint8_t* sb = reinterpret_cast<const uint8_t*>(se);
+    const uint32_t gstep = FRAG ? 1024u : (uint32_t)kGroup / 2;
+    uint32_t woff[kPfNT], soff[kPfNT];
+#pragma unroll
+    for (int j = 0; j < kPfNT; ++j) {
+        woff[j] = FRAG ? (uint32_t)(wrow[j] >> 4) * (uint32_t)G * 1024u + (uint32_t)lane * 16u
+                       : (uint32_t)wrow[j] * (uint32_t)(p.K / 2) + (uint32_t)q * 16u;
+        soff[j] = (uint32_t)wrow[j] * (uint32_t)G * 2u;
+    }
     // one group of MFMAs on LDS slot g & 1 with spread B fragments bf and scales s
     auto mma = [&](const v8i (&bf)[kPfNT], const float (&s)[kPfNT], int g) {
         const uint8_t* A = s_a + (g & 1) * (BM * kPfAStride) + c16 * kPfAStride + q * 32;
@@ -261,23 +286,23 @@ __global__ void __launch_bounds__(256, 1) prefill_mfma_kernel(Params p, int nblo
     // B runs two groups ahead in two register sets (alternating with the group parity; the
     // loop is unrolled by 2); A runs one group ahead: A(g+1) is requested at the top of
     // group g and lands in the other LDS slot at its end.
-    pf_load_b<FRAG>(wv0, sv0, we, se16, wrow, kw_row, G, 0, lane);
-    pf_load_b<FRAG>(wv1, sv1, we, se16, wrow, kw_row, G, min(1, Gl), lane);
+    pf_load_b(wv0, sv0, wb, gstep, woff, sb, soff, 0);
+    pf_load_b(wv1, sv1, wb, gstep, woff, sb, soff, min(1, Gl));
     {
-        uint4 a_reg[A_CHUNKS];
+        u32x4 a_reg[A_CHUNKS];
         pf_load_a(a_reg, p.xq, a_src, 0);
         pf_store_a(a_reg, slot(0), a_dst);
     }
     __syncthreads();
     for (int g = 0; g < G; g += 2) {
         {
-            uint4 a_reg[A_CHUNKS];
+            u32x4 a_reg[A_CHUNKS];
             pf_load_a(a_reg, p.xq, a_src, min(g + 1, Gl));
             v8i bf[kPfNT];
             float sc[kPfNT];
 #pragma unroll
             for (int j = 0; j < kPfNT; ++j) { bf[j] = spread_nibbles(wv0[j]); sc[j] = half_bits(sv0[j]); }
-            pf_load_b<FRAG>(wv0, sv0, we, se16, wrow, kw_row, G, min(g + 2, Gl), lane);
+            pf_load_b(wv0, sv0, wb, gstep, woff, sb, soff, min(g + 2, Gl));
             mma(bf, sc, g);
             pf_store_a(a_reg, slot(g + 1), a_dst);
             lds_barrier();
@@ -287,13 +312,13 @@ __global__ void __launch_bounds__(256, 1) prefill_mfma_kernel(Params p, int nblo
             // dynamically through scratch): with odd G the extra half re-reads the last
             // group and folds it with scale 0, which adds exactly nothing to finite sums
             const float live = g + 1 < G ? 1.0f : 0.0f;
-            uint4 a_reg[A_CHUNKS];
+            u32x4 a_reg[A_CHUNKS];
             pf_load_a(a_reg, p.xq, a_src, min(g + 2, Gl));
             v8i bf[kPfNT];
             float sc[kPfNT];
 #pragma unroll
             for (int j = 0; j < kPfNT; ++j) { bf[j] = spread_nibbles(wv1[j]); sc[j] = half_bits(sv1[j]) * live; }
-            pf_load_b<FRAG>(wv1, sv1, we, se16, wrow, kw_row, G, min(g + 3, Gl), lane);
+            pf_load_b(wv1, sv1, wb, gstep, woff, sb, soff, min(g + 3, Gl));
             mma(bf, sc, g + 1);
             pf_store_a(a_reg, slot(g + 2), a_dst);
             lds_barrier();
@@ -417,9 +442,9 @@ int launch_grouped_prefill(const GroupedArgs& a, hipStream_t s) {
     const Params p = make_params(a);
     if (p.P == 0) return W4A8_OK;
     if (!prefill_supported(a.K, a.group_size, a.e2m1) || p.xq == nullptr || p.asum == nullptr ||
-        a.x_rows * a.K >= ((int64_t)1 << 31)) {
+        a.x_rows * a.K >= ((int64_t)1 << 31) || a.N * a.K / 2 >= ((int64_t)1 << 31)) {
         set_error("prefill grouped GEMM: needs g128 int4 weights, K <= 4096, prequantised rows "
-                  "(rows * K < 2^31) and their group sums");
+                  "(rows * K < 2^31), their group sums and expert slices below 2 GiB");
         return W4A8_ERR_INVALID;
     }
     if (a.w_frag && (a.N % 16 != 0 || (a.epi == Epi::kSiluHalf && (a.N / 2) % 16 != 0))) {

@@ -33,9 +33,14 @@ logger = logging.getLogger(__name__)
 
 #: Rows up to which the decode GEMV runs when VLLM_ROCM_W4A8_DECODE_MAX_M is unset. Measured
 #: on MI355X (HIP-graph replay) against the MFMA tiles for (N, K) = (1024, 2048), (4096, 4096),
-#: (12288, 4096), (4096, 12288): the GEMV leads through M = 128 on every shape, the tiles from
-#: M = 512 on all but the smallest; M = 256 splits.
+#: (12288, 4096), (4096, 12288): the GEMV leads through M = 128 on every shape.
 DECODE_MAX_M_DEFAULT = 128
+#: Past that (env unset) the GEMV still runs while the MFMA tile grid, ceil(N / 256) x
+#: ceil(M / 64) work-groups, holds fewer than half as many tiles as MI355X has CUs: such a grid
+#: leaves most CUs idle, and the GEMV measured faster on every shape above (e.g. (4096, 4096)
+#: at M = 256: 37.7 against 61.2 us; (1024, 2048) at M = 512: 14.3 against 38.0 us).
+DENSE_GEMV_MAX_M = 2048
+DENSE_TILE_ROWS, DENSE_TILE_COLS, DENSE_MIN_TILES = 64, 256, 128
 #: Symmetric int4 (vLLM ``uint4b8``) stores w + 8; the kernels' implicit zero point.
 UINT4B8_BIAS = 8
 
@@ -54,12 +59,17 @@ def decode_max_m() -> int:
     return int(os.environ.get("VLLM_ROCM_W4A8_DECODE_MAX_M", str(DECODE_MAX_M_DEFAULT)))
 
 
-def dense_kernel_for(M: int, K: int, group_size: int) -> str:
-    """The dense kernel name for an (M, K) batch with this group size (the ladder of
+def dense_kernel_for(M: int, N: int, K: int, group_size: int) -> str:
+    """The dense kernel name for an (M, N, K) GEMM with this group size (the ladder of
     vllm_adapter.py:296-324 without its Triton band). A K outside the GEMV's split-K table
     runs the MFMA tiles under either name (the C ABI's own fallback)."""
-    if group_size == 128 and K % group_size == 0 and M <= decode_max_m():
-        return "decode_gemv"
+    if group_size == 128 and K % group_size == 0:
+        if M <= decode_max_m():
+            return "decode_gemv"
+        tiles = -(-N // DENSE_TILE_COLS) * -(-M // DENSE_TILE_ROWS)
+        if ("VLLM_ROCM_W4A8_DECODE_MAX_M" not in os.environ and M <= DENSE_GEMV_MAX_M
+                and tiles < DENSE_MIN_TILES):
+            return "decode_gemv"
     return "prefill_wmma_ashuffle" if group_size in (32, 128) else "prefill_wmma"
 
 
@@ -84,7 +94,7 @@ def w4a8_dense_apply(x2d: torch.Tensor, w_q: torch.Tensor, w_s: torch.Tensor,
     if x2d.dtype != torch.float16:
         x2d = x2d.to(torch.float16)
     x2d = x2d.contiguous()
-    kernel = dense_kernel_for(x2d.shape[0], K, group_size)
+    kernel = dense_kernel_for(x2d.shape[0], N, K, group_size)
     return mmq_fp8_gemm(x2d, w_q, w_s, kernel=kernel, w_zeros=w_zp if use_zp else None)
 
 

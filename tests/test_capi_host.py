@@ -311,13 +311,20 @@ def test_dense_ladder_and_env(monkeypatch):
     from w4a8_fp8_wmma import linear
     monkeypatch.delenv("VLLM_ROCM_W4A8_DECODE_MAX_M", raising=False)
     d = linear.DECODE_MAX_M_DEFAULT
-    assert linear.dense_kernel_for(1, 2048, 128) == "decode_gemv"
-    assert linear.dense_kernel_for(d, 2048, 128) == "decode_gemv"
-    assert linear.dense_kernel_for(d + 1, 2048, 128) == "prefill_wmma_ashuffle"
-    assert linear.dense_kernel_for(1, 2048, 64) == "prefill_wmma"
-    assert linear.dense_kernel_for(1, 2048, 32) == "prefill_wmma_ashuffle"
+    big = 12288                       # N: 48 tile columns, so M = d + 1 fills >= 128 tiles
+    assert linear.dense_kernel_for(1, big, 2048, 128) == "decode_gemv"
+    assert linear.dense_kernel_for(d, big, 2048, 128) == "decode_gemv"
+    assert linear.dense_kernel_for(d + 1, big, 2048, 128) == "prefill_wmma_ashuffle"
+    assert linear.dense_kernel_for(1, big, 2048, 64) == "prefill_wmma"
+    assert linear.dense_kernel_for(1, big, 2048, 32) == "prefill_wmma_ashuffle"
+    # an under-filled tile grid stays on the GEMV: ceil(4096/256) * ceil(M/64) < 128
+    assert linear.dense_kernel_for(256, 4096, 4096, 128) == "decode_gemv"       # 64 tiles
+    assert linear.dense_kernel_for(512, 4096, 4096, 128) == "prefill_wmma_ashuffle"   # 128
+    assert linear.dense_kernel_for(512, 1024, 2048, 128) == "decode_gemv"       # 32 tiles
+    assert linear.dense_kernel_for(4096, 256, 2048, 128) == "prefill_wmma_ashuffle"   # M cap
     monkeypatch.setenv("VLLM_ROCM_W4A8_DECODE_MAX_M", "2")
-    assert linear.dense_kernel_for(3, 2048, 128) == "prefill_wmma_ashuffle"
+    assert linear.dense_kernel_for(3, big, 2048, 128) == "prefill_wmma_ashuffle"
+    assert linear.dense_kernel_for(3, 256, 2048, 128) == "prefill_wmma_ashuffle"  # env is strict
     for name in ("decode_gemv", "prefill_wmma_ashuffle", "prefill_wmma"):
         assert name in W._DENSE_KERNELS
 

@@ -51,7 +51,7 @@ def test_dense_apply_vs_oracle(M, asym):
     assert torch.equal(out, out16)
 
 
-@pytest.mark.parametrize("M", [1, 8, 16])
+@pytest.mark.parametrize("M", [1, 8, 16, 300, 1000])
 def test_dense_gemv_equals_tiles(M):
     """Both sides of the ladder compute the same arithmetic: the decode GEMV and the MFMA tiles
     agree to within one fp16 rounding of each other (different fp32 summation order)."""
