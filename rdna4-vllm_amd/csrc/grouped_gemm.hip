@@ -206,17 +206,17 @@ __global__ void __launch_bounds__(256) grouped_mfma_kernel(Params p) {
         b_n[i] = n < 0 ? 0 : n;   // edge columns read row 0; they are never stored
     }
 
-    uint4 a_reg[C::A_CHUNKS];
-    uint4 b_reg[C::B_CHUNKS];
+    u32x4 a_reg[C::A_CHUNKS];
+    u32x4 b_reg[C::B_CHUNKS];
     int b_tab[C::B_CHUNKS];
     auto load_group = [&](int g) {
 #pragma unroll
         for (int i = 0; i < C::A_CHUNKS; ++i)
-            a_reg[i] = *reinterpret_cast<const uint4*>(a_ptr[i] + g * kGroup);
+            a_reg[i] = *reinterpret_cast<const u32x4*>(a_ptr[i] + g * kGroup);
 #pragma unroll
         for (int i = 0; i < C::B_CHUNKS; ++i) {
             const int n = b_n[i];
-            b_reg[i] = *reinterpret_cast<const uint4*>(
+            b_reg[i] = *reinterpret_cast<const u32x4*>(
                 we + (int64_t)n * kw_row + g * (kGroup / 8) + ((tid + i * 256) & 3) * 4);
             if constexpr (!FP4) b_tab[i] = table_index(ze, n, g, p.G, p.e2m1);
         }
@@ -228,16 +228,17 @@ __global__ void __launch_bounds__(256) grouped_mfma_kernel(Params p) {
         for (int i = 0; i < C::A_CHUNKS; ++i) {
             const int c = tid + i * 256;
             if (a_row[i] >= 0)
-                *reinterpret_cast<uint4*>(A + a_row[i] * kLdsStride + (c & 7) * 16) = a_reg[i];
+                *reinterpret_cast<u32x4*>(A + a_row[i] * kLdsStride + (c & 7) * 16) = a_reg[i];
         }
 #pragma unroll
         for (int i = 0; i < C::B_CHUNKS; ++i) {
             const int c = tid + i * 256;
             uint8_t* dst = B + b_row[i] * kLdsStride + (c & 3) * 32;
             if constexpr (FP4) {
-                *reinterpret_cast<uint4*>(dst) = b_reg[i];   // 32 codes, first half of the slot
+                *reinterpret_cast<u32x4*>(dst) = b_reg[i];   // 32 codes, first half of the slot
             } else {
-                const v8i d = decode_frag(b_reg[i], load_table(b_tab[i]));
+                const u32x4 w = b_reg[i];
+                const v8i d = decode_frag(make_uint4(w.x, w.y, w.z, w.w), load_table(b_tab[i]));
                 *reinterpret_cast<uint4*>(dst) = make_uint4(d[0], d[1], d[2], d[3]);
                 *reinterpret_cast<uint4*>(dst + 16) = make_uint4(d[4], d[5], d[6], d[7]);
             }

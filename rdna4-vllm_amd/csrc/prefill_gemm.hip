@@ -65,9 +65,6 @@ __device__ __forceinline__ uint32_t pf_opaque(uint32_t v) {
     asm volatile("" : "+v"(v));
     return v;
 }
-// A staging pieces as native 4 x u32 vectors (an array of the uint4 wrapper struct was kept
-// in scratch, each piece stored there as soon as its load returned)
-using u32x4 = uint32_t __attribute__((ext_vector_type(4)));
 template <int A_CHUNKS>
 __device__ __forceinline__ void pf_load_a(u32x4 (&reg)[A_CHUNKS], const uint8_t* __restrict__ xq,
                                           const uint32_t (&src)[A_CHUNKS], int gg) {

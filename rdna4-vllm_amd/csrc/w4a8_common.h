@@ -32,6 +32,10 @@ constexpr int kE2m1Table = 16;
 
 using v8i = int __attribute__((ext_vector_type(8)));
 using v4i = int __attribute__((ext_vector_type(4)));
+// 16-byte register staging of a load on its way to LDS. Arrays of the uint4 wrapper struct
+// were kept in scratch (each piece stored there as soon as its load returned); arrays of
+// this native vector stay in registers.
+using u32x4 = uint32_t __attribute__((ext_vector_type(4)));
 
 // 16-byte streaming load (slc/nt): weights are read once per launch, so keep them from
 // displacing reused data in the caches.
