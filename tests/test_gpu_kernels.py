@@ -191,6 +191,9 @@ GEMM_CASES = [
     (16, 16, 256, 256, 4, 16, 32),
     (64, 8, 128, 256, 2, 16, 32),
     (40, 8, 256, 2048, 8, 128, 128),
+    # K % 512 != 0 keeps these on the streamed-K tiles: 128-row (block_m 128) and 64-row tiles
+    (96, 8, 256, 768, 2, 128, 128),
+    (200, 4, 384, 1280, 4, 64, 128),
 ]
 
 
