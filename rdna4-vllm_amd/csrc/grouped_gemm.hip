@@ -538,28 +538,37 @@ __global__ void __launch_bounds__(256, 2) grouped_gemv_kernel(Params p, int tpt)
         const bool live = c < nch;
         const int t = t_begin + (c / C::NB) * C::CT;
         const int g = live ? g0 + (c % C::NB) * C::GC : g0;
+        // byte offsets: a wave-uniform part (group, step) on a scalar base plus a 32-bit lane
+        // part (the expert's slice is < 2^31 bytes); past the end every lane reads offset 0
+        constexpr uint32_t ustep = FRAG ? 1024u : kGroup / 2;
+        const uint8_t* wg = reinterpret_cast<const uint8_t*>(we) + (uint32_t)g * ustep;
 #pragma unroll
         for (int f = 0; f < C::FR; ++f) {
             const int n = live ? row_of(t, f) : 0;
-            // op layout: row n, words 16 (g + u) + 4 q; fragment layout: block (n / 16, g + u)
-            const int32_t* wr =
-                FRAG ? we + (live ? ((int64_t)(n >> 4) * p.G + g) * 256 + lane * 4 : 0)
-                     : we + (live ? (int64_t)n * kw_row + g * (kGroup / 8) + q * 4 : 0);
-            constexpr int ustep = FRAG ? 256 : kGroup / 8;
+            // op layout: row n, bytes 64 (g + u) + 16 q; fragment layout: block (n / 16, g + u)
+            const uint32_t woff =
+                !live ? 0u
+                : FRAG ? (uint32_t)(n >> 4) * (uint32_t)p.G * 1024u + (uint32_t)lane * 16u
+                       : (uint32_t)n * (uint32_t)(p.K / 2) + (uint32_t)q * 16u;
             // fragment layout: whole 128-byte lines per instruction, streamed (non-temporal,
             // read once per launch); op layout: 64-byte row pieces whose second half the
             // next instruction reads, so they stay cached
 #pragma unroll
-            for (int u = 0; u < C::GC; ++u)
-                wv[b][u * C::FR + f] =
-                    FRAG ? load_stream16(wr + (live ? u * ustep : 0))
-                         : *reinterpret_cast<const uint4*>(wr + (live ? u * ustep : 0));
+            for (int u = 0; u < C::GC; ++u) {
+                const uint8_t* ptr = wg + (live ? u * ustep : 0u) + opaque_u32(woff);
+                wv[b][u * C::FR + f] = FRAG ? load_stream16(ptr) : *reinterpret_cast<const uint4*>(ptr);
+            }
             if constexpr (!C::kStagedSZ) {
-                load_scales<C::GC>(se + (int64_t)n * p.G + g, sw[b][f]);
+                load_scales<C::GC>(reinterpret_cast<const __half*>(
+                                       reinterpret_cast<const uint8_t*>(se) + (uint32_t)g * 2u +
+                                       opaque_u32((uint32_t)n * (uint32_t)p.G * 2u)),
+                                   sw[b][f]);
                 // symmetric weights load (and ignore) scale words instead: same load count
-                load_zero_words<C::GC>(ze ? ze + (int64_t)(n >> 3) * p.G + g
-                                          : reinterpret_cast<const int32_t*>(p.scales),
-                                       zw[b][f]);
+                load_zero_words<C::GC>(
+                    ze ? reinterpret_cast<const int32_t*>(reinterpret_cast<const uint8_t*>(ze) + (uint32_t)g * 4u +
+                                                         opaque_u32((uint32_t)(n >> 3) * (uint32_t)p.G * 4u))
+                       : reinterpret_cast<const int32_t*>(p.scales),
+                    zw[b][f]);
             }
         }
     };

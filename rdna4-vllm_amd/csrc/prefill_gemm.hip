@@ -56,21 +56,15 @@ __device__ __forceinline__ bool prefill_item(int nblocks, int ntiles, int& m_blo
     return true;
 }
 
-// Loads take a wave-uniform base plus a 32-bit per-lane byte offset, so they issue in the
-// scalar-base form (one offset register per load, no 64-bit address arithmetic per lane).
-// The offset passes through an opaque copy: otherwise loop strength reduction turns each
-// address into a 64-bit per-lane induction variable (two registers per load stream), which
-// pushed the 64- and 128-row tiles into scratch.
-__device__ __forceinline__ uint32_t pf_opaque(uint32_t v) {
-    asm volatile("" : "+v"(v));
-    return v;
-}
+// Loads take a wave-uniform base plus a 32-bit per-lane byte offset (opaque_u32), so they
+// issue in the scalar-base form (one offset register per load, no 64-bit address arithmetic
+// per lane).
 template <int A_CHUNKS>
 __device__ __forceinline__ void pf_load_a(u32x4 (&reg)[A_CHUNKS], const uint8_t* __restrict__ xq,
                                           const uint32_t (&src)[A_CHUNKS], int gg) {
     const uint8_t* base = xq + (uint32_t)gg * kGroup;
 #pragma unroll
-    for (int i = 0; i < A_CHUNKS; ++i) reg[i] = *reinterpret_cast<const u32x4*>(base + pf_opaque(src[i]));
+    for (int i = 0; i < A_CHUNKS; ++i) reg[i] = *reinterpret_cast<const u32x4*>(base + opaque_u32(src[i]));
 }
 template <int A_CHUNKS>
 __device__ __forceinline__ void pf_store_a(const u32x4 (&reg)[A_CHUNKS], uint8_t* dst,
@@ -90,8 +84,8 @@ __device__ __forceinline__ void pf_load_b(uint4 (&w)[kPfNT], uint32_t (&sc)[kPfN
     const uint8_t* sg = sb + (uint32_t)gg * 2u;
 #pragma unroll
     for (int j = 0; j < kPfNT; ++j) {
-        w[j] = *reinterpret_cast<const uint4*>(wg + pf_opaque(woff[j]));
-        sc[j] = *reinterpret_cast<const uint16_t*>(sg + pf_opaque(soff[j]));
+        w[j] = *reinterpret_cast<const uint4*>(wg + opaque_u32(woff[j]));
+        sc[j] = *reinterpret_cast<const uint16_t*>(sg + opaque_u32(soff[j]));
     }
 }
 

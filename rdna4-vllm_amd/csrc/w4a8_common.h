@@ -37,6 +37,14 @@ using v4i = int __attribute__((ext_vector_type(4)));
 // this native vector stay in registers.
 using u32x4 = uint32_t __attribute__((ext_vector_type(4)));
 
+// An opaque copy of a per-lane 32-bit value. Loads at a wave-uniform base plus such an
+// offset issue in the scalar-base form; without the copy, loop strength reduction and
+// hoisting turn the addresses into 64-bit per-lane values held (and spilled) across loops.
+__device__ __forceinline__ uint32_t opaque_u32(uint32_t v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
 // 16-byte streaming load (slc/nt): weights are read once per launch, so keep them from
 // displacing reused data in the caches.
 __device__ __forceinline__ uint4 load_stream16(const void* p) {
