@@ -51,6 +51,20 @@ def test_dense_apply_vs_oracle(M, asym):
     assert torch.equal(out, out16)
 
 
+@pytest.mark.parametrize("M", [1, 40])
+def test_dense_long_k_vs_oracle(M):
+    """K = 6144 (48 groups): past the GEMV and streamed-K tables, so both names run the
+    general MFMA tiles."""
+    r = np.random.default_rng(7050 + M)
+    N, K, g = 384, 6144, 128
+    nib, zp, sc = make_weights(r, N, K, g, True)
+    w, z = O.pack_nibbles(nib), O.pack_zeros(zp)
+    x = torch.randn(M, K, generator=torch.Generator().manual_seed(M)).to(torch.float16)
+    out = linear.w4a8_dense_apply(x.to(DEV), torch.from_numpy(w).to(DEV), torch.from_numpy(sc).to(DEV),
+                                  torch.from_numpy(z).to(DEV), None, None, None, N, K, g, True, 0, 0)
+    assert maxrel(out.cpu().numpy(), O.dense_gemm(x.numpy(), w, sc, z)) <= REL_TOL
+
+
 @pytest.mark.parametrize("M", [1, 8, 16, 300, 1000])
 def test_dense_gemv_equals_tiles(M):
     """Both sides of the ladder compute the same arithmetic: the decode GEMV and the MFMA tiles

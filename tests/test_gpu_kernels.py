@@ -194,6 +194,8 @@ GEMM_CASES = [
     # K % 512 != 0 keeps these on the streamed-K tiles: 128-row (block_m 128) and 64-row tiles
     (96, 8, 256, 768, 2, 128, 128),
     (200, 4, 384, 1280, 4, 64, 128),
+    # K / 128 = 36 is past both streamed-K tables: the general tiles (and gemv falls back)
+    (24, 4, 256, 4608, 2, 64, 128),
 ]
 
 
