@@ -5,8 +5,9 @@
 (vllm_adapter.py:265-354): 2-D activations of any float dtype are cast to fp16, the result
 is (M, N) fp16. The kernel for a batch of M rows is picked by name:
 
-  * ``"decode_gemv"`` for M <= ``VLLM_ROCM_W4A8_DECODE_MAX_M`` at group 128 (a K outside the
-    GEMV's split-K table runs the MFMA tiles instead);
+  * ``"decode_gemv"`` for M <= ``VLLM_ROCM_W4A8_DECODE_MAX_M`` at group 128, and (with the
+    variable unset) up to 2048 rows while the MFMA tile grid would hold fewer than 128
+    tiles (a K outside the GEMV's split-K table runs the MFMA tiles instead);
   * ``"prefill_wmma_ashuffle"`` otherwise (``"prefill_wmma"`` for group sizes other than 32 and
     128, the reference's rule). On gfx950 both names run the fp8-MFMA tiles.
 
