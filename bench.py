@@ -224,6 +224,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--tokens", type=int, default=0,
+                    help="override the config's token count (shape studies, not a headline line)")
     ap.add_argument("--layout", choices=["fragments", "op"], default="fragments",
                     help="weights as stored after loading: the gfx950 fragment layout "
                          "(repacked once per weight set, outside the timed region) or the "
@@ -240,6 +242,8 @@ def main():
     from w4a8_fp8_wmma import _lib
 
     cfg = dict(CONFIGS[args.config])
+    if args.tokens > 0:
+        cfg["T"] = args.tokens
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     cfgno = int(args.config[1:])
@@ -410,7 +414,8 @@ def main():
         "dtype": "fp8e4m3 x int4 (fp32 accumulate)",
         "data": "synthetic (seeded; random int4 weights/zero-points, fp16 scales, bf16 N(0,1) "
                 "hidden, router logits)",
-        "config": {"workload": f"{args.config}: MoE layer T={T} H={H} E={E} top{k} I={I} "
+        "config": {"workload": f"{args.config}{' (tokens override)' if args.tokens > 0 else ''}: "
+                               f"MoE layer T={T} H={H} E={E} top{k} I={I} "
                                f"AWQ-int4 g{g} zp, {cfg['routing']} routing",
                    "T": T, "H": H, "E": E, "top_k": k, "I": I, "group": g,
                    "routing": cfg["routing"], "weight_sets_rotated": R,

@@ -211,11 +211,14 @@ struct DecCfg {
     static constexpr int NF = kSilu ? 2 : 1;      // fragments per column tile (gate, up)
     static constexpr int CT = kSilu ? 1 : 2;      // column tiles per unit
     static constexpr int FR = NF * CT;            // fragments per unit and group
-    static constexpr int GC = GPW < 4 ? GPW : 4;  // groups per chunk
+    // groups per chunk: eight groups a wave (K = 4096) take 2-group chunks, so the ring of
+    // four chunks holds one unit and its registers leave room for the 128 of fp16 rows a
+    // pass start holds (4-group chunks spilled ring slots, each spill waiting for its load)
+    static constexpr int GC = GPW < 4 ? GPW : (GPW == 8 ? 2 : 4);
     static constexpr int NB = GPW / GC;           // chunks per unit
     static constexpr int TEAMS = 4 / KSPLIT;      // teams per work-group
     static_assert(KSPLIT == 1 || KSPLIT == 4, "a team is one wave or the whole work-group");
-    static_assert(GPW % GC == 0 && (NB == 1 || NB == 2), "unsupported groups per wave");
+    static_assert(GPW % GC == 0 && (NB == 1 || NB == 2 || NB == 4), "unsupported groups per wave");
     // ring slots: a multiple of NB, so a slot's group batch is fixed
     static constexpr int D = NB == 1 ? kDecRing : 4;
     static_assert(D % NB == 0 && D >= 3 && D <= 4, "ring of three or four slots");
