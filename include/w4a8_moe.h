@@ -285,6 +285,23 @@ W4A8_API int w4a8_moe_forward_noalloc(const void* x, int x_dtype, int64_t T, int
  * count == 0 switches recording off. No reference counterpart (measurement aid). */
 W4A8_API int w4a8_moe_apply_set_stage_events(void* const* events, int count);
 
+/* Fused decode layer switch: on != 0 makes the decode schedule on fragment-layout weights
+ * run gemm1+SiLU and gemm2 as one persistent launch (both GEMVs on the same expert lists;
+ * gemm2 teams wait inside the kernel, with bounded waits, for the gemm1 rows they read).
+ * The default comes from W4A8_DECODE_FUSED=1 in the environment, read once. Returns the
+ * previous setting. The launch needs every work-group (one per CU) resident at once: eager
+ * calls use a cooperative launch, which the runtime refuses otherwise; under graph capture
+ * the launch is an ordinary one, and a wait that gives up makes that call's output NaN.
+ * Process-wide. No reference counterpart (the reference runs separate launches). */
+W4A8_API int w4a8_set_decode_fused(int on);
+
+/* Test hook of the fused decode layer: while on != 0 (a device-side word of the current
+ * device, so captured graphs see it between replays), its in-kernel waits wait for a flag
+ * value no work-group publishes, with a short spin limit, so they give up and the call's
+ * output is NaN; every kernel still ends normally. For failure-path tests only. No
+ * reference counterpart. */
+W4A8_API int w4a8_decode_fused_test_fault(int on);
+
 #ifdef __cplusplus
 }
 #endif

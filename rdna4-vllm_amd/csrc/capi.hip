@@ -3,8 +3,10 @@
 // whole-layer composition (moe_experts.py:493-665).
 #include <atomic>
 #include <cstdlib>
+#include <map>
 #include <mutex>
 #include <string>
+#include <tuple>
 
 #include "w4a8_common.h"
 #include "w4a8_internal.h"
@@ -126,6 +128,58 @@ int check_launch(const char* what) {
     return W4A8_OK;
 }
 
+namespace {
+std::mutex g_dev_mu;
+// (device, kind, kernel, threads, lds) -> cached value; kind 0: LDS reserved, 1: blocks
+// per CU, 2: CU count
+std::map<std::tuple<int, int, const void*, int, size_t>, int> g_dev_facts;
+int current_device() {
+    int dev = 0;
+    return hipGetDevice(&dev) == hipSuccess ? dev : 0;
+}
+}  // namespace
+
+int reserve_dyn_lds(const void* kernel, int bytes, const char* what) {
+    const auto key = std::make_tuple(current_device(), 0, kernel, 0, (size_t)bytes);
+    std::lock_guard<std::mutex> lock(g_dev_mu);
+    if (g_dev_facts.count(key)) return W4A8_OK;
+    const hipError_t e =
+        hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (e != hipSuccess) {
+        set_error(std::string(what) + ": cannot reserve dynamic LDS: " + hipGetErrorString(e));
+        return W4A8_ERR_HIP;
+    }
+    g_dev_facts[key] = 1;
+    return W4A8_OK;
+}
+
+int device_cu_count() {
+    const int dev = current_device();
+    const auto key = std::make_tuple(dev, 2, (const void*)nullptr, 0, (size_t)0);
+    std::lock_guard<std::mutex> lock(g_dev_mu);
+    auto it = g_dev_facts.find(key);
+    if (it != g_dev_facts.end()) return it->second;
+    int ncu = 0;
+    if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        ncu <= 0)
+        ncu = 256;
+    g_dev_facts[key] = ncu;
+    return ncu;
+}
+
+int blocks_per_cu(const void* kernel, int threads, size_t lds) {
+    const auto key = std::make_tuple(current_device(), 1, kernel, threads, lds);
+    std::lock_guard<std::mutex> lock(g_dev_mu);
+    auto it = g_dev_facts.find(key);
+    if (it != g_dev_facts.end()) return it->second;
+    int occ = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, threads, lds) != hipSuccess ||
+        occ < 0)
+        occ = 0;
+    g_dev_facts[key] = occ;
+    return occ;
+}
+
 }  // namespace w4a8
 
 // ---------------------------------------------------------------------------------------
@@ -137,6 +191,9 @@ constexpr int64_t kAlignSmallMax = 1024;  // numel handled by the one-work-group
 constexpr int64_t kGemvMaxM = 96;   // moe_experts.py:563 GEMV_MAX_M
 constexpr int64_t kDecodeBlockM = 16;
 constexpr int64_t kPrefillBlockM = 64;    // 64-row tiles; empty 16-row fragments are skipped
+// the activation-resident tiles address their rows in 32 bits: rows * K < 2^31, else the
+// streamed-K tiles run
+constexpr int64_t kAresMaxElems = (int64_t)1 << 31;
 
 struct ApplyPlan {
     bool decode;
@@ -176,8 +233,8 @@ void carve_apply(WS& w, const ApplyPlan& pl, int64_t T, int64_t H, int64_t inter
     // prefill: per-group sums of the quantised rows (zero-point term of the tiles)
     *gs1 = pl.decode ? nullptr : w.template take<float>((size_t)(T * ((H + 127) / 128)));
     *gs2 = pl.decode ? nullptr : w.template take<float>((size_t)(pl.P * ((inter + 127) / 128)));
-    // decode: completion flags of the fused layer's work-groups and its timeout marker
-    *dflags = pl.decode ? w.template take<uint64_t>((size_t)(kDecodeFlagSlots + 1)) : nullptr;
+    // decode: completion flags of the fused layer's work-groups and their timeout words
+    *dflags = pl.decode ? w.template take<uint64_t>((size_t)(2 * kDecodeFlagSlots)) : nullptr;
 }
 
 // Per-call value of the fused decode layer's completion flags (never 0).
@@ -187,13 +244,21 @@ uint64_t next_decode_nonce() {
     return v == 0 ? counter.fetch_add(1, std::memory_order_relaxed) : v;
 }
 
-// W4A8_DECODE_FUSED=1 runs the decode layer's two GEMVs as one launch (decode_layer_kernel).
+// The decode layer's two GEMVs as one launch (decode_layer_kernel): W4A8_DECODE_FUSED=1 in
+// the environment when the library first needs the setting, or w4a8_set_decode_fused().
 // Off by default: on MI355X it measures slower than the two launches (the in-kernel wait for
-// h through agent-coherent loads costs more than the launch boundary it removes). Read on
-// every call, so a process can switch it.
+// h through agent-coherent loads costs more than the launch boundary it removes).
+std::atomic<int> g_decode_fused{-1};   // -1: not read yet
 bool decode_fused_enabled() {
-    const char* v = std::getenv("W4A8_DECODE_FUSED");
-    return v != nullptr && v[0] == '1';
+    int v = g_decode_fused.load(std::memory_order_relaxed);
+    if (v < 0) {
+        const char* e = std::getenv("W4A8_DECODE_FUSED");
+        int want = (e != nullptr && e[0] == '1') ? 1 : 0;
+        int expected = -1;
+        g_decode_fused.compare_exchange_strong(expected, want, std::memory_order_relaxed);
+        v = g_decode_fused.load(std::memory_order_relaxed);
+    }
+    return v == 1;
 }
 
 constexpr int kStageEvents = 8;
@@ -339,6 +404,7 @@ int moe_apply_impl(const void* x, int x_dtype, int64_t T, int64_t H, int64_t int
             sync.flags = dflags;
             sync.nflags = (int)kDecodeFlagSlots;
             sync.timeout = dflags + kDecodeFlagSlots;
+            sync.ntimeout = decode_layer_grid();
             sync.nonce = next_decode_nonce();
             stamp_gemm(0);
             rc = launch_decode_layer(d, d2, dflags, sync.nonce, dflags + kDecodeFlagSlots, s);
@@ -396,7 +462,8 @@ int moe_apply_impl(const void* x, int x_dtype, int64_t T, int64_t H, int64_t int
     stamp_gemm(0);
     if (!mfma) rc = launch_grouped_scalar(g1, s);
     else if (pl.decode && !e2m1 && gemv_supported(H, group_size)) rc = launch_grouped_gemv(g1, s);
-    else if (pf1 && prefill_ares_supported(H, 2 * inter, group_size, e2m1, pl.block_m, Epi::kSiluHalf))
+    else if (pf1 && prefill_ares_supported(H, 2 * inter, group_size, e2m1, pl.block_m, Epi::kSiluHalf) &&
+             T * H < kAresMaxElems)
         rc = launch_grouped_prefill_ares(g1, s);
     else if (pf1) rc = launch_grouped_prefill(g1, s);
     else rc = launch_grouped_mfma(g1, s);
@@ -407,7 +474,8 @@ int moe_apply_impl(const void* x, int x_dtype, int64_t T, int64_t H, int64_t int
     // would repeat it for every work-group that reads the row); the activation-resident
     // prefill tiles quantise their own rows instead (a tile is the only reader of its rows)
     const bool gemv2 = pl.decode && !e2m1 && gemv_supported(inter, group_size);
-    const bool ares2 = pf2 && prefill_ares_supported(inter, H, group_size, e2m1, pl.block_m, Epi::kHalf);
+    const bool ares2 = pf2 && prefill_ares_supported(inter, H, group_size, e2m1, pl.block_m, Epi::kHalf) &&
+                       pl.P * inter < kAresMaxElems;
     const bool ares2_quant = ares2 && prefill_ares_quantises_rows(inter, Epi::kHalf);
     if (!ares2_quant && (rc = launch_act_quant(h, false, pl.P, inter, hq, s2, k8, s, sti, ntp,
                                                numel, pf2 ? gs2 : nullptr)))
@@ -801,6 +869,18 @@ int w4a8_moe_forward_noalloc(const void* x, int x_dtype, int64_t T, int64_t H, i
                             renormalize, w13, w13_scales_f16, w13_zeros, w2, w2_scales_f16,
                             w2_zeros, weights_layout, expert_map, num_global_experts,
                             topk_weights, topk_ids, out, ws, w4a8::kNoAllocScratchBytes, stream);
+}
+
+int w4a8_set_decode_fused(int on) {
+    clear_error();
+    const int prev = decode_fused_enabled() ? 1 : 0;
+    g_decode_fused.store(on != 0 ? 1 : 0, std::memory_order_relaxed);
+    return prev;
+}
+
+int w4a8_decode_fused_test_fault(int on) {
+    clear_error();
+    return decode_fused_set_fault(on);
 }
 
 int w4a8_moe_fragments_supported(int64_t H, int64_t inter, int64_t group_size) {

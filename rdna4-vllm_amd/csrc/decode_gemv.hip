@@ -278,9 +278,20 @@ struct DecDep {
     uint64_t nonce;           // this call's value (never 0; the slot reduce resets flags to 0)
     int upe1;                 // column units per expert of the first GEMM
     int teams1;               // teams per work-group of the first GEMM
-    uint64_t* timeout;        // set to nonce when a wait gave up (bounded spin; not expected)
+    // one word per work-group: cleared by the work-group at its start, set to nonce when one
+    // of its waits gave up (bounded spin; not expected); the slot reduce reads them all
+    uint64_t* timeout;
+    uint64_t expect;          // the flag value a wait waits for (nonce; see g_dec_fault)
+    int spin_limit;           // polls before a wait gives up
 };
 constexpr int kDecSpinLimit = 1 << 20;   // polls before a wait gives up (~1 s)
+constexpr int kDecFaultSpinLimit = 64;
+
+// Test hook (w4a8_decode_fused_test_fault): while non-zero, the fused layer's waits wait for a
+// flag value no work-group publishes, with a short spin limit, so they give up and every
+// kernel still ends normally. Read from device memory at each launch, so a captured graph
+// sees changes between replays.
+__device__ uint32_t g_dec_fault = 0;
 
 // Last team of a GEMM partition (n teams over W cost units, team t starting at
 // floor(W t / n)) whose start is at or before cost S: the team that runs the unit starting at S.
@@ -453,12 +464,12 @@ __device__ __forceinline__ void dec_run(const DecodeParams& p, const DecodeLists
         for (int w0 = w_lo; w0 <= w_hi; w0 += 64) {
             const int w = w0 + lane;
             bool ok = w > w_hi;
-            for (int spin = 0; spin < kDecSpinLimit; ++spin) {
-                if (!ok) ok = dec_flag(dep.flags, w) == dep.nonce;
+            for (int spin = 0; spin < dep.spin_limit; ++spin) {
+                if (!ok) ok = dec_flag(dep.flags, w) == dep.expect;
                 if (__ballot(!ok) == 0) break;
                 __builtin_amdgcn_s_sleep(2);
             }
-            if (__ballot(!ok) != 0 && lane == 0) *dep.timeout = dep.nonce;
+            if (__ballot(!ok) != 0 && lane == 0) dep.timeout[blockIdx.x] = dep.nonce;
         }
     };
     // quantise the pass's rows, bit-identical to act_quant_kernel: absmax on the magnitude
@@ -673,8 +684,12 @@ __device__ __forceinline__ void dec_run(const DecodeParams& p, const DecodeLists
         __builtin_amdgcn_sched_barrier(0);
     }
     if constexpr (DEP) {
-        if (w_hi - w_lo >= 64 || __ballot(lane <= w_hi - w_lo && fl0 != dep.nonce) != 0)
+        if (w_hi - w_lo >= 64 || __ballot(lane <= w_hi - w_lo && fl0 != dep.expect) != 0)
             wait_rows(w_lo, w_hi);
+        // the row loads below must not be moved above the flag reads that allowed them (an
+        // acquire at work-group scope orders them in the compiler; the loads themselves are
+        // agent-coherent)
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
         load_rows(cc);
     }
     quantize(cc);
@@ -737,6 +752,9 @@ __global__ void __launch_bounds__(kDecThreads, 1) decode_layer_kernel(DecodePara
     __shared__ float s_amax[4][16];
     extern __shared__ __attribute__((aligned(16))) uint8_t s_dyn[];
     __shared__ int32_t s_ids[kDecMaxSlots];
+    // this work-group's timeout word: the previous call's slot reduce has read it
+    if (threadIdx.x == 0) dep.timeout[blockIdx.x] = 0;
+    const uint32_t fault = g_dec_fault;
     const uint32_t warm = dec_warm(p1);
     const int32_t* ids = p1.ids;
     if (p1.logits != nullptr) {
@@ -744,6 +762,10 @@ __global__ void __launch_bounds__(kDecThreads, 1) decode_layer_kernel(DecodePara
         ids = s_ids;
     }
     build_lists(p1, ids, L);
+    if (fault != 0) {
+        dep.expect = (dep.nonce ^ 0x8000000000000000ull) | 1ull;   // never published, never 0
+        dep.spin_limit = kDecFaultSpinLimit;
+    }
     dec_run<Epi::kSiluHalf, GPW1, KS1, ABF16, false>(p1, L, s_amax, reinterpret_cast<v4f*>(s_dyn), dep);
     // every wave's h stores complete (vmcnt(0)), then one release at agent scope publishes them
     __builtin_amdgcn_s_waitcnt(0x0F70);
@@ -773,32 +795,17 @@ DecSplit dec_split(int G) {
     }
 }
 
-int persistent_grid() {
-    int dev = 0, ncu = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        ncu <= 0)
-        ncu = 256;
-    return ncu;   // one four-wave work-group per CU (one wave per SIMD, up to 512 registers)
-}
+// one four-wave work-group per CU (one wave per SIMD, up to 512 registers)
+int persistent_grid() { return device_cu_count(); }
 
 template <Epi EPI, int GPW, int KSPLIT, bool ABF16>
 int launch_dec_a(const DecodeParams& p, hipStream_t s) {
     using C = DecCfg<EPI, GPW, KSPLIT>;
     const size_t lds = C::LDS_BYTES;
-    static bool attr_set = false;
-    if (!attr_set) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&decode_gemv_kernel<EPI, GPW, KSPLIT, ABF16>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
-            set_error("decode_gemv_kernel: cannot reserve dynamic LDS");
-            return W4A8_ERR_HIP;
-        }
-        attr_set = true;
-    }
-    static int grid = 0;
-    if (grid == 0) grid = persistent_grid();
-    launch_kernel(&decode_gemv_kernel<EPI, GPW, KSPLIT, ABF16>, dim3(grid), dim3(kDecThreads), lds,
-                  s, p);
+    auto* kern = &decode_gemv_kernel<EPI, GPW, KSPLIT, ABF16>;
+    if (int rc = reserve_dyn_lds(reinterpret_cast<const void*>(kern), (int)lds, "decode_gemv_kernel"))
+        return rc;
+    launch_kernel(kern, dim3(persistent_grid()), dim3(kDecThreads), lds, s, p);
     return check_launch("decode_gemv_kernel");
 }
 
@@ -835,18 +842,35 @@ int launch_layer_a(const DecodeParams& p1, const DecodeParams& p2, const DecDep&
     constexpr size_t l2 = DecCfg<Epi::kSlotF32, GPW2, KS2>::LDS_BYTES;
     constexpr size_t lds = l1 > l2 ? l1 : l2;
     auto* kern = &decode_layer_kernel<GPW1, KS1, GPW2, KS2, ABF16>;
-    static bool attr_set = false;
-    if (!attr_set) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
-            set_error("decode_layer_kernel: cannot reserve dynamic LDS");
+    const void* fn = reinterpret_cast<const void*>(kern);
+    if (int rc = reserve_dyn_lds(fn, (int)lds, "decode_layer_kernel")) return rc;
+    // gemm2 teams wait for other work-groups' flags: the whole grid (one work-group per CU)
+    // must be resident at once
+    if (blocks_per_cu(fn, kDecThreads, lds) < 1) {
+        set_error("decode_layer_kernel: a work-group does not fit on one CU");
+        return W4A8_ERR_INVALID;
+    }
+    const dim3 grid(persistent_grid());
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cap) != hipSuccess) cap = hipStreamCaptureStatusActive;
+    if (cap == hipStreamCaptureStatusNone && next_kernel_stamp().start == nullptr) {
+        // eager: a cooperative launch, which the runtime refuses unless the grid can be
+        // resident all at once (a graph capture takes the ordinary launch below; the bounded
+        // waits and the NaN output of a wait that gave up cover that case)
+        DecodeParams a1 = p1, a2 = p2;
+        DecDep a3 = dep;
+        void* args[] = {&a1, &a2, &a3};
+        const hipError_t e = hipLaunchCooperativeKernel(fn, grid, dim3(kDecThreads), args,
+                                                        (unsigned)lds, s);
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            set_error(std::string("decode_layer_kernel: cooperative launch refused: ") +
+                      hipGetErrorString(e));
             return W4A8_ERR_HIP;
         }
-        attr_set = true;
+        return W4A8_OK;
     }
-    static int grid = 0;
-    if (grid == 0) grid = persistent_grid();
-    launch_kernel(kern, dim3(grid), dim3(kDecThreads), lds, s, p1, p2, dep);
+    launch_kernel(kern, grid, dim3(kDecThreads), lds, s, p1, p2, dep);
     return check_launch("decode_layer_kernel");
 }
 
@@ -907,6 +931,19 @@ bool decode_layer_fused_supported(int64_t H, int64_t inter) {
     return dec_fused_shape((int)(H / kGroup), (int)(inter / kGroup));
 }
 
+int decode_layer_grid() { return persistent_grid(); }
+
+int decode_fused_set_fault(int on) {
+    const uint32_t v = on != 0 ? 1u : 0u;
+    const hipError_t e = hipMemcpyToSymbol(HIP_SYMBOL(g_dec_fault), &v, sizeof(v), 0,
+                                           hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        set_error(std::string("decode fused test hook: ") + hipGetErrorString(e));
+        return W4A8_ERR_HIP;
+    }
+    return W4A8_OK;
+}
+
 int launch_decode_layer(const DecodeLaunch& d1, const DecodeLaunch& d2, uint64_t* flags,
                         uint64_t nonce, uint64_t* timeout, hipStream_t s) {
     if (d1.numel == 0) return W4A8_OK;
@@ -921,6 +958,8 @@ int launch_decode_layer(const DecodeLaunch& d1, const DecodeLaunch& d2, uint64_t
     dep.upe1 = (int)(d1.N / 2 / 16);                 // gemm1: 16 gate + 16 up columns a unit
     dep.teams1 = dec_split(p1.G).ksplit > 1 ? 1 : 4;
     dep.timeout = timeout;
+    dep.expect = nonce;
+    dep.spin_limit = kDecSpinLimit;
     return launch_layer_e(p1, p2, dep, s);
 }
 

@@ -96,8 +96,16 @@ __global__ void slot_reduce_kernel(const float* __restrict__ y, const float* __r
     const int n = (blockIdx.x * blockDim.x + threadIdx.x) * 4;
     // after the fused decode layer: its completion flags go back to 0 for the next call, and
     // a wait of this call that gave up (never expected) turns the whole output into NaN
-    // instead of leaving rows that may have read unpublished h
-    const bool failed = sync.timeout != nullptr && *sync.timeout == sync.nonce;
+    // instead of leaving rows that may have read unpublished h. Every work-group of that
+    // launch has its own timeout word, which it clears itself when it starts, so a wait that
+    // gave up in one call (or one graph replay) does not mark the next.
+    bool failed = false;
+    if (sync.timeout != nullptr) {   // uniform over the grid: every thread reaches the barrier
+        bool mine = false;
+        for (int i = threadIdx.x; i < sync.ntimeout; i += blockDim.x)
+            mine = mine || sync.timeout[i] == sync.nonce;
+        failed = __syncthreads_or(mine) != 0;
+    }
     if (sync.flags != nullptr && blockIdx.x == 0 && blockIdx.y == 0)
         for (int i = threadIdx.x; i < sync.nflags; i += blockDim.x) sync.flags[i] = 0;
     if (n >= N || t >= T) return;

@@ -846,16 +846,10 @@ int launch_scalar_t(const Params& p, hipStream_t s) {
 template <Epi EPI, int BM, int BN, bool FP4>
 int launch_mfma_t(const Params& p, hipStream_t s) {
     using C = TileCfg<EPI, BM, BN>;
-    static bool attr_set = false;   // > 64 KB dynamic LDS needs an explicit opt-in
-    if (!attr_set) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&grouped_mfma_kernel<EPI, BM, BN, FP4>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize,
-                                C::LDS_BYTES) != hipSuccess) {
-            set_error("grouped_mfma_kernel: cannot reserve dynamic LDS");
-            return W4A8_ERR_HIP;
-        }
-        attr_set = true;
-    }
+    // > 64 KB dynamic LDS needs an explicit opt-in
+    if (int rc = reserve_dyn_lds(reinterpret_cast<const void*>(&grouped_mfma_kernel<EPI, BM, BN, FP4>),
+                                 C::LDS_BYTES, "grouped_mfma_kernel"))
+        return rc;
     const int ncols = EPI == Epi::kSiluHalf ? p.N / 2 : p.N;
     dim3 grid((unsigned)((ncols + BN - 1) / BN), (unsigned)((p.P + BM - 1) / BM));
     grouped_mfma_kernel<EPI, BM, BN, FP4><<<grid, 256, C::LDS_BYTES, s>>>(p);
@@ -919,16 +913,10 @@ int gemv_default_tpt(const Params& p, int ntiles, int frag_bytes_per_tile_wave, 
 template <Epi EPI, int GPW, int KSPLIT, bool AQ, bool FRAG>
 int launch_gemv_a(const Params& p, int tpt, dim3 grid, size_t lds, hipStream_t s) {
     using C = GemvCfg<EPI, GPW, KSPLIT>;
-    static bool attr_set = false;
-    if (!attr_set) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&grouped_gemv_kernel<EPI, GPW, KSPLIT, AQ, FRAG>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize,
-                                4 * kGemvMaxTiles * C::NF * 64 * (int)sizeof(v4f)) != hipSuccess) {
-            set_error("grouped_gemv_kernel: cannot reserve dynamic LDS");
-            return W4A8_ERR_HIP;
-        }
-        attr_set = true;
-    }
+    if (int rc = reserve_dyn_lds(reinterpret_cast<const void*>(&grouped_gemv_kernel<EPI, GPW, KSPLIT, AQ, FRAG>),
+                                 4 * kGemvMaxTiles * C::NF * 64 * (int)sizeof(v4f),
+                                 "grouped_gemv_kernel"))
+        return rc;
     launch_kernel(&grouped_gemv_kernel<EPI, GPW, KSPLIT, AQ, FRAG>, grid, dim3(256), lds, s, p, tpt);
     return check_launch("grouped_gemv_kernel");
 }

@@ -666,39 +666,13 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
 template <Epi EPI, bool FRAG, int BM, bool SQ>
 int launch_ares_bm(const Params& p, hipStream_t s) {
     const size_t lds = ar_lds_bytes<BM>(p.K);
-    static bool attr_set = false;
-    if (!attr_set) {   // > 64 KB of dynamic LDS needs an explicit opt-in
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_ares_kernel<EPI, FRAG, BM, SQ>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)ar_lds_bytes<BM>(ar_max_k<BM>())) != hipSuccess) {
-            set_error("prefill_ares_kernel: cannot reserve dynamic LDS");
-            return W4A8_ERR_HIP;
-        }
-        attr_set = true;
-    }
+    const void* fn = reinterpret_cast<const void*>(&prefill_ares_kernel<EPI, FRAG, BM, SQ>);
+    // > 64 KB of dynamic LDS needs an explicit opt-in
+    if (int rc = reserve_dyn_lds(fn, (int)ar_lds_bytes<BM>(ar_max_k<BM>()), "prefill_ares_kernel"))
+        return rc;
     // work-groups one XCD holds at once (the split of the last round is sized to it)
-    static int occ_lds[4] = {-1, -1, -1, -1}, occ_val[4] = {0, 0, 0, 0};
-    static int ncu = 0;
-    if (ncu == 0) {
-        int dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-            ncu <= 0)
-            ncu = 256;
-    }
-    int occ = 0;
-    for (int i = 0; i < 4 && occ == 0; ++i) {
-        if (occ_lds[i] == (int)lds) occ = occ_val[i];
-        else if (occ_lds[i] < 0) {
-            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                    &occ, reinterpret_cast<const void*>(&prefill_ares_kernel<EPI, FRAG, BM, SQ>),
-                    kArThreads, lds) != hipSuccess || occ <= 0)
-                occ = 1;
-            occ_lds[i] = (int)lds;
-            occ_val[i] = occ;
-        }
-    }
-    if (occ == 0) occ = 1;
+    const int occ = std::max(1, blocks_per_cu(fn, kArThreads, lds));
+    const int ncu = device_cu_count();
     Params q = p;
     q.xcd_slots = std::max(1, ncu * occ / kArXcds);
     // a multiple of 8 work-groups covers every tile under the XCD-aware order, plus one more

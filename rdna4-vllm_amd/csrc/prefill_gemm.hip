@@ -393,16 +393,10 @@ int launch_prefill_t(const Params& p, hipStream_t s) {
     const int nblocks = (int)((p.P + 16 * MT - 1) / (16 * MT));
     const int64_t grid = (int64_t)ntiles * nblocks;
     const PfLds L(16 * MT, (p.G + 15) / 16 * 16);
-    static bool attr_set = false;
-    if (!attr_set) {   // > 64 KB of dynamic LDS needs an explicit opt-in
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_mfma_kernel<EPI, MT, FRAG>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize,
-                                PfLds(16 * MT, kPfMaxGroups).total) != hipSuccess) {
-            set_error("prefill_mfma_kernel: cannot reserve dynamic LDS");
-            return W4A8_ERR_HIP;
-        }
-        attr_set = true;
-    }
+    // > 64 KB of dynamic LDS needs an explicit opt-in
+    if (int rc = reserve_dyn_lds(reinterpret_cast<const void*>(&prefill_mfma_kernel<EPI, MT, FRAG>),
+                                 PfLds(16 * MT, kPfMaxGroups).total, "prefill_mfma_kernel"))
+        return rc;
     launch_kernel(&prefill_mfma_kernel<EPI, MT, FRAG>, dim3((unsigned)grid), dim3(256),
                   (size_t)L.total, s, p, nblocks, ntiles);
     return check_launch("prefill_mfma_kernel");

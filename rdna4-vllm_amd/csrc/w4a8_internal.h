@@ -18,6 +18,17 @@ void clear_error();
 // Returns W4A8_ERR_HIP (with message) if the last launch failed, else W4A8_OK.
 int check_launch(const char* what);
 
+// Per-device launch facts, looked up once per (current device, kernel) under a lock, so
+// several threads and several GPUs in one process each get their own values.
+// Reserves `bytes` of dynamic LDS for `kernel` on the current device (hipFuncSetAttribute;
+// more than 64 KB needs the opt-in); W4A8_OK or W4A8_ERR_HIP with a message naming `what`.
+int reserve_dyn_lds(const void* kernel, int bytes, const char* what);
+// Compute units of the current device (256 if the query fails).
+int device_cu_count();
+// Work-groups of `threads` threads and `lds` dynamic LDS bytes one CU holds at once
+// (hipOccupancyMaxActiveBlocksPerMultiprocessor; 0 if the query fails).
+int blocks_per_cu(const void* kernel, int threads, size_t lds);
+
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 // Kernel-exact timing (measurement aid): when set, the next launch made through
@@ -103,11 +114,12 @@ int launch_gather_reduce(const void* out2, int64_t P, int64_t N, const int32_t* 
 // out[t, n] = cast(sum_{j asc} w[t*k+j] * y[(t*k+j), n]) with y fp32 (rows = T*k);
 // slots whose (mapped) expert is outside [0, E) are skipped (map as launch_align_quant).
 // sync (after the fused decode layer): flags[0..nflags) are reset to 0, and the output is
-// NaN when *timeout == nonce (an in-kernel wait of this call gave up).
+// NaN when any of timeout[0..ntimeout) == nonce (an in-kernel wait of this call gave up).
 struct SlotReduceSync {
     uint64_t* flags = nullptr;
     int nflags = 0;
     const uint64_t* timeout = nullptr;
+    int ntimeout = 0;
     uint64_t nonce = 0;
 };
 int launch_slot_reduce(const float* y, const float* tw, const int32_t* topk_ids,
@@ -213,10 +225,15 @@ bool decode_routes_in_kernel(int64_t T, int64_t n_router, int64_t top_k);
 int launch_decode_gemv(const DecodeLaunch& d, hipStream_t stream);
 // Both GEMVs in one launch (gemm2 waits in-kernel for the gemm1 rows it reads): d1 is gemm1,
 // d2 gemm2. flags: kDecodeFlagSlots words, 0 or a value other than nonce on entry (the slot
-// reduce resets them to 0); timeout: set to nonce if an in-kernel wait gave up.
+// reduce resets them to 0); timeout: kDecodeFlagSlots words, word w set to nonce if a wait
+// of work-group w gave up (each work-group clears its own word when it starts). The grid
+// is decode_layer_grid() work-groups.
 constexpr int64_t kDecodeFlagSlots = 1024;
 bool decode_layer_fused_supported(int64_t H, int64_t inter);
+int decode_layer_grid();
 int launch_decode_layer(const DecodeLaunch& d1, const DecodeLaunch& d2, uint64_t* flags,
                         uint64_t nonce, uint64_t* timeout, hipStream_t stream);
+// Test hook of the fused layer (g_dec_fault): on != 0 makes its waits give up.
+int decode_fused_set_fault(int on);
 
 }  // namespace w4a8

@@ -22,6 +22,7 @@ from ._ops import (  # noqa: F401
     moe_apply,
     moe_forward,
     repack_fragments,
+    set_decode_fused,
     silu_and_mul,
 )
 
@@ -122,5 +123,6 @@ __all__ = [
     "mmq_fp8_gemm", "mmq_fp8_moe_gemm", "mmq_fp8_moe_gemm1_silu", "mmq_fp8_moe_gemm_scatter",
     "mmq_fp8_moe_gather_reduce", "act_quant_fp8", "dequant_fp8", "fragments_supported",
     "fused_topk",
-    "moe_align_block_size", "moe_apply", "moe_forward", "repack_fragments", "silu_and_mul",
+    "moe_align_block_size", "moe_apply", "moe_forward", "repack_fragments", "set_decode_fused",
+    "silu_and_mul",
 ]

@@ -491,3 +491,15 @@ def fragments_supported(hidden: int, inter: int, group_size: int) -> bool:
     """Whether moe_apply takes fragment-layout weights of this shape for every batch size
     (what a load hook checks before it repacks)."""
     return bool(lib.w4a8_moe_fragments_supported(int(hidden), int(inter), int(group_size)))
+
+
+def set_decode_fused(on: bool) -> bool:
+    """Runs the decode layer's two GEMVs as one persistent launch (on) or two launches (off,
+    the default unless W4A8_DECODE_FUSED=1); returns the previous setting. Process-wide."""
+    return bool(lib.w4a8_set_decode_fused(1 if on else 0))
+
+
+def _decode_fused_test_fault(on: bool) -> None:
+    """Test hook: makes the fused decode layer's in-kernel waits give up (its output is then
+    NaN), on the current device, until switched off."""
+    check(lib.w4a8_decode_fused_test_fault(1 if on else 0), "decode fused test hook")

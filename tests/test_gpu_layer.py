@@ -418,3 +418,86 @@ def test_decode_six_group_intermediate(T, frag):
     if frag:
         op = W.moe_apply(x, ws["w13"], ws["w2"], ws["s13"], ws["s2"], ws["z13"], ws["z2"], tw, ids)
         assert torch.equal(out, op)
+
+
+def _same_fp32_output(ob, oh):
+    """ob (bf16) and oh (fp16) are the two roundings (RNE) of one fp32 value per element: the
+    bf16 output lies between the bf16 roundings of the ends of the fp32 interval that rounds
+    to the fp16 output (out_h +- half its spacing; rounding is monotone). NaN matches NaN."""
+    nb, nh = torch.isnan(ob), torch.isnan(oh)
+    if not torch.equal(nb, nh):
+        return False, int((nb != nh).sum())
+    hf = oh.float()
+    a = hf.abs()
+    e = torch.floor(torch.log2(torch.where(a > 0, a, torch.full_like(a, 2.0 ** -30)))).clamp(min=-14)
+    half = torch.exp2(e - 11)                               # half an fp16 ulp (2^-25 floor)
+    lo, hi = (hf - half).to(torch.bfloat16), (hf + half).to(torch.bfloat16)
+    ok = ((ob >= lo) & (ob <= hi)) | nb
+    return bool(ok.all()), int((~ok).sum())
+
+
+def _bf16_routes(cfg, ws, x, logits, frag):
+    w13, w2 = ws["w13"], ws["w2"]
+    if frag:
+        w13, w2 = W.repack_fragments(w13), W.repack_fragments(w2)
+    ob, twb, idb = W.moe_forward(x, logits, cfg["k"], w13, w2, ws["s13"], ws["s2"], ws["z13"],
+                                 ws["z2"])
+    oh, twh, idh = W.moe_forward(x.to(torch.float16), logits, cfg["k"], w13, w2, ws["s13"],
+                                 ws["s2"], ws["z13"], ws["z2"])
+    assert ob.dtype == torch.bfloat16 and oh.dtype == torch.float16
+    assert torch.equal(idb, idh) and torch.equal(twb, twh)
+    return ob, oh, twb, idb
+
+
+@pytest.mark.parametrize("T", [5, 32, 96, 97, 300])
+@pytest.mark.parametrize("frag", [False, True])
+def test_bf16_input_route_equals_fp16_cast(T, frag):
+    """a3: a bf16 layer input is cast to fp16 before it is quantised, as the reference's
+    x.to(fp16) (moe_experts.py:596). moe_forward(x_bf16) and moe_forward(x_bf16.to(fp16)) must
+    then produce bf16(v) and fp16(v) of the same fp32 layer output v (bit-exact up to the two
+    output casts). One row holds 65536 (fp16 infinity after the cast: the whole output row is
+    NaN on both routes), one the largest finite bf16 below 65504 (finite through the cast;
+    the layer then overflows fp16 in h on both routes alike). T covers the decode (<= 96) and
+    prefill schedules; the fp16-subnormal range is the next test."""
+    cfg = dict(T=T, H=512, E=16, k=4, I=256, g=128, routing="uniform")
+    ws = bench.make_weights(cfg, 8100 + T, DEV)
+    x, logits = bench.make_inputs(cfg, 8101 + T, DEV)
+    x = x.to(torch.bfloat16)
+    x[3, 17] = 65536.0                                       # fp16 overflow -> inf
+    x[4, 5] = 65280.0                                        # largest finite bf16 < 65504
+    ob, oh, _, _ = _bf16_routes(cfg, ws, x, logits, frag)
+    nb = torch.isnan(ob)
+    assert nb[3].all() and not nb[:3].any() and not nb[5:].any()
+    ok, bad = _same_fp32_output(ob, oh)
+    assert ok, bad
+
+
+@pytest.mark.parametrize("T", [6, 130])
+@pytest.mark.parametrize("frag", [False, True])
+def test_bf16_input_route_fp16_subnormals(T, frag):
+    """a3 where the cast is not the identity below fp16's normal range: rows of N(0,1) scaled
+    to 1e-6 .. 5e-5 (fp16 quantum 2^-24 below 2^-14), so bf16 -> fp16 rounds them, and act
+    scales at the 1e-8 floor. gemm1 scales x2000 keep the layer output of such rows above
+    fp16 underflow. Both routes must give the same fp32 output (as above), and the fp16 route
+    must match the oracle (x16 = fp16(x) first) on every row."""
+    cfg = dict(T=T, H=512, E=16, k=4, I=256, g=128, routing="uniform")
+    ws = bench.make_weights(cfg, 8200 + T, DEV)
+    ws["s13"] = (ws["s13"].float() * 2000).to(torch.float16)
+    x, logits = bench.make_inputs(cfg, 8201 + T, DEV)
+    mag = torch.tensor([1e-6, 4e-6, 3e-5, 5e-5], device=DEV).repeat(T)[:T]
+    x = (x.float() * mag[:, None]).to(torch.bfloat16)
+    x16 = x.to(torch.float16)
+    assert not torch.equal(x16.float(), x.float())          # the cast rounds these rows
+    ob, oh, tw, ids = _bf16_routes(cfg, ws, x, logits, frag)
+    assert not torch.isnan(ob).any()
+    ok, bad = _same_fp32_output(ob, oh)
+    assert ok, bad
+    ref = oracle_layer(cfg, ws, x, tw, ids, round_y=T > 96)
+    nz = np.abs(ref).max(axis=1) > 0
+    assert nz.sum() >= T // 2, "the rows must not underflow to zero"
+    # per row, within the layer bar of that row's own magnitude plus half the fp16 output's
+    # quantum (2^-25: these outputs sit near fp16's subnormal range)
+    got = oh.float().cpu().numpy()
+    for r in np.nonzero(nz)[0]:
+        err = float(np.abs(got[r].astype(np.float64) - ref[r]).max())
+        assert err <= REL_TOL * float(np.abs(ref[r]).max()) + 2.0 ** -25, (r, err)
