@@ -287,6 +287,7 @@ def measure(name, args, steps, warmup, cpu_budget, tokens=0, eager=False, strati
     torch.cuda.synchronize()
 
     graphs = None
+    L = 0
     if not args.no_graph:
         graphs = []
         s = torch.cuda.Stream()
@@ -296,19 +297,21 @@ def measure(name, args, steps, warmup, cpu_budget, tokens=0, eager=False, strati
                 step(r)
         torch.cuda.current_stream().wait_stream(s)
         torch.cuda.synchronize()
-        # One graph holds R consecutive layer steps (one per weight set), as a serving engine
-        # captures a model's layers back to back in one graph; a second graph holds the first
-        # K % R steps when K is not a multiple of R. Replays then carry no per-layer graph
-        # launch gap, and the timed region still runs exactly K steps.
+        # One graph holds L consecutive layer steps (the weight sets in turn, L a multiple of
+        # R near 40), as a serving engine captures a model's layers back to back in one graph
+        # (a 30B-A3B-class model has ~48 MoE layers); a second graph holds the first K % L
+        # steps when K is not a multiple of L. Replays then carry no per-layer graph launch
+        # gap, and the timed region still runs exactly K steps.
+        L = min(steps, R * max(1, round(40 / R)))
         def capture(n):
             gph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(gph):
                 for r in range(n):
                     step(r)
             return gph
-        graphs = [capture(R)]
-        if steps % R:
-            graphs.append(capture(steps % R))
+        graphs = [capture(L)]
+        if steps % L:
+            graphs.append(capture(steps % L))
         for gph in graphs:
             gph.replay()
         torch.cuda.synchronize()
@@ -322,9 +325,9 @@ def measure(name, args, steps, warmup, cpu_budget, tokens=0, eager=False, strati
     t_wall = time.perf_counter()
     hip.hipEventRecord(ev.ev[0], stream)
     if graphs is not None:
-        for _ in range(steps // R):
+        for _ in range(steps // L):
             graphs[0].replay()
-        if steps % R:
+        if steps % L:
             graphs[1].replay()
     else:
         for i in range(steps):
@@ -434,7 +437,7 @@ def measure(name, args, steps, warmup, cpu_budget, tokens=0, eager=False, strati
             roof["traffic_source"] = "profiles/roofline_traffic.json (" + tr["kernel"] + ")"
 
     res = dict(cfg=cfg, T=T, R=R, ms_per_step=ms_per_step, wall_ms=wall_ms, roof=roof,
-               graphs=graphs is not None, distinct=distinct, layer_bytes=layer_bytes,
+               graphs=graphs is not None, graph_steps=L, distinct=distinct, layer_bytes=layer_bytes,
                layer_flops=layer_flops, stage_ms=stage_ms, g1_ms=g1_ms, g2_ms=g2_ms,
                fused=fused, eager=eager_info)
     if cpu_budget > 0:
@@ -503,6 +506,7 @@ def main():
                    "group": cfg["g"], "routing": cfg["routing"],
                    "weight_sets_rotated": m["R"],
                    "timing": "hip-graph replay" if m["graphs"] else "eager",
+                   "layer_steps_per_graph": m["graph_steps"],
                    "weight_layout": args.layout,
                    "parallelism": "1 GPU"},
         "roofline": m["roof"],
