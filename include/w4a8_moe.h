@@ -163,6 +163,14 @@ W4A8_API int w4a8_mmq_fp8_moe_gather_reduce(const void* out2_f16, int64_t P, int
 W4A8_API int w4a8_silu_and_mul(const void* in_f16, int64_t rows, int64_t inter, void* out_f16,
                       void* stream);
 
+/* vLLM swigluoai_and_mul (gpt-oss) on (rows, 2*inter) fp16 with gate and up interleaved
+ * (gate = row[2c], up = row[2c + 1]) -> (rows, inter) fp16: in fp32, g = min(gate, limit),
+ * u = clamp(up, -limit, limit), out = fp16((u + 1) * g * sigmoid(alpha * g)); vLLM's defaults
+ * are alpha = 1.702, limit = 7. The activation the reference's mxfp4 (gpt-oss) hook applies
+ * between the unfused GEMMs (moe_experts.py:1416-1424 -> apply_moe_activation). */
+W4A8_API int w4a8_swigluoai_and_mul(const void* in_f16, int64_t rows, int64_t inter, float alpha,
+                                    float limit, void* out_f16, void* stream);
+
 /* ---------------------------------------------------------------------------------
  * Dense W4A8 GEMM: x (M, K) fp16, w (N, K/8), scales (N, K/g), zeros (N/8, K/g) or NULL
  * -> out (M, N) fp16. Replaces mmq_fp8_gemm (bindings.cpp:98-146 ->

@@ -49,6 +49,13 @@ PINNING = {
     "expert_weights_f64": "equals the e4m3 byte round trip E4M3_TO_F64[dequant_codes] on "
                            "random weights, sym and asym (exhaustive table test covers all "
                            "256 nibble/zero-point pairs)",
+    "swigluoai_and_mul": "float64 closed form within fp16 half-ulp; the clamp and interleave "
+                         "cases by hand; planted mistakes (halves instead of interleave, no "
+                         "clamp, +1 dropped) must fail",
+    "e8m0_to_fp16": "all 256 codes against exact powers of two (math.ldexp) and fp16's "
+                    "normal/subnormal/overflow limits",
+    "convert_mxfp4": "per-element brute force of the nibble order on random bytes; scales "
+                     "through e8m0_to_fp16",
     "repack_fragments": "per-element brute force of the layout definition on tiny shapes "
                         "(nibble of row n, k lands in lane n % 16 + 16 * ((k % 128) // 32)); "
                         "inverse restores the op layout exactly",
@@ -406,6 +413,53 @@ def silu_and_mul(gate_h, up_h) -> np.ndarray:
             ).astype(np.float16)
 
 
+SWIGLUOAI_ALPHA = np.float32(1.702)   # vLLM SwigluOAIAndMul defaults (gpt-oss)
+SWIGLUOAI_LIMIT = np.float32(7.0)
+
+
+def swigluoai_and_mul(x16, alpha=SWIGLUOAI_ALPHA, limit=SWIGLUOAI_LIMIT) -> np.ndarray:
+    """vLLM ``swigluoai_and_mul`` (third-party: vLLM 0.22.69, csrc/activation_kernels.cu
+    ``swigluoai_and_mul_kernel`` / layers/activation.py ``SwigluOAIAndMul``, not vendored in
+    the reference; called through ``apply_moe_activation`` by the reference's mxfp4 hook,
+    moe_experts.py:1416-1424): x (..., 2I) fp16 with gate and up interleaved, gate = x[2c],
+    up = x[2c + 1]; in fp32 g = min(gate, limit), u = clamp(up, -limit, limit),
+    sig = 1 / (1 + exp(-g * alpha)), out = fp16((u + 1) * (g * sig)). fp32 exp here; the
+    kernel uses expf."""
+    x = np.asarray(x16, dtype=np.float16).astype(np.float32)
+    gate, up = x[..., 0::2], x[..., 1::2]
+    lim = np.float32(limit)
+    with np.errstate(over="ignore", invalid="ignore"):
+        g = np.where(gate > lim, lim, gate).astype(np.float32)
+        u = np.where(up > lim, lim, np.where(up < -lim, -lim, up)).astype(np.float32)
+        sig = (np.float32(1.0) / (np.float32(1.0) + np.exp((-g * np.float32(alpha)).astype(np.float32)))
+               ).astype(np.float32)
+        glu = (g * sig).astype(np.float32)
+        return ((u + np.float32(1.0)) * glu).astype(np.float32).astype(np.float16)
+
+
+def e8m0_to_fp16(codes) -> np.ndarray:
+    """OCP MX E8M0 block scales (uint8, value 2^(s - 127)) -> fp16, the reference's mxfp4
+    load step (mxfp4/convert.py:68-98: torch.pow(2, s - 127) in fp32, cast to fp16):
+    exact for s - 127 in [-24, 15] (subnormal below -14), 0 below (2^-25 rounds to even),
+    +inf above 15, and +inf for the E8M0 NaN code 255 (2^128 overflows fp32)."""
+    e = np.asarray(codes, dtype=np.uint8).astype(np.int64) - 127
+    with np.errstate(over="ignore"):
+        return np.ldexp(np.float64(1.0), e).astype(np.float32).astype(np.float16)
+
+
+def convert_mxfp4(weight_packed, weight_scale):
+    """mxfp4 (compressed-tensors / gpt-oss) expert weights -> the op layout
+    (mxfp4/convert.py:100-140): weight_packed (..., N, K/2) uint8, two E2M1 codes a byte, the
+    lower K index in the low nibble; weight_scale (..., N, K/32) uint8 E8M0. Returns
+    (w_packed (..., N, K/8) int32 with code k at nibble k % 8 of word k / 8, scales fp16
+    (..., N, K/32)); the codes are not remapped."""
+    wb = np.asarray(weight_packed, dtype=np.uint8)
+    codes = np.empty(wb.shape[:-1] + (wb.shape[-1] * 2,), np.uint8)
+    codes[..., 0::2] = wb & 0xF
+    codes[..., 1::2] = wb >> 4
+    return pack_nibbles(codes), e8m0_to_fp16(weight_scale)
+
+
 def gemm_scatter(xpad16, w_packed, scales, w_zeros, sorted_ids, expert_ids, ntp,
                  topk_weights, output, top_k: int, block_m: int, e2m1: bool = False):
     """`mmq_fp8_moe_gemm_scatter` (moe_kernel.hip:1053-1056, bindings.cpp:293-353):
@@ -490,7 +544,8 @@ def _add_bias_f16(v16, bias, experts):
 
 def moe_layer(x, w13, s13, z13, w2, s2, z2, topk_weights, topk_ids,
               group_size: int = 128, round_y_fp16: bool = True, e2m1: bool = False,
-              return_stages: bool = False, w1_bias=None, w2_bias=None, expert_map=None):
+              return_stages: bool = False, w1_bias=None, w2_bias=None, expert_map=None,
+              activation: str = "silu"):
     """Whole gated MoE in token order (moe_experts.py:493-665, arithmetic per
     test_moe_experts.py:155-191 with the kernel SiLU moe_kernel.hip:555-561):
       x16 = fp16(x); a1,s1 = act_quant(x16); run1 over w13 per (t, j);
@@ -501,6 +556,8 @@ def moe_layer(x, w13, s13, z13, w2, s2, z2, topk_weights, topk_ids,
       out[t] = sum_{j ascending} w[t,j] * y[t,j] in fp32.
     With ``expert_map`` (global id -> local expert or -1) slots without a local expert add
     nothing (moe_experts.py:587-589 aligns with global_num_experts and the map).
+    ``activation`` "swigluoai" (gpt-oss) replaces silu_and_mul of the [gate | up] halves by
+    swigluoai_and_mul of interleaved gate/up columns.
     ``x`` is float32 (holding bf16 or fp16 values). Returns float32 (T, H)."""
     x16 = np.asarray(x, dtype=np.float32).astype(np.float16)
     T, H = x16.shape
@@ -517,7 +574,12 @@ def moe_layer(x, w13, s13, z13, w2, s2, z2, topk_weights, topk_ids,
     g1 = (run1 * sc1[tok][:, None]).astype(np.float32).astype(np.float16)
     if w1_bias is not None:
         g1 = _add_bias_f16(g1, w1_bias, ids.reshape(-1))
-    h = silu_and_mul(g1[:, :inter], g1[:, inter:])
+    if activation == "swigluoai":
+        h = swigluoai_and_mul(g1)
+    elif activation == "silu":
+        h = silu_and_mul(g1[:, :inter], g1[:, inter:])
+    else:
+        raise ValueError(f"unknown activation {activation!r}")
     a2, sc2 = act_quant(h)
     run2 = grouped_run(a2, ids.reshape(-1), w2, s2, z2, group_size, e2m1)
     y = (run2 * sc2[:, None]).astype(np.float32)

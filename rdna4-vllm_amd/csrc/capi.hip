@@ -739,6 +739,14 @@ int w4a8_silu_and_mul(const void* in_f16, int64_t rows, int64_t inter, void* out
     return launch_silu_and_mul(in_f16, rows, inter, out_f16, as_stream(stream));
 }
 
+int w4a8_swigluoai_and_mul(const void* in_f16, int64_t rows, int64_t inter, float alpha,
+                           float limit, void* out_f16, void* stream) {
+    clear_error();
+    W4A8_REQUIRE(rows >= 0 && inter >= 0, "swigluoai_and_mul: invalid sizes");
+    W4A8_REQUIRE(rows * inter == 0 || (in_f16 && out_f16), "swigluoai_and_mul: null pointer");
+    return launch_swigluoai_and_mul(in_f16, rows, inter, alpha, limit, out_f16, as_stream(stream));
+}
+
 int w4a8_mmq_fp8_gemm(const void* x_f16, int64_t M, int64_t K, const int32_t* w_packed,
                       const void* scales_f16, const int32_t* w_zeros, int64_t N,
                       int64_t group_size, int64_t kernel, int weight_is_e2m1, void* out_f16,

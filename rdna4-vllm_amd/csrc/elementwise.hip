@@ -56,6 +56,25 @@ __global__ void silu_and_mul_kernel(const __half* __restrict__ in, int64_t rows,
     out[i] = silu_mul_h(in[r * 2 * inter + c], in[r * 2 * inter + inter + c]);
 }
 
+// gpt-oss gated activation (vLLM's swigluoai_and_mul, the activation the reference's mxfp4
+// hook passes to apply_moe_activation, moe_experts.py:1416-1424): gate and up interleaved
+// along the row (gate = x[2c], up = x[2c + 1]); in fp32, g = min(gate, limit),
+// u = clamp(up, -limit, limit), out = fp16((u + 1) * (g * (1 / (1 + exp(-g * alpha))))).
+__global__ void swigluoai_and_mul_kernel(const __half* __restrict__ in, int64_t rows, int inter,
+                                         float alpha, float limit, __half* __restrict__ out) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= rows * inter) return;
+    const int64_t r = i / inter;
+    const int c = (int)(i % inter);
+    const __half2 gu = *reinterpret_cast<const __half2*>(in + r * 2 * inter + 2 * c);
+    const float gate = __low2float(gu), up = __high2float(gu);
+    const float g = gate > limit ? limit : gate;
+    const float u = up > limit ? limit : (up < -limit ? -limit : up);
+    const float sig = 1.0f / (1.0f + expf(as_f32(-g * alpha)));
+    const float glu = as_f32(g * sig);
+    out[i] = __float2half(as_f32((u + 1.0f) * glu));
+}
+
 __global__ void inverse_map_kernel(const int32_t* __restrict__ sorted_ids,
                                    const int32_t* __restrict__ ntp, int64_t P, int64_t m_tk,
                                    int32_t* __restrict__ slot_to_row) {
@@ -269,6 +288,15 @@ int launch_dequant(const int32_t* w, const int32_t* z, int64_t E, int64_t N, int
     dequant_kernel<<<blocks_for(n, 256), 256, 0, stream>>>(w, z, E, N, (int)K, (int)gs, e2m1,
                                                           out);
     return check_launch("dequant_kernel");
+}
+
+int launch_swigluoai_and_mul(const void* in, int64_t rows, int64_t inter, float alpha,
+                             float limit, void* out, hipStream_t stream) {
+    const int64_t n = rows * inter;
+    if (n == 0) return W4A8_OK;
+    swigluoai_and_mul_kernel<<<blocks_for(n, 256), 256, 0, stream>>>(
+        static_cast<const __half*>(in), rows, (int)inter, alpha, limit, static_cast<__half*>(out));
+    return check_launch("swigluoai_and_mul_kernel");
 }
 
 int launch_silu_and_mul(const void* in, int64_t rows, int64_t inter, void* out,

@@ -209,15 +209,21 @@ __global__ void __launch_bounds__(256) grouped_mfma_kernel(Params p) {
     u32x4 a_reg[C::A_CHUNKS];
     u32x4 b_reg[C::B_CHUNKS];
     int b_tab[C::B_CHUNKS];
+    // K step g covers k [128 g, 128 g + 128); E2M1 takes K % 128 == 32, 64 or 96 too, and the
+    // pieces of its last step past K load as zeros (zero codes against zero activations)
     auto load_group = [&](int g) {
 #pragma unroll
-        for (int i = 0; i < C::A_CHUNKS; ++i)
-            a_reg[i] = *reinterpret_cast<const u32x4*>(a_ptr[i] + g * kGroup);
+        for (int i = 0; i < C::A_CHUNKS; ++i) {
+            const bool in = !FP4 || g * kGroup + ((tid + i * 256) & 7) * 16 < p.K;
+            a_reg[i] = in ? *reinterpret_cast<const u32x4*>(a_ptr[i] + g * kGroup) : u32x4{0u, 0u, 0u, 0u};
+        }
 #pragma unroll
         for (int i = 0; i < C::B_CHUNKS; ++i) {
             const int n = b_n[i];
-            b_reg[i] = *reinterpret_cast<const u32x4*>(
-                we + (int64_t)n * kw_row + g * (kGroup / 8) + ((tid + i * 256) & 3) * 4);
+            const bool in = !FP4 || g * kGroup + ((tid + i * 256) & 3) * 32 < p.K;
+            b_reg[i] = in ? *reinterpret_cast<const u32x4*>(
+                                we + (int64_t)n * kw_row + g * (kGroup / 8) + ((tid + i * 256) & 3) * 4)
+                          : u32x4{0u, 0u, 0u, 0u};
             if constexpr (!FP4) b_tab[i] = table_index(ze, n, g, p.G, p.e2m1);
         }
     };
@@ -263,9 +269,10 @@ __global__ void __launch_bounds__(256) grouped_mfma_kernel(Params p) {
 #pragma unroll
         for (int j = 0; j < C::NTT; ++j) run[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
-    // K steps of 128; FP4 takes groups of 32, 64 or 128 (gps groups per step)
-    const int nsteps = p.K / kGroup;
-    const int gps = p.G / nsteps;
+    // K steps of 128 (FP4: the last may be partial); FP4 takes groups of 32, 64 or 128 (gps
+    // groups per full step)
+    const int nsteps = (p.K + kGroup - 1) / kGroup;
+    const int gps = FP4 ? kGroup / (p.K / p.G) : 1;
     // this lane's 32-wide K block within a step, and the group of the step it belongs to
     const int lane_grp = FP4 ? (lane >> 4) * gps / 4 : 0;
 
@@ -308,6 +315,7 @@ __global__ void __launch_bounds__(256) grouped_mfma_kernel(Params p) {
         }
         for (int sg = 0; sg < gps; ++sg) {   // gps == 1 without FP4
             const int gi = g * gps + sg;
+            if (gi >= p.G) break;               // past K in a partial last step
             float sc[C::NTT];
 #pragma unroll
             for (int j = 0; j < C::NTT; ++j) sc[j] = __half2float(se[(int64_t)t_srow[j] * p.G + gi]);
@@ -968,8 +976,9 @@ bool gemv_supported(int64_t K, int64_t group_size) {
 }
 
 bool mfma_supported(int64_t K, int64_t group_size, bool e2m1) {
-    // E2M1 runs fp4 operands with one MFMA per group of 32, 64 or 128
-    if (e2m1) return (group_size == 32 || group_size == 64 || group_size == kGroup) && K % kGroup == 0;
+    // E2M1 runs fp4 operands with one MFMA per group of 32, 64 or 128; K a multiple of the
+    // group (the last 128-wide K step may be partial: gpt-oss's 2880)
+    if (e2m1) return (group_size == 32 || group_size == 64 || group_size == kGroup) && K % group_size == 0;
     return group_size == kGroup && K % kGroup == 0;
 }
 

@@ -86,6 +86,8 @@ int launch_dequant(const int32_t* w, const int32_t* z, int64_t E, int64_t N, int
                    int64_t gs, bool e2m1, uint8_t* out, hipStream_t stream);
 int launch_silu_and_mul(const void* in, int64_t rows, int64_t inter, void* out,
                         hipStream_t stream);
+int launch_swigluoai_and_mul(const void* in, int64_t rows, int64_t inter, float alpha,
+                             float limit, void* out, hipStream_t stream);
 // x non-null: the routing wave of token t also quantises row t of x (act_quant_kernel's
 // arithmetic, k8-interleaved, group sums when gsum is non-null).
 int launch_topk_softmax(const float* logits, int64_t T, int64_t E, int64_t top_k,

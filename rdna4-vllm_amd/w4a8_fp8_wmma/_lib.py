@@ -47,6 +47,8 @@ SIGNATURES = {
                                               _c_void_p, _i64, _c_void_p, _c_void_p, _size,
                                               _c_void_p]),
     "w4a8_silu_and_mul": (_int, [_c_void_p, _i64, _i64, _c_void_p, _c_void_p]),
+    "w4a8_swigluoai_and_mul": (_int, [_c_void_p, _i64, _i64, ctypes.c_float, ctypes.c_float,
+                                      _c_void_p, _c_void_p]),
     "w4a8_mmq_fp8_gemm": (_int, [_c_void_p, _i64, _i64, _c_void_p, _c_void_p, _c_void_p, _i64,
                                  _i64, _i64, _int, _c_void_p, _c_void_p, _size, _c_void_p]),
     "w4a8_moe_apply_workspace_size": (_size, [_i64, _i64, _i64, _i64, _i64]),

@@ -345,6 +345,24 @@ def silu_and_mul(out: torch.Tensor, x: torch.Tensor) -> None:
     check(lib.w4a8_silu_and_mul(_ptr(x), R, I2 // 2, _ptr(out), _stream(x)), "silu_and_mul")
 
 
+SWIGLUOAI_ALPHA = 1.702     # vLLM SwigluOAIAndMul defaults (gpt-oss)
+SWIGLUOAI_LIMIT = 7.0
+
+
+def swigluoai_and_mul(out: torch.Tensor, x: torch.Tensor, alpha: float = SWIGLUOAI_ALPHA,
+                      limit: float = SWIGLUOAI_LIMIT) -> None:
+    """vLLM ``swigluoai_and_mul(out, x, alpha, limit)`` (gpt-oss): (R, 2I) fp16 with gate and
+    up interleaved (gate = x[:, 0::2], up = x[:, 1::2]) -> out (R, I) fp16,
+    (clamp(up, -limit, limit) + 1) * g * sigmoid(alpha * g) with g = min(gate, limit)."""
+    _check(x.is_cuda and x.dtype == torch.float16 and x.is_contiguous() and x.dim() == 2,
+           "x must be contiguous CUDA fp16 (R, 2I)")
+    R, I2 = x.shape
+    _check(out.shape == (R, I2 // 2) and out.dtype == torch.float16 and out.is_contiguous(),
+           "out must be contiguous fp16 (R, I)")
+    check(lib.w4a8_swigluoai_and_mul(_ptr(x), R, I2 // 2, float(alpha), float(limit), _ptr(out),
+                                     _stream(x)), "swigluoai_and_mul")
+
+
 def repack_fragments(w_packed: torch.Tensor) -> torch.Tensor:
     """Op-layout int4 weights (E, N, K/8) int32 -> fragment layout (E, N/16, K/128, 64, 4)
     int32: block (e, t, g) holds, in lane l's 16 bytes, row 16t + l % 16 and k in

@@ -32,6 +32,9 @@ logger = logging.getLogger(__name__)
 # inverse list, [0, 4, 1, 5, 2, 6, 3, 7], which reads column c from nibble AWQ_NIBBLE_OF[c]).
 AWQ_NIBBLE_OF = (0, 4, 1, 5, 2, 6, 3, 7)
 MOE_KERNEL_NAMES = ("scalar", "wmma", "gemv")        # moe_experts.py:72
+# gated activations between the GEMMs: SiLU (fused into gemm1 on the whole-layer path) and
+# gpt-oss's swigluoai (op by op, as the reference's mxfp4 hook runs it)
+GATED_ACTIVATIONS = ("silu", "swigluoai")
 GEMV_MAX_M = 96                                      # moe_experts.py:563
 APPLY_CHUNK = 4096                                   # moe_experts.py:533
 # Transient bytes a converter may hold per chunk of experts (unpacked nibbles are bytes).
@@ -157,6 +160,50 @@ def _wna16_moe_to_op_layout(qweight_u8, scales, qzeros_u8):
     return w, s, z
 
 
+# mxfp4 (OCP E2M1 codes + E8M0 block scales; gpt-oss through vLLM's GptOssMxfp4MoEMethod)
+MXFP4_BLOCK = 32          # one E8M0 scale per 32 weights along K (the MX block)
+
+
+def e8m0_to_fp16(scale_u8: torch.Tensor) -> torch.Tensor:
+    """E8M0 block scales (uint8, value 2^(s - 127)) -> fp16, built from the exponent bits:
+    2^e is exact in fp16 for e in [-24, 15] (subnormal below -14); below that it rounds to 0,
+    above to +inf (also for the E8M0 NaN code 255), as the reference's fp32 power cast to fp16
+    gives (mxfp4/convert.py:68-98). Same device as the input."""
+    if scale_u8.dtype != torch.uint8:
+        raise TypeError(f"E8M0 scales must be uint8, got {scale_u8.dtype}")
+    e = scale_u8.to(torch.int32) - 127
+    sub = torch.where(e >= -24, torch.ones_like(e) << (e + 24).clamp(0, 9), torch.zeros_like(e))
+    bits = torch.where(e >= -14, (e + 15).clamp(0, 31) << 10, sub)
+    bits = torch.where(e > 15, torch.full_like(e, 0x7C00), bits)
+    return bits.to(torch.int16).view(torch.float16)
+
+
+def convert_mxfp4_moe(weight_packed: torch.Tensor, weight_scale: torch.Tensor) -> dict:
+    """mxfp4 MoE weights -> the op layout the E2M1 kernels read (mxfp4/convert.py:100-140):
+    weight_packed (E, N, K/2) uint8, two E2M1 codes a byte with the lower K index in the low
+    nibble, is already the (E, N, K/8) int32 container byte for byte (code k at nibble k % 8 of
+    word k / 8), so it is viewed, not copied; weight_scale (E, N, K/32) uint8 E8M0 becomes fp16
+    group scales. Symmetric (no zero-points), group size 32. ``scale_info`` reports scales
+    fp16 cannot hold (the reference's warning: such layers would need fp32 group scales)."""
+    if weight_packed.dtype != torch.uint8 or weight_packed.dim() != 3:
+        raise ValueError("mxfp4 weight_packed must be (E, N, K/2) uint8")
+    E, N, kh = weight_packed.shape
+    K = 2 * kh
+    if K % 8 != 0 or tuple(weight_scale.shape) != (E, N, K // MXFP4_BLOCK):
+        raise ValueError(f"mxfp4 weight_scale must be (E, N, K/{MXFP4_BLOCK}) for K = {K}")
+    w = weight_packed.contiguous().view(torch.int32).view(E, N, K // 8)
+    scales = e8m0_to_fp16(weight_scale.contiguous())
+    e = weight_scale.to(torch.int32) - 127
+    info = dict(exp_min=int(e.min()), exp_max=int(e.max()),
+                fp16_overflow_groups=int((e > 15).sum()),
+                fp16_subnormal_groups=int(((e < -14) & (e >= -24)).sum()),
+                fp16_zero_groups=int((e < -24).sum()),
+                e8m0_nan_groups=int((weight_scale == 255).sum()))
+    info["fp16_range_ok"] = (info["fp16_overflow_groups"] == 0 and info["e8m0_nan_groups"] == 0
+                             and info["fp16_zero_groups"] == 0)
+    return dict(w_packed=w, scales=scales, w_zeros=None, group_size=MXFP4_BLOCK, scale_info=info)
+
+
 def _fragments_to_op_layout(w_frag: torch.Tensor) -> torch.Tensor:
     """Fragment layout (E, N/16, K/128, 64, 4) -> op layout (E, N, K/8): lane l = 16 q + c of
     block (t, g) holds row 16 t + c, words 16 g + 4 q .. + 3."""
@@ -175,10 +222,11 @@ def _activation_name(activation) -> str:
 
 def _run_unfused(x16, w1, w2, w1_s, w2_s, w1_zp, w2_zp, tw_flat, topk_ids, top_k,
                  global_num_experts, expert_map, kernel, weight_is_e2m1, w1_bias, w2_bias,
-                 block_m):
-    """Op-by-op composition (moe_experts.py:587-665): align, gemm1, + bias, silu_and_mul,
-    gemm2 on the padded rows, + bias, gather-reduce. Runs the "scalar" golden kernel and
-    layers with per-expert biases."""
+                 block_m, activation="silu"):
+    """Op-by-op composition (moe_experts.py:587-665): align, gemm1, + bias, the gated
+    activation (silu_and_mul on [gate | up] halves, or gpt-oss swigluoai_and_mul on
+    interleaved gate/up), gemm2 on the padded rows, + bias, gather-reduce. Runs the "scalar"
+    golden kernel, layers with per-expert biases and non-SiLU activations."""
     sorted_ids, expert_ids, ntp = moe_align_block_size(
         topk_ids, block_m, global_num_experts, expert_map)
     P = sorted_ids.size(0)
@@ -190,7 +238,10 @@ def _run_unfused(x16, w1, w2, w1_s, w2_s, w1_zp, w2_zp, tw_flat, topk_ids, top_k
     if w1_bias is not None:
         out1 = out1 + w1_bias.to(out1.dtype).index_select(0, row_expert)
     h = torch.empty((P, out1.size(1) // 2), dtype=torch.float16, device=x16.device)
-    silu_and_mul(h, out1.contiguous())
+    if activation == "swigluoai":
+        _ops.swigluoai_and_mul(h, out1.contiguous())
+    else:
+        silu_and_mul(h, out1.contiguous())
     rows = torch.arange(P, dtype=torch.int32, device=x16.device)   # gemm2 gathers by row
     out2 = mmq_fp8_moe_gemm(h, w2, w2_s, rows, expert_ids, ntp, 1, block_m,
                             kernel=kernel, w_zeros=w2_zp, weight_is_e2m1=weight_is_e2m1)
@@ -213,9 +264,11 @@ def _run_grouped_moe(x, w1, w2, w1_s, w2_s, w1_zp, w2_zp,
     M, K = x.shape
     top_k = topk_ids.size(1)
     out_dtype = x.dtype if out_dtype is None else out_dtype
-    if _activation_name(activation) != "silu":
+    act = _activation_name(activation)
+    if act not in GATED_ACTIVATIONS:
         raise NotImplementedError(
-            f"w4a8_fp8_wmma (gfx950) implements the SiLU-gated MoE; got {activation!r}")
+            f"w4a8_fp8_wmma (gfx950) implements the gated activations {GATED_ACTIVATIONS}; "
+            f"got {activation!r}")
     if kernel not in MOE_KERNEL_NAMES:
         raise ValueError(f"unknown moe kernel {kernel!r}; known: {list(MOE_KERNEL_NAMES)}")
     env = MoeEnv.read()
@@ -242,13 +295,13 @@ def _run_grouped_moe(x, w1, w2, w1_s, w2_s, w1_zp, w2_zp,
         tw = topk_weights.to(torch.float32)
     ids = topk_ids.to(torch.int32)
 
-    if kernel == "scalar" or w1_bias is not None or w2_bias is not None:
+    if kernel == "scalar" or w1_bias is not None or w2_bias is not None or act != "silu":
         if w1.dim() == 5:   # the op-by-op kernels read the op layout
             w1, w2 = _fragments_to_op_layout(w1), _fragments_to_op_layout(w2)
         acc = _run_unfused(x.to(torch.float16).contiguous(), w1, w2, w1_s, w2_s, w1_zp, w2_zp,
                            tw.reshape(-1).contiguous(), ids, top_k, global_num_experts,
                            expert_map, kernel, weight_is_e2m1, w1_bias, w2_bias,
-                           env.block_m or 64)
+                           env.block_m or 64, act)
         return acc.to(out_dtype)
 
     if x.dtype not in (torch.float16, torch.bfloat16):
@@ -408,4 +461,121 @@ def register_moe_wna16(verbose: bool = True) -> bool:
         return False
     install_moe_wna16_hooks(MoeWNA16Method, verbose)
     _MOE_WNA16_REGISTERED = True
+    return True
+
+
+# --------------------------------------------------------------------------- #
+# vLLM mxfp4 (gpt-oss) hook (moe_experts.py:1351-1450)
+# --------------------------------------------------------------------------- #
+class MoeMxfp4Hook:
+    """Load and apply hooks for a ``GptOssMxfp4MoEMethod``-like class.
+
+    Load: the layer's E2M1 weights (``w13_weight`` / ``w2_weight``, (E, N, K/2) uint8) and
+    E8M0 scales (``w*_weight_scale``, (E, N, K/32) uint8) become the op layout on their own
+    device (``convert_mxfp4_moe``: the weight bytes are viewed, the scales become fp16); the
+    per-expert biases are kept; the source scale parameters are emptied. Apply: every batch
+    runs ``_run_grouped_moe`` with ``weight_is_e2m1`` (fp4-operand matrix-core tiles), the
+    layer's activation (swigluoai for gpt-oss) and both biases. A layer whose tensors are not
+    in that layout keeps the stock path."""
+
+    ATTR = "_w4a8_mxfp4"
+
+    def __init__(self, method_cls, verbose: bool = False):
+        self.method_cls = method_cls
+        self.verbose = verbose
+        self.stock_process = method_cls.process_weights_after_loading
+        self.stock_apply = method_cls.apply
+
+    @staticmethod
+    def prepare(layer) -> dict:
+        c13 = convert_mxfp4_moe(layer.w13_weight.data, layer.w13_weight_scale.data)
+        c2 = convert_mxfp4_moe(layer.w2_weight.data, layer.w2_weight_scale.data)
+        b13 = getattr(layer, "w13_bias", None)
+        b2 = getattr(layer, "w2_bias", None)
+        rec = dict(w13=c13["w_packed"], w2=c2["w_packed"], s13=c13["scales"], s2=c2["scales"],
+                   b13=None if b13 is None else b13.data, b2=None if b2 is None else b2.data,
+                   scale_info=(c13["scale_info"], c2["scale_info"]))
+        layer._w4a8_mx = rec
+        # the fp16 scales replace the E8M0 bytes; the weight parameters keep their storage
+        # (the op-layout weights are views of it)
+        for name in ("w13_weight_scale", "w2_weight_scale"):
+            prm = getattr(layer, name, None)
+            if prm is not None and hasattr(prm, "data"):
+                prm.data = torch.empty(0, dtype=prm.dtype, device=prm.device)
+        return rec
+
+    def process(self, method, layer):
+        try:
+            rec = self.prepare(layer)
+        except (AttributeError, ValueError, TypeError) as e:   # not the E2M1/E8M0 layout
+            setattr(method, self.ATTR, False)
+            if self.verbose:
+                print(f"[w4a8_fp8_wmma] mxfp4 MoE: stock path ({e})")
+            return self.stock_process(method, layer)
+        setattr(method, self.ATTR, True)
+        if not all(i["fp16_range_ok"] for i in rec["scale_info"]):
+            logger.warning("mxfp4 MoE: E8M0 scales outside the fp16 group-scale range; "
+                           "results may be wrong (%s)", rec["scale_info"])
+        if self.verbose:
+            print("[w4a8_fp8_wmma] mxfp4 MoE weights ready (E2M1, E8M0 -> fp16, group 32) "
+                  "-> gfx950 fp4-operand MFMA")
+
+    def apply(self, method, layer, x, topk_weights, topk_ids, shared_experts=None,
+              shared_experts_input=None, **kw):
+        if not getattr(method, self.ATTR, False):
+            return self.stock_apply(method, layer, x, topk_weights, topk_ids, shared_experts,
+                                    shared_experts_input, **kw)
+        w = layer._w4a8_mx
+        flat = x.reshape(-1, x.shape[-1])
+        out = _run_grouped_moe(
+            flat, w["w13"], w["w2"], w["s13"], w["s2"], None, None, topk_weights, topk_ids,
+            layer.activation, layer.global_num_experts, layer.expert_map,
+            layer.apply_router_weight_on_input, _moe_kernel(), out_dtype=x.dtype,
+            weight_is_e2m1=True, w1_bias=w["b13"], w2_bias=w["b2"])
+        return out.reshape(*x.shape[:-1], out.shape[-1])
+
+    def install(self) -> None:
+        hook = self
+
+        def process_weights_after_loading(self, layer):
+            hook.process(self, layer)
+
+        def apply(self, layer, x, topk_weights, topk_ids, shared_experts=None,
+                  shared_experts_input=None, **kw):
+            return hook.apply(self, layer, x, topk_weights, topk_ids, shared_experts,
+                              shared_experts_input, **kw)
+
+        self.method_cls.process_weights_after_loading = process_weights_after_loading
+        self.method_cls.apply = apply
+
+
+_MOE_MXFP4_REGISTERED = False
+
+
+def install_moe_mxfp4_hooks(method_cls, verbose: bool = False) -> MoeMxfp4Hook:
+    """Patch a GptOssMxfp4MoEMethod-like class (split out so tests can use a stand-in)."""
+    hook = MoeMxfp4Hook(method_cls, verbose)
+    hook.install()
+    return hook
+
+
+def register_moe_mxfp4(verbose: bool = True) -> bool:
+    """Route gpt-oss mxfp4 expert layers to the gfx950 path (moe_experts.py:1351-1450).
+    Idempotent; False without vLLM or when disabled by the environment."""
+    global _MOE_MXFP4_REGISTERED
+    if _MOE_MXFP4_REGISTERED:
+        return True
+    env = MoeEnv.read()
+    if not env.enabled:
+        if verbose:
+            print("[w4a8_fp8_wmma] mxfp4 MoE disabled via env")
+        return False
+    try:
+        from vllm.model_executor.layers.quantization.mxfp4 import GptOssMxfp4MoEMethod
+    except Exception as e:  # noqa: BLE001  (vLLM absent: nothing to patch)
+        if verbose:
+            print(f"[w4a8_fp8_wmma] mxfp4 MoE: vLLM not importable ({type(e).__name__})")
+        return False
+    install_moe_mxfp4_hooks(GptOssMxfp4MoEMethod, verbose)
+    _MOE_MXFP4_REGISTERED = True
     return True

@@ -1,9 +1,9 @@
 """vLLM general-plugin entry point (w4a8_fp8_wmma/w4a8_fp8_wmma/register.py:42-175).
 
 ``register()`` prepends the dense W4A8 linear kernel to vLLM's ROCm linear-kernel list and
-installs the MoeWNA16 MoE hook, each best-effort so one failing leaves the other in place.
-The reference's other hooks (mxfp4 dense registry, compressed-tensors and mxfp4 MoE) are
-outside this package's scope. Removed env knobs raise at boot, like the reference
+installs the MoeWNA16 and the mxfp4 (gpt-oss) MoE hooks, each best-effort so one failing
+leaves the others in place. The reference's other hooks (mxfp4 dense registry,
+compressed-tensors MoE) are outside this package's scope. Removed env knobs raise at boot, like the reference
 (register.py:29-39).
 """
 from __future__ import annotations
@@ -29,8 +29,9 @@ def register() -> None:
         register_dense_linear()
     except ImportError as e:
         print(f"[w4a8_fp8_wmma] dense linear kernel not registered: {e}")
-    from .moe_experts import register_moe_wna16
-    try:
-        register_moe_wna16()
-    except ImportError as e:
-        print(f"[w4a8_fp8_wmma] MoE hook not installed: {e}")
+    from .moe_experts import register_moe_mxfp4, register_moe_wna16
+    for hook in (register_moe_wna16, register_moe_mxfp4):
+        try:
+            hook()
+        except ImportError as e:
+            print(f"[w4a8_fp8_wmma] MoE hook {hook.__name__} not installed: {e}")

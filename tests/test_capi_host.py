@@ -194,12 +194,81 @@ def test_torch_converters_match_oracle():
     assert np.array_equal(O.unpack_nibbles(cw.numpy()), np.swapaxes(q, 1, 2))
 
 
-def test_run_grouped_moe_rejects_non_silu():
+def test_run_grouped_moe_rejects_unknown_activations():
     x = torch.zeros(2, 256, dtype=torch.bfloat16)
     with pytest.raises(NotImplementedError):
         moe_experts._run_grouped_moe(x, None, None, None, None, None, None, None,
                                      torch.zeros(2, 2, dtype=torch.int32), "gelu", 4, None,
                                      False, "wmma")
+
+
+def test_mxfp4_converter_matches_oracle():
+    """convert_mxfp4_moe: the E2M1 bytes are viewed as the op layout (no copy) and the E8M0
+    scales become the oracle's fp16 values, every code included."""
+    r = np.random.default_rng(11)
+    E, N, K = 3, 16, 256
+    wp = r.integers(0, 256, (E, N, K // 2), dtype=np.uint8)
+    ws = r.integers(0, 256, (E, N, K // 32), dtype=np.uint8)
+    ws.reshape(-1)[:256] = np.arange(256)                      # all 256 E8M0 codes
+    c = moe_experts.convert_mxfp4_moe(torch.from_numpy(wp), torch.from_numpy(ws))
+    ow, osc = O.convert_mxfp4(wp, ws)
+    assert c["w_packed"].dtype == torch.int32 and c["w_packed"].shape == (E, N, K // 8)
+    assert np.array_equal(c["w_packed"].numpy(), ow)
+    assert np.array_equal(c["scales"].numpy().view(np.uint16), osc.view(np.uint16))
+    assert c["w_zeros"] is None and c["group_size"] == 32
+    info = c["scale_info"]
+    assert info["e8m0_nan_groups"] >= 1 and not info["fp16_range_ok"]
+    with pytest.raises(ValueError):
+        moe_experts.convert_mxfp4_moe(torch.from_numpy(wp), torch.from_numpy(ws[..., :-1]))
+
+
+def test_mxfp4_hook_with_stand_in_class():
+    """Drive the patched mxfp4 process with a stand-in GptOssMxfp4MoEMethod (no vLLM): the
+    layer gets op-layout views of its E2M1 bytes, fp16 scales and its biases; a layer in
+    another layout keeps the stock path."""
+    calls = {}
+
+    class Method:
+        def process_weights_after_loading(self, layer):
+            calls["process"] = True
+
+        def apply(self, layer, x, topk_weights, topk_ids, shared_experts=None,
+                  shared_experts_input=None, **kw):
+            return "stock"
+
+    moe_experts.install_moe_mxfp4_hooks(Method)
+    E, H, I = 2, 64, 32
+    r = np.random.default_rng(12)
+
+    def u8(*shape):
+        return torch.nn.Parameter(torch.from_numpy(r.integers(0, 256, shape, dtype=np.uint8)), False)
+
+    class Layer:
+        w13_weight = u8(E, 2 * I, H // 2)
+        w13_weight_scale = u8(E, 2 * I, H // 32)
+        w2_weight = u8(E, H, I // 2)
+        w2_weight_scale = u8(E, H, I // 32)
+        w13_bias = torch.nn.Parameter(torch.zeros(E, 2 * I), False)
+        w2_bias = torch.nn.Parameter(torch.zeros(E, H), False)
+
+    layer = Layer()
+    s13 = layer.w13_weight_scale.data.clone()
+    m = Method()
+    m.process_weights_after_loading(layer)
+    assert "process" not in calls and m._w4a8_mxfp4
+    rec = layer._w4a8_mx
+    assert rec["w13"].shape == (E, 2 * I, H // 8) and rec["w13"].dtype == torch.int32
+    assert rec["w13"].data_ptr() == layer.w13_weight.data.data_ptr()      # zero-copy view
+    assert np.array_equal(rec["s13"].numpy().view(np.uint16), O.e8m0_to_fp16(s13.numpy()).view(np.uint16))
+    assert rec["b13"].data_ptr() == layer.w13_bias.data_ptr() and layer.w13_weight_scale.numel() == 0
+
+    class Other:       # a layout the converter refuses: the stock path stays
+        w13_weight = torch.nn.Parameter(torch.zeros(E, 2 * I, H // 2), False)
+
+    m2 = Method()
+    m2.process_weights_after_loading(Other())
+    assert calls.get("process") and not m2._w4a8_mxfp4
+    assert m2.apply(Other(), None, None, None) == "stock"
 
 
 def test_env_hard_break_and_kernel_env(monkeypatch):

@@ -187,3 +187,77 @@ def test_repack_fragments_is_a_permutation_of_words():
     bad = f.copy()
     bad[..., [0, 16], :] = bad[..., [16, 0], :]
     assert not np.array_equal(O.unrepack_fragments(bad), w)
+
+
+def _swigluoai_f64(x16, alpha=1.702, limit=7.0):
+    x = np.asarray(x16, np.float16).astype(np.float64)
+    gate, up = x[..., 0::2], x[..., 1::2]
+    g = np.minimum(gate, limit)
+    u = np.clip(up, -limit, limit)
+    return (u + 1.0) * g / (1.0 + np.exp(-alpha * g))
+
+
+def test_swigluoai_against_float64_closed_form():
+    """Within half an fp16 ulp (plus the fp32 intermediates' few ulps) of the float64 closed
+    form, over values that cross both clamps."""
+    r = np.random.default_rng(21)
+    x = (r.standard_normal((64, 512)) * 6).astype(np.float16)
+    got = O.swigluoai_and_mul(x).astype(np.float64)
+    ref = _swigluoai_f64(x)
+    ulp = np.spacing(np.abs(ref).astype(np.float16)).astype(np.float64)
+    assert np.all(np.abs(got - ref) <= 0.5 * ulp + 1e-6 * np.abs(ref) + 1e-12)
+
+
+def test_swigluoai_cases_and_planted_mistakes():
+    # clamps: gate above 7 -> 7; up beyond +-7 -> +-7; up = -1 -> 0; gate = 0 -> 0
+    x = np.array([[100, 0, 100, 100, 100, -100, 0, 5, 3, -1]], np.float16)
+    got = O.swigluoai_and_mul(x).astype(np.float64)[0]
+    s7 = 7.0 / (1.0 + np.exp(-1.702 * 7.0))
+    exp = np.array([s7 * 1.0, s7 * 8.0, s7 * -6.0, 0.0, 0.0])
+    assert np.allclose(got, exp, rtol=1e-3, atol=0)
+    # mistakes the definition rules out: [gate | up] halves instead of interleaved pairs,
+    # no clamp, the +1 dropped
+    r = np.random.default_rng(22)
+    x = (r.standard_normal((16, 256)) * 6).astype(np.float16)
+    good = O.swigluoai_and_mul(x).astype(np.float64)
+    halves = np.concatenate([x[:, :128], x[:, 128:]], axis=1)
+    inter = np.empty_like(x)
+    inter[:, 0::2], inter[:, 1::2] = x[:, :128], x[:, 128:]
+    assert np.abs(O.swigluoai_and_mul(inter).astype(np.float64) - good).max() > 1e-1
+    xf = x.astype(np.float64)
+    no_clamp = (xf[:, 1::2] + 1) * xf[:, 0::2] / (1 + np.exp(-1.702 * xf[:, 0::2]))
+    assert np.abs(no_clamp - good).max() > 1e-1
+    no_plus1 = _swigluoai_f64(x) - np.minimum(xf[:, 0::2], 7.0) / (1 + np.exp(-1.702 * np.minimum(xf[:, 0::2], 7.0)))
+    assert np.abs(no_plus1 - good).max() > 1e-1
+    del halves
+
+
+def test_e8m0_to_fp16_all_codes():
+    """2^(s - 127): exact in fp16 for exponents -24..15, 0 below (2^-25 ties to even), +inf
+    above and for the NaN code 255."""
+    import math
+    got = O.e8m0_to_fp16(np.arange(256)).astype(np.float64)
+    for s_ in range(256):
+        e = s_ - 127
+        if e > 15:
+            assert np.isinf(got[s_]) and got[s_] > 0
+        elif e >= -24:
+            assert got[s_] == math.ldexp(1.0, e), s_
+        else:
+            assert got[s_] == 0.0, s_
+
+
+def test_convert_mxfp4_nibble_order_bruteforce():
+    """Code k of row n is the low nibble of byte k / 2 for even k, the high one for odd k,
+    and lands at nibble k % 8 of word k / 8."""
+    r = np.random.default_rng(23)
+    wp = r.integers(0, 256, (2, 4, 32), dtype=np.uint8)
+    wp_s = r.integers(100, 140, (2, 4, 2), dtype=np.uint8)
+    w, sc = O.convert_mxfp4(wp, wp_s)
+    wu = w.view(np.uint32)
+    for e in range(2):
+        for n in range(4):
+            for k in range(64):
+                code = (int(wp[e, n, k // 2]) >> (4 * (k % 2))) & 0xF
+                assert (int(wu[e, n, k // 8]) >> (4 * (k % 8))) & 0xF == code
+    assert np.array_equal(sc, O.e8m0_to_fp16(wp_s))
