@@ -155,8 +155,8 @@ def cpu_baseline(cfg, ws, x, tw, ids, out_gpu, budget_s, sample=None):
     torch.set_num_threads(cores)
     host = {k: (None if v is None else v.cpu()) for k, v in ws.items()}
     for k in ("w13", "w2"):   # the port reads the op layout
-        if host[k].dim() == 5:
-            host[k] = torch.from_numpy(O.unrepack_fragments(host[k].numpy()))
+        if host[k].dim() == 4:
+            host[k] = torch.from_numpy(O.unrepack_fragments(host[k].numpy())[0])
     xc, twc, idc = x.float().cpu(), tw.cpu(), ids.cpu()
     T = xc.shape[0]
     round_y = T > 96
@@ -268,8 +268,8 @@ def measure(name, args, steps, warmup, cpu_budget, tokens=0, eager=False, strati
     if args.layout == "fragments":
         # load-time repack (the process_weights_after_loading step); op-layout copies freed
         for ws in sets:
-            ws["w13"] = W.repack_fragments(ws["w13"])
-            ws["w2"] = W.repack_fragments(ws["w2"])
+            ws["w13"] = W.repack_fragments(ws["w13"], ws["s13"], ws["z13"])
+            ws["w2"] = W.repack_fragments(ws["w2"], ws["s2"], ws["z2"])
         torch.cuda.synchronize()
         torch.cuda.empty_cache()
     x, logits = make_inputs(cfg, 1000 + cfgno, dev)

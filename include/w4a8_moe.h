@@ -205,18 +205,31 @@ W4A8_API int w4a8_moe_apply(const void* x, int x_dtype, int64_t T, int64_t H, in
                    const int32_t* expert_map, int64_t num_global_experts, int weight_is_e2m1,
                    void* out, void* workspace, size_t workspace_bytes, void* stream);
 
-/* Load-time repack of int4 weights from the op layout (E, N, K/8) int32 (moe_kernel.hip:7-17)
- * into the fragment layout the gfx950 kernels stream: per expert, 16-row tile t and 128-wide
- * K group g, one 1 KB block whose 16-byte lane l holds row 16t + l % 16, k in
- * [128g + 32 (l / 16), +32) (the fp8 MFMA B operand of lane l); blocks ordered (e, t, g).
- * A pure permutation of 16-byte words (same size). Needs N % 16 == 0, K % 128 == 0; out
- * must not alias w_packed. No reference counterpart: the reference streams the op layout,
- * and its load hook (moe_experts.py:1277-1306) is where a caller runs this once. */
-W4A8_API int w4a8_repack_int4_fragments(const int32_t* w_packed, int64_t E, int64_t N, int64_t K,
+/* Load-time repack of int4 weights, their scales and zero-points from the op layout
+ * (moe_kernel.hip:7-17) into the fragment layout the gfx950 kernels stream, with each
+ * 16-row tile's metadata next to its weights. Per expert and 16-row tile t, G = K/128 blocks
+ * of 1 KB, then G * 16 metadata words (w4a8_fragments_words() words in all, out is
+ * (E, N/16, 272 G) int32):
+ *   - block g's 16-byte lane l holds row 16t + l % 16, k in [128g + 32 (l / 16), +32) (the
+ *     fp8 MFMA B operand of lane l), so a wave's fragment-group is one contiguous KB;
+ *   - metadata word r * G + g is row 16t + r, group g: fp16 scale bits in bits 0..15, the
+ *     zero-point in bits 16..19 (8 when w_zeros is NULL).
+ * The int4 words are a pure permutation of 16-byte words. Needs N % 16 == 0, K % 128 == 0,
+ * group size 128; out must not alias w_packed. No reference counterpart: the reference
+ * streams the op layout, and its load hook (moe_experts.py:1277-1306) is where a caller runs
+ * this once. */
+W4A8_API int w4a8_repack_int4_fragments(const int32_t* w_packed, const void* scales_f16,
+                                        const int32_t* w_zeros, int64_t E, int64_t N, int64_t K,
                                         int32_t* out, void* stream);
 
-/* w4a8_moe_apply on weights repacked by w4a8_repack_int4_fragments (w13 and w2); scales
- * and zero-points stay in the op layout. Same workspace (w4a8_moe_apply_workspace_size) and
+/* int32 words of w4a8_repack_int4_fragments' output for E experts of N rows and K columns
+ * (E * N/16 * 272 * K/128), or -1 for sizes it does not take. No reference counterpart. */
+W4A8_API int64_t w4a8_fragments_words(int64_t E, int64_t N, int64_t K);
+
+/* w4a8_moe_apply on weights repacked by w4a8_repack_int4_fragments (w13 and w2). The
+ * op-layout scales and zero-points are still passed (the schedules that do not read the
+ * copies inside the fragment layout use them) and must be the ones the repack read. Same
+ * workspace (w4a8_moe_apply_workspace_size) and
  * bit-identical results. Needs group_size 128 and int4 weights (no E2M1); hidden and
  * intermediate sizes must be multiples of 128 that the schedule chosen for T takes: the
  * decode GEMV (T <= 96) needs K/128 in {1,2,3,4,6,8,12,16,32}, the prefill tiles K <= 4096.

@@ -57,8 +57,9 @@ PINNING = {
     "convert_mxfp4": "per-element brute force of the nibble order on random bytes; scales "
                      "through e8m0_to_fp16",
     "repack_fragments": "per-element brute force of the layout definition on tiny shapes "
-                        "(nibble of row n, k lands in lane n % 16 + 16 * ((k % 128) // 32)); "
-                        "inverse restores the op layout exactly",
+                        "(nibble of row n, k lands in lane n % 16 + 16 * ((k % 128) // 32); "
+                        "scale and zero-point of (n, g) in metadata word (n % 16) G + g of "
+                        "tile n / 16); inverse restores the op layout exactly",
 }
 
 # --------------------------------------------------------------------------- #
@@ -166,27 +167,48 @@ def pack_nibbles(nib) -> np.ndarray:
     return w.astype(np.uint32).view(np.int32)
 
 
-def repack_fragments(w_packed) -> np.ndarray:
-    """Op layout (E, N, K/8) int32 -> fragment layout (E, N/16, K/128, 64, 4) int32.
+FRAG_TILE_WORDS_PER_GROUP = 272    # per 16-row tile and K group: 256 fragment + 16 metadata words
 
-    Not a reference function: the gfx950 kernels' load-time layout. Block (e, t, g) lane l
+
+def repack_fragments(w_packed, scales, w_zeros=None) -> np.ndarray:
+    """Op layout (E, N, K/8) int32, scales (E, N, K/128) fp16 and zero-points
+    (E, N/8, K/128) int32 or None -> fragment layout (E, N/16, 17, 16 K/128) int32 (tile t:
+    [..., :16, :] its weight blocks, [..., 16, :] its metadata).
+
+    Not a reference function: the gfx950 kernels' load-time layout. 16-row tile t of expert e
+    is G = K/128 blocks of 1 KB, then its metadata, G * 16 words. Block (e, t, g) lane l
     (16 bytes = 4 words) holds row n = 16t + l % 16, words 16g + 4 (l // 16) .. +3, i.e.
-    k in [128g + 32 (l // 16), +32): the raw-nibble fp8 MFMA B operand of lane l."""
+    k in [128g + 32 (l // 16), +32): the raw-nibble fp8 MFMA B operand of lane l. Metadata
+    word r * G + g of the tile is row 16t + r, group g: its fp16 scale's bits in bits 0..15
+    and its zero-point (8 when there are none) in bits 16..19."""
     w = np.asarray(w_packed)
     E, N, K8 = w.shape
     G = K8 // 16
     assert N % 16 == 0 and K8 % 16 == 0
     # (E, t, c, g, q, word) -> (E, t, g, q, c, word); lane = 16 q + c
-    v = w.reshape(E, N // 16, 16, G, 4, 4).transpose(0, 1, 3, 4, 2, 5)
-    return np.ascontiguousarray(v).reshape(E, N // 16, G, 64, 4)
+    v = w.reshape(E, N // 16, 16, G, 4, 4).transpose(0, 1, 3, 4, 2, 5).reshape(E, N // 16, G * 256)
+    sb = np.asarray(scales, dtype=np.float16).view(np.uint16).astype(np.uint32)
+    assert sb.shape == (E, N, G)
+    z = np.full((E, N, G), 8, np.uint32) if w_zeros is None else \
+        unpack_zeros(w_zeros, N).astype(np.uint32)
+    meta = (sb | (z << 16)).reshape(E, N // 16, 16 * G)
+    f = np.concatenate([v.astype(np.int32), meta.view(np.int32)], axis=2)
+    return np.ascontiguousarray(f).reshape(E, N // 16, 17, 16 * G)
 
 
-def unrepack_fragments(w_frag) -> np.ndarray:
-    """Inverse of repack_fragments: (E, N/16, K/128, 64, 4) -> (E, N, K/8)."""
+def unrepack_fragments(w_frag):
+    """Inverse of repack_fragments: (E, N/16, 17, 16 G) -> (w_packed (E, N, K/8) int32,
+    scales (E, N, G) fp16, zero-points (E, N, G) uint8 as integers 0..15)."""
     f = np.asarray(w_frag)
-    E, NT, G = f.shape[:3]
-    v = f.reshape(E, NT, G, 4, 16, 4).transpose(0, 1, 4, 2, 3, 5)
-    return np.ascontiguousarray(v).reshape(E, NT * 16, G * 16)
+    E, NT = f.shape[:2]
+    G = f.shape[3] // 16
+    f = f.reshape(E, NT, FRAG_TILE_WORDS_PER_GROUP * G)
+    v = f[:, :, :G * 256].reshape(E, NT, G, 4, 16, 4).transpose(0, 1, 4, 2, 3, 5)
+    w = np.ascontiguousarray(v).reshape(E, NT * 16, G * 16)
+    meta = f[:, :, G * 256:].view(np.uint32).reshape(E, NT * 16, G)
+    sc = (meta & 0xFFFF).astype(np.uint16).view(np.float16)
+    zp = ((meta >> 16) & 0xF).astype(np.uint8)
+    return w, sc, zp
 
 
 def unpack_zeros(w_zeros, N: int) -> np.ndarray:

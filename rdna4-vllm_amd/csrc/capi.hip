@@ -555,7 +555,7 @@ int noalloc_scratch(void** out) {
 
 extern "C" {
 
-int w4a8_abi_version(void) { return 2; }
+int w4a8_abi_version(void) { return 3; }
 
 const char* w4a8_last_error(void) { return g_error.c_str(); }
 
@@ -896,14 +896,20 @@ int w4a8_moe_fragments_supported(int64_t H, int64_t inter, int64_t group_size) {
            fragments_schedule_ok(false, H, inter, group_size);
 }
 
-int w4a8_repack_int4_fragments(const int32_t* w_packed, int64_t E, int64_t N, int64_t K,
+int64_t w4a8_fragments_words(int64_t E, int64_t N, int64_t K) {
+    if (E < 0 || N < 0 || K < 0 || N % 16 != 0 || K % 128 != 0) return -1;
+    return fragments_words(E, N, K);
+}
+
+int w4a8_repack_int4_fragments(const int32_t* w_packed, const void* scales_f16,
+                               const int32_t* w_zeros, int64_t E, int64_t N, int64_t K,
                                int32_t* out, void* stream) {
     clear_error();
     W4A8_REQUIRE(E >= 0 && N >= 0 && K >= 0, "repack: invalid sizes");
     W4A8_REQUIRE(N % 16 == 0 && K % 128 == 0, "repack: needs N % 16 == 0 and K % 128 == 0");
-    W4A8_REQUIRE(E * N * K == 0 || (w_packed && out), "repack: null pointer");
+    W4A8_REQUIRE(E * N * K == 0 || (w_packed && scales_f16 && out), "repack: null pointer");
     W4A8_REQUIRE(w_packed != out, "repack: out must not alias w_packed");
-    return launch_repack_fragments(w_packed, E, N, K, out, as_stream(stream));
+    return launch_repack_fragments(w_packed, scales_f16, w_zeros, E, N, K, out, as_stream(stream));
 }
 
 }  // extern "C"

@@ -52,9 +52,7 @@ struct DecodeParams {
     const void* a;           // activation rows, fp16 / bf16
     int a_bf16;
     int a_per_token;         // 1: slot s reads row s / top_k (x); 0: row s (h)
-    const int32_t* w;        // fragment layout (E, N/16, G, 64, 4)
-    const __half* scales;    // (E, N, G)
-    const int32_t* zeros;    // (E, N/8, G) or null
+    const int32_t* w;        // fragment layout (E, N/16, 272 G): blocks, then scales/zeros
     void* out;               // kSiluHalf: (numel, N/2) fp16; kSlotF32: (numel, N) fp32
     int K, N, G;
 };
@@ -227,27 +225,20 @@ struct DecCfg {
     static constexpr int LDS_BYTES = KSPLIT > 1 ? 2 * D * KSPLIT * FR * 64 * 16 : 0;
 };
 
-// GC fp16 scales, two per word (group u in the low half of word u / 2 when u is even)
+// GC metadata words of one row (groups g .. g + GC - 1, adjacent in the tile): one 16-byte
+// load for 4 groups and one 8-byte load for 2 (their offsets are multiples of that size:
+// G % 4 == 0 and g % 4 == 0 where GC == 4, g even where GC == 2), single words otherwise
 template <int GC>
-__device__ __forceinline__ void dec_load_scales(const __half* ptr, uint32_t (&s)[(GC + 1) / 2]) {
-    const uint16_t* h = reinterpret_cast<const uint16_t*>(ptr);
+__device__ __forceinline__ void dec_load_meta(const int32_t* ptr, uint32_t (&m)[GC]) {
     if constexpr (GC == 4) {
-        const uint2 v = *reinterpret_cast<const uint2*>(h);
-        s[0] = v.x; s[1] = v.y;
+        const uint4 v = *reinterpret_cast<const uint4*>(ptr);
+        m[0] = v.x; m[1] = v.y; m[2] = v.z; m[3] = v.w;
+    } else if constexpr (GC == 2) {
+        const uint2 v = *reinterpret_cast<const uint2*>(ptr);
+        m[0] = v.x; m[1] = v.y;
     } else {
 #pragma unroll
-        for (int u = 0; u < GC; u += 2)
-            s[u / 2] = (uint32_t)h[u] | (u + 1 < GC ? (uint32_t)h[u + 1] << 16 : 0u);
-    }
-}
-template <int GC>
-__device__ __forceinline__ void dec_load_zeros(const int32_t* ptr, int32_t (&z)[GC]) {
-    if constexpr (GC == 4) {
-        const int4 v = *reinterpret_cast<const int4*>(ptr);
-        z[0] = v.x; z[1] = v.y; z[2] = v.z; z[3] = v.w;
-    } else {
-#pragma unroll
-        for (int u = 0; u < GC; ++u) z[u] = ptr[u];
+        for (int u = 0; u < GC; ++u) m[u] = (uint32_t)ptr[u];
     }
 }
 
@@ -382,8 +373,7 @@ __device__ __forceinline__ void dec_run(const DecodeParams& p, const DecodeLists
     };
 
     uint4 wv[C::D][C::GC * C::FR];
-    uint32_t sw[C::D][C::FR][(C::GC + 1) / 2];
-    int32_t zw[C::D][C::FR][C::GC];
+    uint32_t mw[C::D][C::FR][C::GC];   // metadata words: fp16 scale | zero-point << 16
     uint4 raw[GPW][4];
     v8i af[GPW];
     v4f sa[GPW];   // 2^-9 * group sums of rows 4q .. 4q + 3 (zero-point term)
@@ -409,21 +399,18 @@ __device__ __forceinline__ void dec_run(const DecodeParams& p, const DecodeLists
         const int g = g0 + (live ? c.b * C::GC : 0);
         const int ucol = live ? c.u - c.r * upe : 0;
         const int64_t e = live ? c.e : 0;
-        const int32_t* we = p.w + e * p.N * (p.K / 8);
-        const __half* se = p.scales + e * p.N * p.G;
-        // symmetric weights read (and ignore) the scale words in place of zero points: one
-        // address computation, no branch (branches here make the compiler's waits conservative)
-        const int32_t* zb = p.zeros ? p.zeros : reinterpret_cast<const int32_t*>(p.scales);
-        const int64_t zstride = p.zeros ? (int64_t)p.G : 0;
-        const int32_t* ze = zb + (p.zeros ? e * (p.N / 8) * p.G : 0);
+        const int tw = frag_tile_words(p.G);
+        const int32_t* we = p.w + e * (int64_t)(p.N / 16) * tw;
 #pragma unroll
         for (int f = 0; f < C::FR; ++f) {
             const int n = row_of(ucol, f, c16);
-            const int32_t* wr = we + ((int64_t)(n >> 4) * p.G + g) * 256 + lane * 4;
+            // the 16-row tile of row n: its weight blocks, then its rows' scales and
+            // zero-points (the lane's row, groups g .. g + GC - 1 adjacent)
+            const int32_t* wt = we + (int64_t)(n >> 4) * tw;
+            const int32_t* wr = wt + g * 256 + lane * 4;
 #pragma unroll
             for (int uu = 0; uu < C::GC; ++uu) wv[b][uu * C::FR + f] = load_stream16(wr + uu * 256);
-            dec_load_scales<C::GC>(se + (int64_t)n * p.G + g, sw[b][f]);
-            dec_load_zeros<C::GC>(ze + (n >> 3) * zstride + (p.zeros ? g : 0), zw[b][f]);
+            dec_load_meta<C::GC>(wt + frag_meta_word(p.G, n & 15, g), mw[b][f]);
         }
     };
 
@@ -594,17 +581,16 @@ __device__ __forceinline__ void dec_run(const DecodeParams& p, const DecodeLists
         const int ucol = c.u - c.r * upe;
 #pragma unroll
         for (int f = 0; f < C::FR; ++f) {
-            const int zsh = (row_of(ucol, f, c16) & 7) * 4;
 #pragma unroll
             for (int uu = 0; uu < C::GC; ++uu) {
                 const int ga = gb * C::GC + uu;
                 v4f acc = mfma_16x16x128(af[ga], spread_nibbles(wv[b][uu * C::FR + f]),
                                          v4f{0.f, 0.f, 0.f, 0.f});
-                const float z = p.zeros ? (float)((zw[b][f][uu] >> zsh) & 0xF) : 8.0f;
+                const uint32_t m = mw[b][f][uu];
+                const float z = (float)((m >> 16) & 0xF);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) acc[i] = fmaf(-z, sa[ga][i], acc[i]);
-                const float s = __half2float(__ushort_as_half(
-                    (unsigned short)(uu % 2 ? sw[b][f][uu / 2] >> 16 : sw[b][f][uu / 2])));
+                const float s = __half2float(__ushort_as_half((unsigned short)(m & 0xFFFF)));
 #pragma unroll
                 for (int i = 0; i < 4; ++i) run[f][i] = fmaf(acc[i], s, run[f][i]);
             }
@@ -916,8 +902,6 @@ DecodeParams dec_params(const DecodeLaunch& d) {
     p.a_bf16 = d.a_bf16 ? 1 : 0;
     p.a_per_token = d.silu ? 1 : 0;
     p.w = d.w;
-    p.scales = reinterpret_cast<const __half*>(d.scales);
-    p.zeros = d.zeros;
     p.out = d.out;
     p.K = (int)d.K;
     p.N = (int)d.N;

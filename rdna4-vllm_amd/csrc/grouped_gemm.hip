@@ -518,7 +518,9 @@ __global__ void __launch_bounds__(256, 2) grouped_gemv_kernel(Params p, int tpt)
     const int t_end = min(ntiles, t_begin + tpt);
     const int nsets = t_end > t_begin ? (t_end - t_begin + C::CT - 1) / C::CT : 0;
     const int nch = nsets * C::NB;
-    const int32_t* we = p.w + (int64_t)e * p.N * kw_row;
+    // fragment layout: 16-row tiles of frag_tile_words(G) words (blocks, then metadata)
+    const int32_t* we = p.w + (int64_t)e * (FRAG ? (int64_t)(p.N / 16) * frag_tile_words(p.G)
+                                                 : (int64_t)p.N * kw_row);
     const __half* se = p.scales + (int64_t)e * p.N * p.G;
     const int32_t* ze = p.zeros ? p.zeros + (int64_t)e * (p.N / 8) * p.G : nullptr;
     constexpr float wscale = kNibbleScale;
@@ -556,7 +558,7 @@ __global__ void __launch_bounds__(256, 2) grouped_gemv_kernel(Params p, int tpt)
             // op layout: row n, bytes 64 (g + u) + 16 q; fragment layout: block (n / 16, g + u)
             const uint32_t woff =
                 !live ? 0u
-                : FRAG ? (uint32_t)(n >> 4) * (uint32_t)p.G * 1024u + (uint32_t)lane * 16u
+                : FRAG ? (uint32_t)(n >> 4) * (uint32_t)frag_tile_words(p.G) * 4u + (uint32_t)lane * 16u
                        : (uint32_t)n * (uint32_t)(p.K / 2) + (uint32_t)q * 16u;
             // fragment layout: whole 128-byte lines per instruction, streamed (non-temporal,
             // read once per launch); op layout: 64-byte row pieces whose second half the

@@ -10,11 +10,17 @@ constexpr int kGroup = 128;          // K per group == K per fp8 MFMA
 // Raw-nibble MFMA operands carry n * 2^-9; results are scaled back by 2^9.
 constexpr float kNibbleScale = 512.0f;
 
+// Fragment layout (repack.hip): per expert and 16-row tile, G 1 KB blocks (256 words each)
+// and then G * 16 metadata words (row r, group g at word 256 G + r G + g: fp16 scale bits
+// 0..15, zero-point bits 16..19).
+__host__ __device__ constexpr int frag_tile_words(int G) { return 272 * G; }
+__host__ __device__ constexpr int frag_meta_word(int G, int r, int g) { return 256 * G + r * G + g; }
+
 struct Params {
     const uint8_t* xq;          // (x_rows, K) e4m3, k8-interleaved
     const float* asc;           // (x_rows,)
     const void* xh;             // (x_rows, K) fp16/bf16 rows (fused quantisation path)
-    const int32_t* w;           // (E, N, K/8), or fragment layout when w_frag
+    const int32_t* w;           // (E, N, K/8), or fragment layout when w_frag (E, N/16, 272 G)
     const __half* scales;       // (E, N, G)
     const int32_t* zeros;       // (E, N/8, G) or null
     const int32_t* sorted_ids;

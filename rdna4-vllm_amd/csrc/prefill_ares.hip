@@ -213,23 +213,27 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
     };
 
     const uint32_t half_k = (uint32_t)K / 2;           // bytes per op-layout weight row
-    const uint8_t* we = reinterpret_cast<const uint8_t*>(p.w) + (int64_t)e * p.N * half_k;
+    // fragment layout: 16-row tiles of tile_b bytes (the G weight blocks, then the tile's
+    // scales and zero-points)
+    const uint32_t tile_b = (uint32_t)frag_tile_words(G) * 4u;
+    const uint8_t* we = reinterpret_cast<const uint8_t*>(p.w) +
+                        (int64_t)e * (FRAG ? (int64_t)(p.N / 16) * tile_b : (int64_t)p.N * half_k);
     const uint16_t* se = reinterpret_cast<const uint16_t*>(p.scales) + (int64_t)e * p.N * G;
     const int32_t* ze = p.zeros ? p.zeros + (int64_t)e * (p.N / 8) * G : nullptr;
 
     // ---- B ring. Byte offset of fragment j at step (range r, group g) =
     //      step_off(r, g) + frag_off[j] (wave-uniform) + lane_off ----
-    //   fragment layout: 1 KB per (16-row block, group): ((row / 16) * G + g) * 1024 + lane * 16
+    //   fragment layout: 1 KB per (16-row block, group): (row / 16) * tile_b + g * 1024 + lane * 16
     //   op layout: row * K / 2 + g * 64 + q * 16 with row = first row + c16
     const uint32_t g_step = FRAG ? 1024u : 64u;
-    const uint32_t r_step = FRAG ? (uint32_t)(ar_range_cols<kSilu>() / 16) * G * 1024u
+    const uint32_t r_step = FRAG ? (uint32_t)(ar_range_cols<kSilu>() / 16) * tile_b
                                  : (uint32_t)ar_range_cols<kSilu>() * half_k;
     const uint32_t lane_off = FRAG ? (uint32_t)lane * 16u : (uint32_t)c16 * half_k + q * 16u;
     uint32_t frag_off[kArNT];
 #pragma unroll
     for (int j = 0; j < kArNT; ++j) {
         const uint32_t n0 = (uint32_t)ar_row<kSilu>(0, wave, j, 0, ncols);
-        frag_off[j] = FRAG ? (n0 / 16) * G * 1024u : n0 * half_k;
+        frag_off[j] = FRAG ? (n0 / 16) * tile_b : n0 * half_k;
     }
     uint4 bw[kArD][kArNT];
     uint32_t i_off = (uint32_t)r_begin * r_step;   // step_off of the next issue
@@ -266,7 +270,8 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
     //      fragment (l >> 4) & 1, column l & 15, for groups 16 h + 8 (l >> 5) .. + 7: two
     //      8-byte scale loads. Lane l also loads zero-point word 16 h + (l & 15) of the
     //      wave's 8-row group l >> 4; a row's group then reads its 8 words from the staging
-    //      area ----
+    //      area. On the fragment layout the lane's row keeps its scales and zero-points side
+    //      by side after its tile's weights: two 16-byte loads, no staging ----
     const int trow = lane & 31, tj = trow >> 4, tc = trow & 15, th = lane >> 5;
     // The range-boundary code (prefetch, build) recomputes its lane-derived indices from an
     // opaque copy of the lane id: hoisted out of the range loop, they stayed live across the
@@ -276,11 +281,23 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
     const int lrow = 32 * wave + trow;
     uint2 pf_s[2];
     uint32_t pf_z;
+    uint4 pf_m[2];      // fragment layout: metadata words (fp16 scale | zero-point << 16)
     auto prefetch = [&](int r, int h) __attribute__((always_inline)) {
         const int lane = lane_now();
         const int tj = (lane & 31) >> 4, tc = lane & 15, th = lane >> 5;
         const int rr = std::min(r, r_end - 1);
         const int n = ar_row<kSilu>(rr, wave, tj, tc, ncols);
+        if constexpr (FRAG) {
+            // row n's words for groups 16 h + 8 th .. + 7 (G % 4 == 0: 16-byte aligned)
+            const uint8_t* mt = we + (uint32_t)(n >> 4) * tile_b +
+                                (uint32_t)frag_meta_word(G, n & 15, 0) * 4u;
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int qd = std::min(4 * h + 2 * th + u, G / 4 - 1);
+                pf_m[u] = *reinterpret_cast<const uint4*>(mt + 16u * (uint32_t)qd);
+            }
+            return;
+        }
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
             const int qd = std::min(4 * h + 2 * th + u, G / 4 - 1);
@@ -296,9 +313,15 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
         const int lane = lane_now();
         const int tj = (lane & 31) >> 4, tc = lane & 15, th = lane >> 5, lrow = 32 * wave + (lane & 31);
         const int n = ar_row<kSilu>(r, wave, tj, tc, ncols);
-        s_zst[64 * wave + lane] = pf_z;
         uint32_t zw[8];
-        {
+        if constexpr (FRAG) {
+            // scale bits and zero-point of group 8 th + tt, word tt of the two loads
+            const uint32_t mw[8] = {pf_m[0].x, pf_m[0].y, pf_m[0].z, pf_m[0].w,
+                                    pf_m[1].x, pf_m[1].y, pf_m[1].z, pf_m[1].w};
+#pragma unroll
+            for (int tt = 0; tt < 8; ++tt) zw[tt] = mw[tt];
+        } else {
+            s_zst[64 * wave + lane] = pf_z;
             const int rgl = 2 * tj + (tc >> 3);
             const uint4* zr = reinterpret_cast<const uint4*>(s_zst + 64 * wave + 16 * rgl + 8 * th);
             const uint4 z0 = zr[0], z1 = zr[1];
@@ -313,11 +336,18 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
 #pragma unroll
             for (int v = 0; v < 2; ++v) {
                 const int tt = t + v, g = 8 * th + tt;
-                const uint2 sp = pf_s[tt / 4];
-                const uint32_t w2 = (tt & 2) ? sp.y : sp.x;
-                const uint16_t hb = (tt & 1) ? (uint16_t)(w2 >> 16) : (uint16_t)(w2 & 0xFFFF);
+                uint16_t hb;
+                float z;
+                if constexpr (FRAG) {
+                    hb = (uint16_t)(zw[tt] & 0xFFFF);
+                    z = (float)((zw[tt] >> 16) & 0xF);
+                } else {
+                    const uint2 sp = pf_s[tt / 4];
+                    const uint32_t w2 = (tt & 2) ? sp.y : sp.x;
+                    hb = (tt & 1) ? (uint16_t)(w2 >> 16) : (uint16_t)(w2 & 0xFFFF);
+                    z = ze ? (float)((zw[tt] >> zsh) & 0xF) : 8.0f;
+                }
                 const float sv = __half2float(__ushort_as_half(hb));
-                const float z = ze ? (float)((zw[tt] >> zsh) & 0xF) : 8.0f;
                 sz[v] = kArGp * h + g < G ? sv * z : 0.f;   // exact: fp16 scale x integer <= 15
                 s_sc[((wave * kArGp + g) * 4 + (tc >> 2)) * 8 + tj * 4 + (tc & 3)] = hb;
             }

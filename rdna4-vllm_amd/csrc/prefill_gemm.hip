@@ -155,7 +155,9 @@ __global__ void __launch_bounds__(256, 1) prefill_mfma_kernel(Params p, int nblo
 
     // ---- B fragments of this wave ----
     // SiLU: fragments 0,1 = gate columns col0 + {0..15, 16..31}, 2,3 = the same up columns.
-    const int32_t* we = p.w + (int64_t)e * p.N * kw_row;
+    // fragment layout: 16-row tiles of frag_tile_words(G) words (blocks, then metadata)
+    const int32_t* we = p.w + (int64_t)e * (FRAG ? (int64_t)(p.N / 16) * frag_tile_words(G)
+                                                 : (int64_t)p.N * kw_row);
     const __half* se = p.scales + (int64_t)e * p.N * G;
     const int32_t* ze = p.zeros ? p.zeros + (int64_t)e * (p.N / 8) * G : nullptr;
     auto weight_row = [&](int wv_, int j, int c, int& col) {
@@ -249,7 +251,7 @@ __global__ void __launch_bounds__(256, 1) prefill_mfma_kernel(Params p, int nblo
     uint32_t woff[kPfNT], soff[kPfNT];
 #pragma unroll
     for (int j = 0; j < kPfNT; ++j) {
-        woff[j] = FRAG ? (uint32_t)(wrow[j] >> 4) * (uint32_t)G * 1024u + (uint32_t)lane * 16u
+        woff[j] = FRAG ? (uint32_t)(wrow[j] >> 4) * (uint32_t)frag_tile_words(G) * 4u + (uint32_t)lane * 16u
                        : (uint32_t)wrow[j] * (uint32_t)(p.K / 2) + (uint32_t)q * 16u;
         soff[j] = (uint32_t)wrow[j] * (uint32_t)G * 2u;
     }

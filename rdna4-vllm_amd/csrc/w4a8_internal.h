@@ -185,8 +185,10 @@ bool prefill_ares_quantises_rows(int64_t K, Epi epi);
 // (E, N, K/8) int32 op layout -> fragment layout: per expert, 16-row tile t and 128-wide
 // group g, a 1 KB block whose 16-byte lane l holds row 16t + l % 16, k in
 // [128g + 32 (l / 16), +32) (the MFMA B operand of lane l). N % 16 == 0, K % 128 == 0.
-int launch_repack_fragments(const int32_t* w, int64_t E, int64_t N, int64_t K, int32_t* out,
-                            hipStream_t stream);
+int launch_repack_fragments(const int32_t* w, const void* scales, const int32_t* zeros,
+                            int64_t E, int64_t N, int64_t K, int32_t* out, hipStream_t stream);
+// int32 words of the fragment layout of E experts of N rows and K columns (K % 128 == 0)
+int64_t fragments_words(int64_t E, int64_t N, int64_t K);
 // Prefill tiles with raw-nibble B in registers; needs x_fp8, act_scales and act_group_sums.
 int launch_grouped_prefill(const GroupedArgs& a, hipStream_t stream);
 bool prefill_supported(int64_t K, int64_t group_size, bool e2m1);   // g128, K <= 4096, no E2M1

@@ -57,7 +57,9 @@ SIGNATURES = {
                               _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                               _c_void_p, _c_void_p, _i64, _int, _c_void_p, _c_void_p, _size,
                               _c_void_p]),
-    "w4a8_repack_int4_fragments": (_int, [_c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p]),
+    "w4a8_repack_int4_fragments": (_int, [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64,
+                                          _c_void_p, _c_void_p]),
+    "w4a8_fragments_words": (_i64, [_i64, _i64, _i64]),
     "w4a8_moe_forward": (_int, [_c_void_p, _int, _i64, _i64, _i64, _i64, _i64, _i64, _c_void_p,
                                 _int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                 _c_void_p, _int, _c_void_p, _i64, _c_void_p, _c_void_p,
@@ -75,7 +77,7 @@ SIGNATURES = {
     "w4a8_decode_fused_test_fault": (_int, [_int]),
 }
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 
 class W4A8LibraryError(RuntimeError):

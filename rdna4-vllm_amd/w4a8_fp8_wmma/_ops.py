@@ -363,20 +363,32 @@ def swigluoai_and_mul(out: torch.Tensor, x: torch.Tensor, alpha: float = SWIGLUO
                                      _stream(x)), "swigluoai_and_mul")
 
 
-def repack_fragments(w_packed: torch.Tensor) -> torch.Tensor:
-    """Op-layout int4 weights (E, N, K/8) int32 -> fragment layout (E, N/16, K/128, 64, 4)
-    int32: block (e, t, g) holds, in lane l's 16 bytes, row 16t + l % 16 and k in
-    [128g + 32 (l // 16), +32), the fp8 MFMA B operand of lane l. Run once at weight load
-    (the reference's process_weights_after_loading, moe_experts.py:1277-1306)."""
+def repack_fragments(w_packed: torch.Tensor, scales: torch.Tensor,
+                     w_zeros: torch.Tensor | None = None) -> torch.Tensor:
+    """Op-layout int4 weights (E, N, K/8) int32 with their fp16 scales (E, N, K/128) and
+    zero-points (E, N/8, K/128) int32 (or None) -> fragment layout (E, N/16, 17, 16 K/128)
+    int32. Tile t (rows 16t .. 16t + 15): [..., :16, :] holds K/128 blocks of 1 KB, block g's
+    lane l holding row 16t + l % 16 and k in [128g + 32 (l // 16), +32) (the fp8 MFMA B
+    operand of lane l); [..., 16, :] holds word r K/128 + g = row 16t + r, group g: fp16 scale
+    bits | zero-point << 16 (8 without zero-points). Run once at weight load (the reference's
+    process_weights_after_loading, moe_experts.py:1277-1306)."""
     _check(w_packed.is_cuda and w_packed.dtype == torch.int32 and w_packed.dim() == 3,
            "w_packed must be CUDA int32 (E, N, K/8)")
     w = w_packed.contiguous()
     E, N, K8 = w.shape
     K = K8 * 8
     _check(N % 16 == 0 and K % 128 == 0, "fragment layout needs N % 16 == 0 and K % 128 == 0")
-    out = torch.empty((E, N // 16, K // 128, 64, 4), dtype=torch.int32, device=w.device)
-    check(lib.w4a8_repack_int4_fragments(_ptr(w), E, N, K, _ptr(out), _stream(w)),
-          "repack_fragments")
+    G = K // 128
+    _check(scales.dtype == torch.float16 and tuple(scales.shape) == (E, N, G)
+           and scales.device == w.device, f"scales must be fp16 (E, N, K/128)=({E},{N},{G})")
+    sc = scales.contiguous()
+    z = _zeros_of(w_zeros, E, N, G, "zeros")
+    if z is not None:
+        _check(z.device == w.device, "zeros must be on w_packed's device")
+    out = torch.empty((E, N // 16, 17, 16 * G), dtype=torch.int32, device=w.device)
+    assert out.numel() == lib.w4a8_fragments_words(E, N, K)
+    check(lib.w4a8_repack_int4_fragments(_ptr(w), _ptr(sc), _ptr(z), E, N, K, _ptr(out),
+                                         _stream(w)), "repack_fragments")
     return out
 
 
@@ -400,17 +412,19 @@ def _layer_args(x, w13, w2, w13_s, w2_s, w13_z, w2_z, topk_weights, topk_ids, ex
     _check(x.dtype in (torch.float16, torch.bfloat16) and x.dim() == 2,
            "x must be fp16/bf16 (T, H)")
     T, H = x.shape
-    frag = w13.dim() == 5
+    frag = w13.dim() == 4
     _check(w2.dim() == w13.dim(), "w13 and w2 must share a layout")
     if frag:
-        _check(tuple(w13.shape[3:]) == (64, 4) and tuple(w2.shape[3:]) == (64, 4),
-               "fragment-layout weights must be (E, N/16, K/128, 64, 4)")
-        E, nt13, g13 = w13.shape[:3]
+        _check(w13.shape[2] == 17 and w2.shape[2] == 17 and w13.shape[3] % 16 == 0,
+               "fragment-layout weights must be (E, N/16, 17, 16 K/128)")
+        E, nt13 = w13.shape[:2]
+        g13 = w13.shape[3] // 16
         _check(nt13 % 2 == 0, "w13 fragments must hold 2*inter rows")
         inter = nt13 * 8
         _check(g13 * 128 == H, f"w13 fragments must cover K = H = {H}")
-        _check(tuple(w2.shape[:3]) == (E, H // 16, inter // 128),
-               f"w2 fragments must be (E, H/16, inter/128, 64, 4)=({E},{H // 16},{inter // 128},64,4)")
+        _check(tuple(w2.shape) == (E, H // 16, 17, 16 * (inter // 128)),
+               f"w2 fragments must be (E, H/16, 17, 16 inter/128)="
+               f"({E},{H // 16},17,{16 * (inter // 128)})")
         _check(not weight_is_e2m1, "fragment layout holds int4 weights only")
     else:
         _check(w13.dim() == 3, "w13 must be (E, 2*inter, H/8) int32")
@@ -456,7 +470,7 @@ def moe_apply(x, w13, w2, w13_s, w2_s, w13_z, w2_z, topk_weights, topk_ids, expe
               weight_is_e2m1: bool = False, global_num_experts: int | None = None) -> torch.Tensor:
     """Whole gated-SiLU MoE layer in one C-ABI call (the _run_grouped_moe composition,
     moe_experts.py:493-665). x (T, H) fp16/bf16 -> (T, H) same dtype. w13 / w2 are op-layout
-    (E, N, K/8) int32, or both fragment layout from repack_fragments (5-d). topk_ids hold
+    (E, N, K/8) int32, or both fragment layout from repack_fragments (4-d). topk_ids hold
     global expert ids; with expert_map (global_num_experts entries, -1 = not local) they are
     mapped to the E local experts."""
     x = x.contiguous()

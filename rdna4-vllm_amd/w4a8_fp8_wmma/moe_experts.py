@@ -205,10 +205,13 @@ def convert_mxfp4_moe(weight_packed: torch.Tensor, weight_scale: torch.Tensor) -
 
 
 def _fragments_to_op_layout(w_frag: torch.Tensor) -> torch.Tensor:
-    """Fragment layout (E, N/16, K/128, 64, 4) -> op layout (E, N, K/8): lane l = 16 q + c of
-    block (t, g) holds row 16 t + c, words 16 g + 4 q .. + 3."""
-    E, NT, G = w_frag.shape[:3]
-    v = w_frag.reshape(E, NT, G, 4, 16, 4).permute(0, 1, 4, 2, 3, 5)
+    """Fragment layout (E, N/16, 17, 16 K/128) -> op-layout weights (E, N, K/8): tile t's
+    first 16 rows of 16 G words are its G blocks of 64 lanes x 4 words, lane l = 16 q + c of
+    block g holding row 16 t + c, words 16 g + 4 q .. + 3 (row 16 is the tile's scale and
+    zero-point words, which the op layout keeps in its own tensors)."""
+    E, NT = w_frag.shape[:2]
+    G = w_frag.shape[3] // 16
+    v = w_frag[:, :, :16].reshape(E, NT, G, 4, 16, 4).permute(0, 1, 4, 2, 3, 5)
     return v.reshape(E, NT * 16, G * 16).contiguous()
 
 
@@ -258,7 +261,7 @@ def _run_grouped_moe(x, w1, w2, w1_s, w2_s, w1_zp, w2_zp,
     """Whole gated MoE -> (M, K) in ``out_dtype`` (moe_experts.py:493-665).
 
     w1 (E, 2*inter, K/8) / w2 (E, K, inter/8) int32 in the op layout, or both in the fragment
-    layout (5-d, ``repack_fragments``); scales (E, N, K/g); zero-points (E, N/8, K/g) or None
+    layout (4-d, ``repack_fragments``); scales (E, N, K/g); zero-points (E, N/8, K/g) or None
     (symmetric, zp = 8). topk_ids are global expert ids; ``expert_map`` maps them to the E
     local experts."""
     M, K = x.shape
@@ -296,7 +299,7 @@ def _run_grouped_moe(x, w1, w2, w1_s, w2_s, w1_zp, w2_zp,
     ids = topk_ids.to(torch.int32)
 
     if kernel == "scalar" or w1_bias is not None or w2_bias is not None or act != "silu":
-        if w1.dim() == 5:   # the op-by-op kernels read the op layout
+        if w1.dim() == 4:   # the op-by-op kernels read the op layout
             w1, w2 = _fragments_to_op_layout(w1), _fragments_to_op_layout(w2)
         acc = _run_unfused(x.to(torch.float16).contiguous(), w1, w2, w1_s, w2_s, w1_zp, w2_zp,
                            tw.reshape(-1).contiguous(), ids, top_k, global_num_experts,
@@ -344,9 +347,10 @@ class MoeWNA16Hook:
 
     Load (``process_weights_after_loading``): after the stock step, an int4 layer with a
     supported group size gets op-layout scales and zero-points, and its weights are repacked
-    once into the gfx950 fragment layout, written over the u8 parameters' own storage (same
-    byte count, no second copy; the parameters keep their shapes). Shapes the fragment
-    kernels do not take, and the "scalar" golden kernel, keep zero-copy op-layout views.
+    once into the gfx950 fragment layout (weights plus each tile's scale / zero-point words,
+    17/16 of the u8 bytes), which replaces the weight parameters' data, one weight at a time,
+    so the u8 bytes are freed as each fragment tensor is made. Shapes the fragment kernels
+    do not take, and the "scalar" golden kernel, keep zero-copy op-layout views.
     Apply: every batch of an engaged layer runs ``_run_grouped_moe``; other layers keep the
     stock apply."""
 
@@ -383,11 +387,11 @@ class MoeWNA16Hook:
         if kernel != "scalar" and _ops.fragments_supported(hidden, inter, group):
             layout = "fragments"
             for name in ("w13", "w2"):
-                param = getattr(layer, f"{name}_qweight")
-                frag = _ops.repack_fragments(views[name][0])
-                # the fragments replace the u8 bytes in place: same size, same parameter
-                param.data.view(torch.int32).view(-1).copy_(frag.view(-1))
-                views[name] = (param.data.view(torch.int32).view(frag.shape),) + views[name][1:]
+                w, s, z = views[name]
+                frag = _ops.repack_fragments(w, s, z)
+                del w
+                views[name] = (frag, s, z)
+                getattr(layer, f"{name}_qweight").data = frag   # the u8 bytes are released
             w13, w2 = views["w13"][0], views["w2"][0]
         layer._w4a8 = dict(w13=w13, w2=w2, s13=s13, s2=s2, z13=z13, z2=z2, layout=layout)
         return layout

@@ -39,7 +39,8 @@ def test_library_exports_exactly_the_header():
 
 def test_abi_version_and_sizes():
     L = _lib.lib
-    assert L.w4a8_abi_version() == 2
+    assert L.w4a8_abi_version() == 3
+    assert L.w4a8_fragments_words(2, 32, 256) == 2 * 2 * 272 * 2     # 16-row tiles of 272 G words
     assert L.w4a8_moe_align_sorted_len(256, 256, 16) == O.align_alloc_len(256, 256, 16)
     assert L.w4a8_moe_align_sorted_len(32768, 256, 64) == 48896      # SURVEY C4 P_alloc
     assert L.w4a8_moe_align_sorted_len(8, 256, 8) == 1800            # C2 with block_m 8
@@ -335,7 +336,8 @@ def test_wna16_hook_with_stand_in_class(monkeypatch):
 def test_fragments_to_op_layout_inverts_the_repack():
     r = np.random.default_rng(31)
     w = r.integers(-2**31, 2**31 - 1, (3, 48, 384 // 8), dtype=np.int64).astype(np.int32)
-    f = O.repack_fragments(w)
+    sc = r.standard_normal((3, 48, 3)).astype(np.float16)
+    f = O.repack_fragments(w, sc, O.pack_zeros(r.integers(0, 16, (3, 48, 3))))
     back = moe_experts._fragments_to_op_layout(torch.from_numpy(f))
     assert np.array_equal(back.numpy(), w)
 

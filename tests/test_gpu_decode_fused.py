@@ -39,7 +39,7 @@ def layer(name, T, seed):
     cfg = dict(bench.CONFIGS[name]) if isinstance(name, str) else dict(name)
     cfg["T"] = T
     ws = bench.make_weights(cfg, seed, DEV)
-    ws["f13"], ws["f2"] = W.repack_fragments(ws["w13"]), W.repack_fragments(ws["w2"])
+    ws["f13"], ws["f2"] = W.repack_fragments(ws["w13"], ws["s13"], ws["z13"]), W.repack_fragments(ws["w2"], ws["s2"], ws["z2"])
     x, logits = bench.make_inputs(cfg, seed + 1, DEV)
     return cfg, ws, x, logits
 

@@ -90,7 +90,7 @@ def test_benched_path_full_size_stratified(name):
     print(f"\n[{name}] T={cfg['T']} H={cfg['H']} E={cfg['E']} I={cfg['I']}", flush=True)
     ws = bench.make_weights(cfg, 1000 + cfgno * 17, DEV)
     x, logits = bench.make_inputs(cfg, 1000 + cfgno, DEV)
-    f13, f2 = W.repack_fragments(ws["w13"]), W.repack_fragments(ws["w2"])
+    f13, f2 = W.repack_fragments(ws["w13"], ws["s13"], ws["z13"]), W.repack_fragments(ws["w2"], ws["s2"], ws["z2"])
     out, tw, ids = W.moe_forward(x, logits, cfg["k"], f13, f2, ws["s13"], ws["s2"], ws["z13"],
                                  ws["z2"])
     out_op, tw_op, ids_op = W.moe_forward(x, logits, cfg["k"], ws["w13"], ws["w2"], ws["s13"],
@@ -114,7 +114,7 @@ def test_crafted_counts_cover_every_partial_tile_c4_shape():
     tw_np /= tw_np.sum(1, keepdims=True)
     ids = torch.from_numpy(ids_np).to(DEV)
     tw = torch.from_numpy(tw_np).to(DEV)
-    f13, f2 = W.repack_fragments(ws["w13"]), W.repack_fragments(ws["w2"])
+    f13, f2 = W.repack_fragments(ws["w13"], ws["s13"], ws["z13"]), W.repack_fragments(ws["w2"], ws["s2"], ws["z2"])
     out = W.moe_apply(x, f13, f2, ws["s13"], ws["s2"], ws["z13"], ws["z2"], tw, ids)
     out_op = W.moe_apply(x, ws["w13"], ws["w2"], ws["s13"], ws["s2"], ws["z13"], ws["z2"], tw, ids)
     assert torch.equal(out, out_op)
@@ -131,7 +131,7 @@ def test_c5_shape_decode_fragments(T):
     cfg["T"] = T
     ws = bench.make_weights(cfg, 5150 + T, DEV)
     x, logits = bench.make_inputs(cfg, 5151 + T, DEV)
-    f13, f2 = W.repack_fragments(ws["w13"]), W.repack_fragments(ws["w2"])
+    f13, f2 = W.repack_fragments(ws["w13"], ws["s13"], ws["z13"]), W.repack_fragments(ws["w2"], ws["s2"], ws["z2"])
     out, tw, ids = W.moe_forward(x, logits, cfg["k"], f13, f2, ws["s13"], ws["s2"], ws["z13"],
                                  ws["z2"])
     out_op, _, _ = W.moe_forward(x, logits, cfg["k"], ws["w13"], ws["w2"], ws["s13"], ws["s2"],

@@ -106,11 +106,18 @@ def test_patched_moe_wna16_layer(case):
     rec = layer._w4a8
     want = "fragments" if g == 128 else "op"
     assert rec["layout"] == want
-    assert layer.w13_qweight.data.data_ptr() == u8_ptr      # repacked in place, no copy
-    assert rec["w13"].data_ptr() == u8_ptr
+    # the parameter holds what the kernels read: the fragments, or the zero-copy op view
+    assert rec["w13"].data_ptr() == layer.w13_qweight.data.data_ptr()
     if want == "fragments":
+        assert rec["w13"].shape == (E, 2 * I // 16, 17, 16 * (H // 128))
+        w, sc, zp = O.unrepack_fragments(rec["w13"].cpu().numpy())
+        assert np.array_equal(w, truth["w13"]) and np.array_equal(sc, truth["s13"])
+        want_zp = O.unpack_zeros(truth["z13"], 2 * I) if has_zp else np.full(sc.shape, 8)
+        assert np.array_equal(zp, want_zp)
         assert np.array_equal(moe_experts._fragments_to_op_layout(rec["w13"]).cpu().numpy(),
                               truth["w13"])
+    else:
+        assert rec["w13"].data_ptr() == u8_ptr
 
     x = torch.from_numpy(r.standard_normal((T, H)).astype(np.float32)).to(DEV).to(torch.bfloat16)
     logits = r.standard_normal((T, E)).astype(np.float32)

@@ -100,7 +100,7 @@ def test_expert_map_global_ids_beyond_local_count(T, frag):
     emap = torch.from_numpy(emap_np).to(DEV)
     w13, w2 = ws["w13"], ws["w2"]
     if frag:
-        w13, w2 = W.repack_fragments(w13), W.repack_fragments(w2)
+        w13, w2 = W.repack_fragments(w13, ws["s13"], ws["z13"]), W.repack_fragments(w2, ws["s2"], ws["z2"])
     out, tw, ids = W.moe_forward(x, logits, 3, w13, w2, ws["s13"], ws["s2"], ws["z13"], ws["z2"],
                                  expert_map=emap)
     assert int(ids.max()) >= 4 and int(ids.min()) < 4
@@ -213,7 +213,7 @@ def test_prefill_layer_equals_op_composition(T, frag):
     tw, ids = W.fused_topk(None, logits, cfg["k"], True)
     w13, w2 = ws["w13"], ws["w2"]
     if frag:
-        w13, w2 = W.repack_fragments(w13), W.repack_fragments(w2)
+        w13, w2 = W.repack_fragments(w13, ws["s13"], ws["z13"]), W.repack_fragments(w2, ws["s2"], ws["z2"])
     fused = W.moe_apply(x, w13, w2, ws["s13"], ws["s2"], ws["z13"], ws["z2"], tw, ids)
     unfused = moe_experts._run_unfused(
         x.to(torch.float16), ws["w13"], ws["w2"], ws["s13"], ws["s2"], ws["z13"], ws["z2"],
@@ -235,7 +235,7 @@ def test_prefill_wide_k_tiles(H, T, frag):
     tw, ids = W.fused_topk(None, logits, cfg["k"], True)
     w13, w2 = ws["w13"], ws["w2"]
     if frag:
-        w13, w2 = W.repack_fragments(w13), W.repack_fragments(w2)
+        w13, w2 = W.repack_fragments(w13, ws["s13"], ws["z13"]), W.repack_fragments(w2, ws["s2"], ws["z2"])
     out = W.moe_apply(x, w13, w2, ws["s13"], ws["s2"], ws["z13"], ws["z2"], tw, ids)
     ref = oracle_layer(cfg, ws, x, tw, ids)
     err = maxrel(out.float().cpu().numpy(), ref)
@@ -270,9 +270,9 @@ def test_fragment_layout_bit_identical(T, asym):
     (decode GEMV and prefill tiles), and the repack equals the oracle permutation."""
     cfg, ws, x, tw, ids = small_layer(300 + T, T, 16, 512, 256, 4, asym=asym)
     a = W.moe_apply(x, ws["w13"], ws["w2"], ws["s13"], ws["s2"], ws["z13"], ws["z2"], tw, ids)
-    f13, f2 = W.repack_fragments(ws["w13"]), W.repack_fragments(ws["w2"])
-    assert np.array_equal(f13.cpu().numpy(), O.repack_fragments(ws["w13"].cpu().numpy()))
-    assert np.array_equal(f2.cpu().numpy(), O.repack_fragments(ws["w2"].cpu().numpy()))
+    f13, f2 = W.repack_fragments(ws["w13"], ws["s13"], ws["z13"]), W.repack_fragments(ws["w2"], ws["s2"], ws["z2"])
+    assert np.array_equal(f13.cpu().numpy(), O.repack_fragments(*_host(ws, "13")))
+    assert np.array_equal(f2.cpu().numpy(), O.repack_fragments(*_host(ws, "2")))
     b = W.moe_apply(x, f13, f2, ws["s13"], ws["s2"], ws["z13"], ws["z2"], tw, ids)
     assert torch.equal(a, b)
 
@@ -286,7 +286,7 @@ def test_fragment_layout_full_size(name, T):
     x, logits = bench.make_inputs(cfg, 556, DEV)
     tw, ids = W.fused_topk(None, logits, cfg["k"], True)
     a = W.moe_apply(x, ws["w13"], ws["w2"], ws["s13"], ws["s2"], ws["z13"], ws["z2"], tw, ids)
-    b = W.moe_apply(x, W.repack_fragments(ws["w13"]), W.repack_fragments(ws["w2"]), ws["s13"],
+    b = W.moe_apply(x, W.repack_fragments(ws["w13"], ws["s13"], ws["z13"]), W.repack_fragments(ws["w2"], ws["s2"], ws["z2"]), ws["s13"],
                     ws["s2"], ws["z13"], ws["z2"], tw, ids)
     assert torch.equal(a, b)
 
@@ -305,7 +305,7 @@ def test_moe_forward_equals_router_then_apply(T, frag, E):
     x = x.to(torch.bfloat16)
     w13, w2 = ws["w13"], ws["w2"]
     if frag:
-        w13, w2 = W.repack_fragments(w13), W.repack_fragments(w2)
+        w13, w2 = W.repack_fragments(w13, ws["s13"], ws["z13"]), W.repack_fragments(w2, ws["s2"], ws["z2"])
     tw, ids = W.fused_topk(None, logits, cfg["k"], True)
     a = W.moe_apply(x, w13, w2, ws["s13"], ws["s2"], ws["z13"], ws["z2"], tw, ids)
     b, tw2, ids2 = W.moe_forward(x, logits, cfg["k"], w13, w2, ws["s13"], ws["s2"], ws["z13"],
@@ -372,7 +372,7 @@ def test_graph_replay_forward_fragments_fresh_inputs(T):
     gemm1 launch, 32 has the router launch, 300 is the prefill schedule."""
     cfg = dict(T=T, H=512, E=64, k=8, I=256, g=128, routing="uniform")
     ws = bench.make_weights(cfg, 900 + T, DEV)
-    f13, f2 = W.repack_fragments(ws["w13"]), W.repack_fragments(ws["w2"])
+    f13, f2 = W.repack_fragments(ws["w13"], ws["s13"], ws["z13"]), W.repack_fragments(ws["w2"], ws["s2"], ws["z2"])
     x, logits = bench.make_inputs(cfg, 901 + T, DEV)
     xs, ls = x.clone(), logits.clone()
 
@@ -411,7 +411,7 @@ def test_decode_six_group_intermediate(T, frag):
     assert W.fragments_supported(512, 768, 128)
     w13, w2 = ws["w13"], ws["w2"]
     if frag:
-        w13, w2 = W.repack_fragments(w13), W.repack_fragments(w2)
+        w13, w2 = W.repack_fragments(w13, ws["s13"], ws["z13"]), W.repack_fragments(w2, ws["s2"], ws["z2"])
     out = W.moe_apply(x, w13, w2, ws["s13"], ws["s2"], ws["z13"], ws["z2"], tw, ids)
     ref = oracle_layer(cfg, ws, x, tw, ids)
     assert maxrel(out.float().cpu().numpy(), ref) <= REL_TOL
@@ -436,10 +436,16 @@ def _same_fp32_output(ob, oh):
     return bool(ok.all()), int((~ok).sum())
 
 
+def _host(ws, w):
+    """Op-layout weights, scales and zero-points of weight w ("13" / "2") as numpy."""
+    z = ws["z" + w]
+    return ws["w" + w].cpu().numpy(), ws["s" + w].cpu().numpy(), None if z is None else z.cpu().numpy()
+
+
 def _bf16_routes(cfg, ws, x, logits, frag):
     w13, w2 = ws["w13"], ws["w2"]
     if frag:
-        w13, w2 = W.repack_fragments(w13), W.repack_fragments(w2)
+        w13, w2 = W.repack_fragments(w13, ws["s13"], ws["z13"]), W.repack_fragments(w2, ws["s2"], ws["z2"])
     ob, twb, idb = W.moe_forward(x, logits, cfg["k"], w13, w2, ws["s13"], ws["s2"], ws["z13"],
                                  ws["z2"])
     oh, twh, idh = W.moe_forward(x.to(torch.float16), logits, cfg["k"], w13, w2, ws["s13"],

@@ -159,34 +159,53 @@ def test_bf16_rounding(bits):
     assert np.array_equal(O.f32_to_bf16_bits(x), ref)
 
 
-@pytest.mark.parametrize("E,N,K", [(1, 16, 128), (2, 32, 256), (3, 48, 384)])
-def test_repack_fragments_bruteforce(E, N, K):
-    """Every nibble of row n, column k sits in block (n // 16, k // 128), lane
+@pytest.mark.parametrize("E,N,K,zp", [(1, 16, 128, True), (2, 32, 256, False), (3, 48, 384, True)])
+def test_repack_fragments_bruteforce(E, N, K, zp):
+    """Every nibble of row n, column k sits in block (n // 16, k // 128) of its tile, lane
     n % 16 + 16 * ((k % 128) // 32), nibble (k % 32) of that lane's 16 bytes (low nibble
-    first): the fp8 MFMA B operand layout (lane l -> column l % 16, k = 32 (l // 16) + i)."""
+    first): the fp8 MFMA B operand layout (lane l -> column l % 16, k = 32 (l // 16) + i).
+    Row n's scale and zero-point for group g are metadata word (n % 16) G + g after tile
+    n // 16's blocks (scale bits low, zero-point in bits 16..19, 8 without zero-points)."""
     r = np.random.default_rng(E * 1000 + N + K)
+    G = K // 128
     nib = r.integers(0, 16, (E, N, K))
     w = O.pack_nibbles(nib)
-    f = O.repack_fragments(w)
-    assert f.shape == (E, N // 16, K // 128, 64, 4) and f.dtype == np.int32
-    lane_nib = O.unpack_nibbles(f)            # (E, N/16, K/128, 64, 32)
+    sc = r.uniform(0.005, 0.02, (E, N, G)).astype(np.float16)
+    zz = r.integers(0, 16, (E, N, G))
+    z = O.pack_zeros(zz) if zp else None
+    f = O.repack_fragments(w, sc, z)
+    assert f.shape == (E, N // 16, 17, 16 * G) and f.dtype == np.int32
+    f = f.reshape(E, N // 16, 272 * G)
+    blocks = f[:, :, :256 * G].reshape(E, N // 16, G, 64, 4)
+    lane_nib = O.unpack_nibbles(blocks)            # (E, N/16, G, 64, 32)
+    meta = f[:, :, 256 * G:].view(np.uint32)
     for e in range(E):
         for n in range(N):
             for k in range(K):
                 lane = n % 16 + 16 * ((k % 128) // 32)
                 assert lane_nib[e, n // 16, k // 128, lane, k % 32] == nib[e, n, k]
-    assert np.array_equal(O.unrepack_fragments(f), w)
+            for g in range(G):
+                m = int(meta[e, n // 16, (n % 16) * G + g])
+                assert m & 0xFFFF == int(sc[e, n, g].view(np.uint16))
+                assert (m >> 16) == (int(zz[e, n, g]) if zp else 8)
+    w2, sc2, zp2 = O.unrepack_fragments(f.reshape(E, N // 16, 17, 16 * G))
+    assert np.array_equal(w2, w) and np.array_equal(sc2.view(np.uint16), sc.view(np.uint16))
+    assert np.array_equal(zp2, zz if zp else np.full_like(zz, 8))
 
 
 def test_repack_fragments_is_a_permutation_of_words():
     r = np.random.default_rng(7)
     w = r.integers(-2**31, 2**31, (4, 64, 512 // 8), dtype=np.int64).astype(np.int32)
-    f = O.repack_fragments(w)
-    assert np.array_equal(np.sort(f.ravel()), np.sort(w.ravel()))
+    sc = np.ones((4, 64, 4), np.float16)
+    f = O.repack_fragments(w, sc).reshape(4, 4, 272 * 4)
+    G = 4
+    assert np.array_equal(np.sort(f[:, :, :256 * G].ravel()), np.sort(w.ravel()))
     # a planted transposition of lane halves is caught by the inverse
     bad = f.copy()
-    bad[..., [0, 16], :] = bad[..., [16, 0], :]
-    assert not np.array_equal(O.unrepack_fragments(bad), w)
+    blk = bad[:, :, :256 * G].reshape(4, 4, G, 64, 4)
+    blk[..., [0, 16], :] = blk[..., [16, 0], :]
+    bad[:, :, :256 * G] = blk.reshape(4, 4, 256 * G)
+    assert not np.array_equal(O.unrepack_fragments(bad.reshape(4, 4, 17, 64))[0], w)
 
 
 def _swigluoai_f64(x16, alpha=1.702, limit=7.0):

@@ -32,8 +32,8 @@ def _weights(H, I, E, seed, layout):
     cfg = dict(T=1, H=H, E=E, k=1, I=I, g=128, routing="uniform")
     ws = bench.make_weights(cfg, seed, DEV)
     if layout == 1:
-        ws["w13"] = W.repack_fragments(ws["w13"])
-        ws["w2"] = W.repack_fragments(ws["w2"])
+        ws["w13"] = W.repack_fragments(ws["w13"], ws["s13"], ws["z13"])
+        ws["w2"] = W.repack_fragments(ws["w2"], ws["s2"], ws["z2"])
     return ws
 
 
