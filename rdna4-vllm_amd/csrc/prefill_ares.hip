@@ -604,12 +604,17 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
                 } else {
                     const __half2 a01 = __floats2half2_rn(va[0], va[1]), a23 = __floats2half2_rn(va[2], va[3]);
                     const __half2 b01 = __floats2half2_rn(vb[0], vb[1]), b23 = __floats2half2_rn(vb[2], vb[3]);
-                    if (live) {
-                        *reinterpret_cast<uint2*>(rowp) = make_uint2(__builtin_bit_cast(uint32_t, a01),
-                                                                     __builtin_bit_cast(uint32_t, a23));
-                        *reinterpret_cast<uint2*>(rowp + 16) = make_uint2(__builtin_bit_cast(uint32_t, b01),
-                                                                          __builtin_bit_cast(uint32_t, b23));
-                    }
+                    // one 16-byte piece per lane: rows of 16 lanes pair up (q, q ^ 1); the even
+                    // one takes its partner's four fragment-0 columns, the odd one gives its
+                    // fragment-0 columns and takes its partner's fragment-1 columns, so lane q
+                    // holds columns 4 q + 12 (q & 1) .. + 7 (every lane takes part)
+                    const auto s0 = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, a01),
+                                                                     __builtin_bit_cast(uint32_t, b01), false, false);
+                    const auto s1 = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, a23),
+                                                                     __builtin_bit_cast(uint32_t, b23), false, false);
+                    if (live)
+                        *reinterpret_cast<uint4*>(rowp + 12 * (q & 1)) =
+                            make_uint4((uint32_t)s0[0], (uint32_t)s1[0], (uint32_t)s0[1], (uint32_t)s1[1]);
                 }
             }
         };
