@@ -45,7 +45,9 @@ PINNING = {
         "against the unpacked ground truth (reference test property) + round trips",
     "moe_layer": "float64 un-quantised MoE within the fp8 quantisation error bound; "
                  "composition equals the per-stage oracle chain; biases: closed form on a "
-                 "zero-weight layer and the per-stage chain with torch fp16 adds",
+                 "zero-weight layer and the per-stage chain with torch fp16 adds; "
+                 "swigluoai with biases: float64 un-quantised layer (moe_layer_f64) within "
+                 "the fp8 error, planted bias / gate-up-layout mistakes caught",
     "expert_weights_f64": "equals the e4m3 byte round trip E4M3_TO_F64[dequant_codes] on "
                            "random weights, sym and asym (exhaustive table test covers all "
                            "256 nibble/zero-point pairs)",
@@ -620,9 +622,12 @@ def moe_layer(x, w13, s13, z13, w2, s2, z2, topk_weights, topk_ids,
 
 
 def moe_layer_f64(x, w13, s13, z13, w2, s2, z2, topk_weights, topk_ids,
-                  group_size: int = 128) -> np.ndarray:
+                  group_size: int = 128, activation: str = "silu", w1_bias=None,
+                  w2_bias=None) -> np.ndarray:
     """Un-quantised float64 MoE (dequantised int4 weights, no activation quant):
-    the 'ideal' model test_moe_experts.py reports against."""
+    the 'ideal' model test_moe_experts.py reports against. ``activation`` "swigluoai" is
+    vLLM's gpt-oss activation on interleaved gate/up (alpha 1.702, limit 7); biases are
+    per-expert rows added to gemm1's and gemm2's outputs."""
     xf = np.asarray(x, dtype=np.float64)
     T, H = xf.shape
     ids = np.asarray(topk_ids).astype(np.int64)
@@ -644,8 +649,18 @@ def moe_layer_f64(x, w13, s13, z13, w2, s2, z2, topk_weights, topk_ids,
                 cache[e] = (deq(w13, s13, z13, e), deq(w2, s2, z2, e))
             W1, W2 = cache[e]
             g = W1 @ xf[t]
-            hh = g[:inter] / (1.0 + np.exp(-g[:inter])) * g[inter:]
-            out[t] += tw[t, j] * (W2 @ hh)
+            if w1_bias is not None:
+                g = g + np.asarray(w1_bias, np.float64)[e]
+            if activation == "swigluoai":
+                gt = np.minimum(g[0::2], SWIGLUOAI_LIMIT)
+                up = np.clip(g[1::2], -SWIGLUOAI_LIMIT, SWIGLUOAI_LIMIT)
+                hh = (up + 1.0) * gt / (1.0 + np.exp(-SWIGLUOAI_ALPHA * gt))
+            else:
+                hh = g[:inter] / (1.0 + np.exp(-g[:inter])) * g[inter:]
+            y = W2 @ hh
+            if w2_bias is not None:
+                y = y + np.asarray(w2_bias, np.float64)[e]
+            out[t] += tw[t, j] * y
     return out
 
 

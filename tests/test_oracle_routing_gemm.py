@@ -200,6 +200,27 @@ def test_layer_close_to_unquantised_f64():
     assert rel < 0.08, rel        # fp8 activation quantisation error only
 
 
+def test_swigluoai_bias_layer_close_to_unquantised_f64():
+    """The gpt-oss composition (per-expert biases on both GEMMs, swigluoai on interleaved
+    gate/up) against the float64 model; taking gate/up as halves (the SiLU layout), or
+    dropping either bias, moves the layer far outside the fp8 error."""
+    r = np.random.default_rng(23)
+    d = layer_inputs(r)
+    E, I2, H = d["w13"].shape[0], d["w13"].shape[1], d["w2"].shape[1]
+    b13 = (r.standard_normal((E, I2)) * 1.0).astype(np.float16)
+    b2 = (r.standard_normal((E, H)) * 2.0).astype(np.float16)
+    args = (d["x"], d["w13"], d["s13"], d["z13"], d["w2"], d["s2"], d["z2"], d["tw"], d["ids"])
+    got = O.moe_layer(*args, activation="swigluoai", w1_bias=b13, w2_bias=b2)
+    ideal = O.moe_layer_f64(*args, activation="swigluoai", w1_bias=b13, w2_bias=b2)
+    scale = np.abs(ideal).max()
+    assert np.abs(got - ideal).max() / scale < 0.05     # fp8 activation quantisation only
+    for planted in (dict(activation="swigluoai", w1_bias=b13),
+                    dict(activation="swigluoai", w2_bias=b2),
+                    dict(activation="silu", w1_bias=b13, w2_bias=b2)):
+        wrong = O.moe_layer_f64(*args, **planted)
+        assert np.abs(got - wrong).max() / scale > 0.1, planted
+
+
 def test_layer_equals_stage_chain():
     """The composed layer equals align -> padded gemm1 -> silu -> padded gemm2 (identity)
     -> gather-reduce built from the per-op oracle functions."""
