@@ -193,7 +193,10 @@ W4A8_API int w4a8_mmq_fp8_gemm(const void* x_f16, int64_t M, int64_t K, const in
  * expert_map (num_global_experts int32 entries, -1 = not local) each id is mapped to a local
  * expert in [0, E) and slots without one contribute nothing. Without a map,
  * num_global_experts must be E (or <= 0, meaning E). Chooses the decode (T <= 96) or
- * prefill schedule itself.
+ * prefill schedule itself. The prefill GEMMs take the activation-resident tiles only while
+ * their activation rows hold fewer than 2^31 elements (gemm1: T * H; gemm2: padded rows *
+ * inter), since those tiles address rows in 32 bits; larger calls run the streamed-K tiles
+ * (same results).
  */
 W4A8_API size_t w4a8_moe_apply_workspace_size(int64_t T, int64_t H, int64_t inter, int64_t E,
                                      int64_t top_k);

@@ -215,6 +215,43 @@ def test_moe_gemm_vs_oracle(kernel, asym, case):
     assert maxrel(got, ref[valid]) <= REL_TOL
 
 
+@pytest.mark.parametrize("kernel", ["scalar", "wmma", "gemv"])
+def test_raw_nibble_zero_point_arithmetic_exact(kernel):
+    """Every (nibble, zero-point) pair through the GEMM kernels' own int4 arithmetic (raw
+    nibbles as e4m3 n * 2^-9 with the z * sum(a) term deferred, or the scalar kernel's table),
+    where the sums are exact: token t is one-hot at k = 8 t (e4m3 448 after act-quant),
+    column c = 16 z + o has zero-point z and nibble (t + o) % 16 at that k, and the scales
+    are powers of two, so out[t, c] = e4m3(n - z) * s[c, t // 16] (the dequant table,
+    pinned exhaustively) exactly in fp16. A swapped nibble order, a wrong zero-point or a
+    scale from the wrong group changes at least one of the 16 x 16 pairs."""
+    r = rng(77)
+    T, N, K, g = 64, 256, 512, 128
+    t = np.arange(T)
+    c = np.arange(N)
+    z_of, o_of = c // 16, c % 16
+    nib = r.integers(0, 16, (1, N, K))
+    nib[0][:, 8 * t] = (t[None, :] + o_of[:, None]) % 16
+    zp = np.repeat(z_of[:, None], K // g, axis=1)[None]
+    sc = np.exp2(r.integers(-8, -1, (1, N, K // g))).astype(np.float16)
+    x = np.zeros((T, K), np.float16)
+    x[t, 8 * t] = 1.0
+    w, z = O.pack_nibbles(nib), O.pack_zeros(zp)
+    ids = np.zeros((T, 1), np.int32)
+    sti, eid, ntp = O.moe_align(ids, 16, 1)
+    xd, wd, zd, scd, stid, eidd, ntpd = to_dev(x, w, z, sc, sti, eid, ntp)
+    out = W.mmq_fp8_moe_gemm(xd, wd, scd, stid, eidd, ntpd, 1, 16, kernel=kernel, w_zeros=zd)
+    got = out.cpu().numpy()
+    rows = np.empty(T, np.int64)
+    rows[sti[:T]] = np.arange(T)           # padded row of token t (all of them are real here)
+    nv = nib[0][:, 8 * t].T                 # (T, N) nibble at the token's k
+    want = np.empty((T, N), np.float32)
+    for zz in range(16):
+        tab = O.e4m3_decode(O.dequant_table(zz)).astype(np.float32)
+        cols = z_of == zz
+        want[:, cols] = tab[nv[:, cols]] * sc[0][cols][:, t // 16].T.astype(np.float32)
+    assert np.array_equal(got[rows].astype(np.float32), want.astype(np.float16).astype(np.float32))
+
+
 E2M1_CASES = [
     # (T, E, N, K, top_k, block_m, g): mxfp4's block of 32, 64 and 128-wide groups
     (64, 8, 128, 256, 2, 16, 32),
