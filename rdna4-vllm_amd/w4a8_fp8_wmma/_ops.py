@@ -392,14 +392,21 @@ def repack_fragments(w_packed: torch.Tensor, scales: torch.Tensor,
     return out
 
 
+def _fail(msg: str):
+    raise RuntimeError(msg)
+
+
+# The per-call checks of the whole-layer entry points test plain conditions first and build
+# their messages only on failure (formatting every message cost ~8 us per call).
 def _zeros_of(z, E, N, G, name):
     """Optional packed zero-points (E, N/8, G) int32 of one weight, or None."""
     if z is None or z.numel() == 0:
         return None
-    _check(z.dtype == torch.int32, f"{name} must be int32 (packed)")
-    _check(N % 8 == 0 and tuple(z.shape) == (E, N // 8, G),
-           f"{name} must be (E, N/8, K/group)=({E},{N // 8},{G}); got {tuple(z.shape)}")
-    return z.contiguous()
+    if z.dtype != torch.int32:
+        _fail(f"{name} must be int32 (packed)")
+    if N % 8 != 0 or tuple(z.shape) != (E, N // 8, G):
+        _fail(f"{name} must be (E, N/8, K/group)=({E},{N // 8},{G}); got {tuple(z.shape)}")
+    return z if z.is_contiguous() else z.contiguous()
 
 
 def _layer_args(x, w13, w2, w13_s, w2_s, w13_z, w2_z, topk_weights, topk_ids, expert_map,
@@ -409,60 +416,73 @@ def _layer_args(x, w13, w2, w13_s, w2_s, w13_z, w2_z, topk_weights, topk_ids, ex
     mismatched tensor raises here instead of becoming an out-of-bounds read on the device.
     Shapes are checked before devices. Returns the sizes, the zero-point tensors, the expert
     map and the workspace."""
-    _check(x.dtype in (torch.float16, torch.bfloat16) and x.dim() == 2,
-           "x must be fp16/bf16 (T, H)")
+    if x.dtype not in (torch.float16, torch.bfloat16) or x.dim() != 2:
+        _fail("x must be fp16/bf16 (T, H)")
     T, H = x.shape
     frag = w13.dim() == 4
-    _check(w2.dim() == w13.dim(), "w13 and w2 must share a layout")
+    if w2.dim() != w13.dim():
+        _fail("w13 and w2 must share a layout")
     if frag:
-        _check(w13.shape[2] == 17 and w2.shape[2] == 17 and w13.shape[3] % 16 == 0,
-               "fragment-layout weights must be (E, N/16, 17, 16 K/128)")
+        if w13.shape[2] != 17 or w2.shape[2] != 17 or w13.shape[3] % 16 != 0:
+            _fail("fragment-layout weights must be (E, N/16, 17, 16 K/128)")
         E, nt13 = w13.shape[:2]
         g13 = w13.shape[3] // 16
-        _check(nt13 % 2 == 0, "w13 fragments must hold 2*inter rows")
+        if nt13 % 2 != 0:
+            _fail("w13 fragments must hold 2*inter rows")
         inter = nt13 * 8
-        _check(g13 * 128 == H, f"w13 fragments must cover K = H = {H}")
-        _check(tuple(w2.shape) == (E, H // 16, 17, 16 * (inter // 128)),
-               f"w2 fragments must be (E, H/16, 17, 16 inter/128)="
-               f"({E},{H // 16},17,{16 * (inter // 128)})")
-        _check(not weight_is_e2m1, "fragment layout holds int4 weights only")
+        if g13 * 128 != H:
+            _fail(f"w13 fragments must cover K = H = {H}")
+        if tuple(w2.shape) != (E, H // 16, 17, 16 * (inter // 128)):
+            _fail(f"w2 fragments must be (E, H/16, 17, 16 inter/128)="
+                  f"({E},{H // 16},17,{16 * (inter // 128)})")
+        if weight_is_e2m1:
+            _fail("fragment layout holds int4 weights only")
     else:
-        _check(w13.dim() == 3, "w13 must be (E, 2*inter, H/8) int32")
+        if w13.dim() != 3:
+            _fail("w13 must be (E, 2*inter, H/8) int32")
         E, I2, kw = w13.shape
-        _check(kw * 8 == H and I2 % 2 == 0, f"w13 must be (E, 2*inter, H/8) with H={H}")
+        if kw * 8 != H or I2 % 2 != 0:
+            _fail(f"w13 must be (E, 2*inter, H/8) with H={H}")
         inter = I2 // 2
-        _check(tuple(w2.shape) == (E, H, inter // 8),
-               f"w2 must be (E, H, inter/8)=({E},{H},{inter // 8})")
-    _check(w13.dtype == torch.int32 and w2.dtype == torch.int32, "weights must be int32")
-    _check(w13_s.dtype == torch.float16 and w2_s.dtype == torch.float16, "scales must be fp16")
-    _check(w13_s.dim() == 3 and tuple(w13_s.shape[:2]) == (E, 2 * inter) and w13_s.shape[2] > 0
-           and H % w13_s.shape[2] == 0, f"w13 scales must be (E, 2*inter, H/group)")
+        if tuple(w2.shape) != (E, H, inter // 8):
+            _fail(f"w2 must be (E, H, inter/8)=({E},{H},{inter // 8})")
+    if w13.dtype != torch.int32 or w2.dtype != torch.int32:
+        _fail("weights must be int32")
+    if w13_s.dtype != torch.float16 or w2_s.dtype != torch.float16:
+        _fail("scales must be fp16")
+    if not (w13_s.dim() == 3 and tuple(w13_s.shape[:2]) == (E, 2 * inter) and w13_s.shape[2] > 0
+            and H % w13_s.shape[2] == 0):
+        _fail("w13 scales must be (E, 2*inter, H/group)")
     gs = H // w13_s.shape[2]
-    _check(inter % gs == 0 and tuple(w2_s.shape) == (E, H, inter // gs),
-           f"w2 scales must be (E, H, inter/group)=({E},{H},{inter // gs})")
-    for t in (w13, w2, w13_s, w2_s):
-        _check(t.is_contiguous(), "weights/scales must be contiguous")
+    if inter % gs != 0 or tuple(w2_s.shape) != (E, H, inter // gs):
+        _fail(f"w2 scales must be (E, H, inter/group)=({E},{H},{inter // gs})")
+    if not (w13.is_contiguous() and w2.is_contiguous() and w13_s.is_contiguous()
+            and w2_s.is_contiguous()):
+        _fail("weights/scales must be contiguous")
     z13 = _zeros_of(w13_z, E, 2 * inter, H // gs, "w13 zeros")
     z2 = _zeros_of(w2_z, E, H, inter // gs, "w2 zeros")
-    _check(topk_ids.dim() == 2 and topk_ids.shape[0] == T, f"topk_ids must be (T, top_k) with T={T}")
+    if topk_ids.dim() != 2 or topk_ids.shape[0] != T:
+        _fail(f"topk_ids must be (T, top_k) with T={T}")
     top_k = topk_ids.shape[1]
-    _check(topk_weights.numel() == T * top_k, f"topk_weights must have T*top_k={T * top_k} entries")
+    if topk_weights.numel() != T * top_k:
+        _fail(f"topk_weights must have T*top_k={T * top_k} entries")
     emap = None
     if expert_map is not None:
-        _check(expert_map.dim() == 1, "expert_map must be 1-d (global_num_experts,)")
+        if expert_map.dim() != 1:
+            _fail("expert_map must be 1-d (global_num_experts,)")
         emap = expert_map.to(torch.int32).contiguous()
         n_global = emap.numel() if global_num_experts is None else int(global_num_experts)
-        _check(n_global == emap.numel(),
-               f"expert_map must have global_num_experts={n_global} entries")
+        if n_global != emap.numel():
+            _fail(f"expert_map must have global_num_experts={n_global} entries")
     else:
         n_global = E if global_num_experts is None else int(global_num_experts)
-        _check(n_global == E, "global_num_experts differs from the local expert count; "
-                              "pass expert_map")
-    tensors = [x, w13, w2, w13_s, w2_s, topk_weights, topk_ids]
-    tensors += [t for t in (z13, z2, emap) if t is not None]
-    _check(all(t.is_cuda and t.device == x.device for t in tensors),
-           "all tensors must be CUDA tensors on x's device")
-    ws = _workspace(lib.w4a8_moe_apply_workspace_size(T, H, inter, E, top_k), x.device)
+        if n_global != E:
+            _fail("global_num_experts differs from the local expert count; pass expert_map")
+    dev = x.device
+    for t in (x, w13, w2, w13_s, w2_s, topk_weights, topk_ids, z13, z2, emap):
+        if t is not None and (not t.is_cuda or t.device != dev):
+            _fail("all tensors must be CUDA tensors on x's device")
+    ws = _workspace(lib.w4a8_moe_apply_workspace_size(T, H, inter, E, top_k), dev)
     return T, H, inter, E, gs, top_k, frag, z13, z2, emap, n_global, ws
 
 
