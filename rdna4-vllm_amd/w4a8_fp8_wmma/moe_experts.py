@@ -5,12 +5,15 @@ Call surface of w4a8_fp8_wmma/w4a8_fp8_wmma/moe_experts.py in patcarter883/rdna4
     (moe_experts.py:493-665): an (M, K) output in ``out_dtype``, top-k weighted and reduced;
   * ``_awq_moe_to_op_layout`` / ``_ct_moe_to_op_layout`` / ``_wna16_moe_to_op_layout`` turn the
     on-disk formats into the op layout (:331-482);
-  * ``register_moe_wna16`` patches ``MoeWNA16Method`` (:1253-1341) when vLLM is present.
+  * ``register_moe_wna16`` patches ``MoeWNA16Method`` (:1253-1341) when vLLM is present;
+  * ``register_moe_mxfp4`` patches ``GptOssMxfp4MoEMethod`` (:1351-1450): E2M1 weights,
+    E8M0 scales converted to fp16 at load, biases and the swigluoai activation.
 
 On MI355X the SiLU-gated layer is one C-ABI call (``moe_apply``): align, act-quant,
-gemm1+SiLU, act-quant, gemm2 and the weighted reduce all run on the GPU. The load hook
-repacks the int4 weights once into the fragment layout the gfx950 kernels stream, in place
-of the u8 parameters (no second copy). There is no crossover gate and no stock fallback.
+gemm1+SiLU, act-quant, gemm2 and the weighted reduce all run on the GPU. The WNA16 load hook
+repacks the int4 weights once into the fragment layout the gfx950 kernels stream (weights
+and each tile's scale / zero-point words), which replaces the u8 parameters' data. There is
+no crossover gate and no stock fallback.
 """
 from __future__ import annotations
 
