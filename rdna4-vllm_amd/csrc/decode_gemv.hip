@@ -19,7 +19,9 @@
 //   * a team walks its range expert by expert and pass by pass; at a pass start it loads the
 //     activation rows (gemm1: x rows of the slots' tokens, fp16 or bf16; gemm2: the slots'
 //     h rows) and quantises them in registers, bit-identical to act_quant_kernel; the weight
-//     loads run three or four chunks ahead of the MFMAs across expert and pass boundaries;
+//     loads run three or four chunks ahead of the MFMAs across expert and pass boundaries,
+//     each fragment's weight blocks and its row's scale / zero-point words (adjacent in the
+//     16-row tile, repack.hip) loaded side by side;
 //   * outputs are per slot: gemm1 writes h (numel, I) fp16 after SiLU*mul, gemm2 writes
 //     y (numel, H) fp32, which the slot reduce sums in j order.
 #include <algorithm>

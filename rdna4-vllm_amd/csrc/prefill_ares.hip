@@ -22,15 +22,16 @@
 //     (n * 2^-9, two ANDs and a shift) with the operands swapped, so lane (q, c16) holds
 //     tile row c16, columns 4q..4q+3; then the fp32 scale fold run += acc * scale[n, g]
 //     (moe_gemm_tiled.h:144-151) with the lane's four scales read from a per-wave LDS table;
-//   * the range's scales and zero-points are fetched one range ahead into registers; at a
-//     range boundary each wave writes the scale table and s*z (bf16 hi/lo) for its own 32
+//   * the range's scales and zero-points are fetched one range ahead into registers (on
+//     fragment weights: the rows' metadata words stored after each 16-row tile's blocks); at
+//     a range boundary each wave writes the scale table and s*z (bf16 hi/lo) for its own 32
 //     weight rows, so no work-group barrier follows the prologue. The tables hold 16 K
 //     groups; for K > 2048 they are rebuilt in the middle of each range, after the first
 //     half's zero-point term;
 //   * after the last group of a range the zero-point term sum_g sum_k a * z * s is formed by
-//     bf16 MFMAs over (row group sums) x (s*z), out = asc * (512 * run - term) is stored as
-//     8-byte row pieces (fp16, or fp16 SiLU(gate) * up, bit-identical to silu_and_mul) and
-//     the accumulators restart;
+//     bf16 MFMAs over (row group sums) x (s*z), out = asc * (512 * run - term) is stored
+//     (fp16 rows as one 16-byte piece per lane after a lane-row swap; fp16 SiLU(gate) * up,
+//     bit-identical to silu_and_mul, as 8-byte pieces) and the accumulators restart;
 //   * the two waves of a SIMD take turns at the higher issue priority, one range each, so
 //     neither ends a tile far behind the other;
 //   * the main loop is instantiated per live 16-row fragment count (1..4), so partial tiles
