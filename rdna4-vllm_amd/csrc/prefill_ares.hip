@@ -583,10 +583,16 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
         // Range output: out = asc * (512 * run - zero term), stored.
         auto store_range = [&](int r) __attribute__((always_inline)) {
             const int64_t ldo = kSilu ? ncols : p.N;
-            __half* outp = reinterpret_cast<__half*>(p.out) + ar_col<kSilu>(r, wave, 0, 0) + 4 * q;
+            // a wave-uniform base and 32-bit lane offsets recomputed here from an opaque lane
+            // id (m * ldo < 2^31): hoisted out of the range loop, the per-fragment 64-bit row
+            // addresses stayed live across the main loop
+            __half* outb = reinterpret_cast<__half*>(p.out) + row0 * ldo + ar_col<kSilu>(r, wave, 0, 0);
+            const int ln = lane_now();
+            const int c16n = ln & 15;
+            const uint32_t qoff = 4u * (uint32_t)(ln >> 4);
 #pragma unroll
             for (int i = 0; i < NF; ++i) {
-                const int m = 16 * i + c16;
+                const int m = 16 * i + c16n;
                 const float av = s_asc[m];
                 float va[4], vb[4];
 #pragma unroll
@@ -594,7 +600,7 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
                     va[rr] = as_f32(av * (kNibbleScale * run[i][0][rr] - za[i][rr]));
                     vb[rr] = as_f32(av * (kNibbleScale * run[i][1][rr] - zb[i][rr]));
                 }
-                __half* rowp = outp + (row0 + m) * ldo;
+                __half* rowp = outb + ((uint32_t)m * (uint32_t)ldo + qoff);
                 const bool live = (vmask >> m) & 1;
                 if constexpr (kSilu) {
                     const __half2 h01 = __halves2half2(silu_mul_tile(va[0], vb[0]), silu_mul_tile(va[1], vb[1]));
