@@ -109,12 +109,6 @@ __device__ __forceinline__ int ar_row(int r, int w, int j, int c, int ncols) {
     return ar_col<kSilu>(r, w, j, c) + (kSilu && j == 1 ? ncols : 0);
 }
 
-// SiLU(gate) * up on the fp16 gate/up values: the same silu_mul_h (expf and an IEEE
-// division, moe_kernel.hip:555-561) as silu_and_mul_kernel, so the fused epilogue is
-// bit-identical to gemm1 followed by silu_and_mul.
-__device__ __forceinline__ __half silu_mul_tile(float gate, float up) {
-    return silu_mul_h(__float2half(gate), __float2half(up));
-}
 
 using bf16x8 = __bf16 __attribute__((ext_vector_type(8)));
 using lds_void_ptr = __attribute__((address_space(3))) void*;
@@ -603,8 +597,10 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
                 __half* rowp = outb + ((uint32_t)m * (uint32_t)ldo + qoff);
                 const bool live = (vmask >> m) & 1;
                 if constexpr (kSilu) {
-                    const __half2 h01 = __halves2half2(silu_mul_tile(va[0], vb[0]), silu_mul_tile(va[1], vb[1]));
-                    const __half2 h23 = __halves2half2(silu_mul_tile(va[2], vb[2]), silu_mul_tile(va[3], vb[3]));
+                    __half hv[4];
+                    silu_mul_h4(va, vb, hv);
+                    const __half2 h01 = __halves2half2(hv[0], hv[1]);
+                    const __half2 h23 = __halves2half2(hv[2], hv[3]);
                     if (live)
                         *reinterpret_cast<uint2*>(rowp) = make_uint2(__builtin_bit_cast(uint32_t, h01),
                                                                      __builtin_bit_cast(uint32_t, h23));

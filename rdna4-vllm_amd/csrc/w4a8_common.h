@@ -231,11 +231,63 @@ __device__ __forceinline__ float as_f32(float x) {
     return x;
 }
 
+// SiLU of an fp16 value, rounded to fp16: the bits of __float2half(g / (1.0f + expf(-g)))
+// (vLLM silu_kernel<half>; moe_kernel.hip:549-561). Since g is one of 65536 fp16 values this
+// is a fixed table, and a cheaper evaluation only has to land on the same fp16 values. Here
+// 2^(-g log2 e) comes from the hardware exp2, with log2 e split so that g * kSiluL2eHi is
+// exact (g has 11 significant bits, kSiluL2eHi 13), and the division from the hardware
+// reciprocal. Over all fp16 inputs whose SiLU is a normal fp16 number this fp32 value lies
+// within 5 fp32 ulps of the exact form's (measured over every input), so it rounds to the
+// same fp16 unless it lies within a few ulps of an fp16 rounding midpoint: values within
+// kSiluGuard ulps of one (0.13% of the inputs), results below the fp16 normal range (where
+// the hardware operations flush denormals) and non-finite inputs take the exact form. The
+// tests check every input against a table of the exact form.
+constexpr float kSiluL2eHi = 1.442626953125f;                 // 5909 / 4096 (0x3FB8A800)
+constexpr float kSiluL2eLo = 1.44269504088896340736f - 1.442626953125f;
+constexpr uint32_t kSiluGuard = 8;                            // fp32 ulps around a midpoint
+// The fast form's fp32 SiLU of g (an fp16 value); ok: it rounds to the exact form's fp16.
+__device__ __forceinline__ float silu_fast_f32(float g, bool& ok) {
+    const float d = fmaf(__builtin_amdgcn_exp2f(g * -kSiluL2eHi),
+                         __builtin_amdgcn_exp2f(g * -kSiluL2eLo), 1.0f);
+    const float r = g * __builtin_amdgcn_rcpf(d);
+    const uint32_t a = __float_as_uint(r) & 0x7FFFFFFFu;
+    // fp16 keeps 10 of the 23 fraction bits: the midpoint between two fp16 neighbours has
+    // low 13 bits 0x1000
+    const uint32_t mid = (a & 0x1FFFu) - (0x1000u - kSiluGuard);   // <= 2 * guard: near it
+    ok = a >= 0x38800000u && a < 0x7F800000u && mid > 2u * kSiluGuard;
+    return r;
+}
+__device__ __forceinline__ float silu_exact_f32(float g) { return g / (1.0f + expf(-g)); }
+
+__device__ __forceinline__ __half silu_h(__half gate_h) {
+    const float g = __half2float(gate_h);
+    bool ok;
+    const float r = silu_fast_f32(g, ok);
+    return __float2half(__builtin_expect(ok, 1) ? r : silu_exact_f32(g));
+}
+
 // vLLM silu_and_mul on fp16 gate/up stores (moe_kernel.hip:555-561).
 __device__ __forceinline__ __half silu_mul_h(__half gate_h, __half up_h) {
-    const float g = __half2float(gate_h);
-    const __half silu_h = __float2half(g / (1.0f + expf(-g)));
-    return __hmul(silu_h, up_h);
+    return __hmul(silu_h(gate_h), up_h);
+}
+
+// silu_mul_h of four (gate, up) pairs given as fp32 values (each rounded to fp16 first): the
+// fast form of all four first, so that their chains interleave, then the exact form of those
+// it does not cover (each a branch that the wave skips unless one of its lanes needs it).
+__device__ __forceinline__ void silu_mul_h4(const float (&gate)[4], const float (&up)[4],
+                                            __half (&out)[4]) {
+    float g[4], r[4];
+    bool ok[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        g[k] = __half2float(__float2half(gate[k]));
+        r[k] = silu_fast_f32(g[k], ok[k]);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        if (__builtin_expect(!ok[k], 0)) r[k] = silu_exact_f32(g[k]);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) out[k] = __hmul(__float2half(r[k]), __float2half(up[k]));
 }
 
 }  // namespace w4a8

@@ -3,6 +3,8 @@
 Bars: bit-exact for act-quant bytes/scales, dequant bytes, align indices and router ids;
 max|out - ref| / max|ref| <= 1e-2 for fp32-accumulated GEMM outputs.
 """
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -87,6 +89,30 @@ def test_dequant_e2m1_bit_exact():
     w = r.integers(-2**31, 2**31, (2, 16, 32), dtype=np.int64).astype(np.int32)
     got = W.dequant_fp8(torch.from_numpy(w).to(DEV), 32, None, weight_is_e2m1=True)
     assert np.array_equal(got.cpu().numpy(), O.dequant_codes(w, None, 32, e2m1=True))
+
+
+def test_silu_every_fp16_input_bit_exact_to_exact_form():
+    """SiLU(gate) * 1 for all 65536 fp16 gates == the exact form's table bit for bit
+    (tests/golden/silu_fp16_exhaustive.npy: fp16(g / (1 + expf(-g))), device expf, IEEE
+    division). The library evaluates SiLU with the hardware exp2 and reciprocal and falls back
+    to the exact form only for results below the fp16 normal range and non-finite inputs, so
+    this covers every input of every SiLU epilogue (they share silu_mul_h)."""
+    table = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
+                                 "silu_fp16_exhaustive.npy"))
+    gate = np.arange(65536, dtype=np.uint32).astype(np.uint16).view(np.float16).reshape(256, 256)
+    out = torch.empty((256, 256), dtype=torch.float16, device=DEV)
+    W.silu_and_mul(out, torch.from_numpy(np.concatenate([gate, np.ones_like(gate)], 1)).to(DEV))
+    got = out.cpu().numpy().view(np.uint16).reshape(-1)
+    bad = np.nonzero(got != table)[0]
+    assert len(bad) == 0, f"{len(bad)} inputs differ, first gates {gate.reshape(-1)[bad[:8]]}"
+    # the up factor multiplies the fp16 SiLU once more (hmul): up = -2 negates and doubles
+    W.silu_and_mul(out, torch.from_numpy(np.concatenate(
+        [gate, np.full_like(gate, -2.0)], 1)).to(DEV))
+    ref = (table.view(np.float16).astype(np.float32) * np.float32(-2.0)).astype(np.float16)
+    got2 = out.cpu().numpy().reshape(-1)
+    num = ~np.isnan(ref)
+    assert np.array_equal(got2[num].view(np.uint16), ref[num].view(np.uint16))
+    assert np.all(np.isnan(got2[~num]))
 
 
 def test_silu_and_mul_close():

@@ -1,9 +1,13 @@
 """Pin the oracle's numeric primitives against libraries and closed forms (CPU)."""
+import os
+
 import numpy as np
 import pytest
 import torch
 
 import oracle as O
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 
 
 def torch_e4m3(x: np.ndarray) -> np.ndarray:
@@ -117,6 +121,26 @@ def test_silu_and_mul_against_torch():
     ref = silu * u.astype(np.float64)
     # two fp16 roundings: |err| <= 2^-10 |ref| + fp16 subnormal step
     assert np.all(np.abs(got - ref) <= np.abs(ref) * 2.0 ** -10 * 1.01 + 2.0 ** -24 * 4)
+
+
+def test_silu_exhaustive_table_against_oracle():
+    """tests/golden/silu_fp16_exhaustive.npy holds fp16(g / (1 + expf(-g))) for every fp16 g,
+    evaluated on the GPU with the device expf and an IEEE division (make_silu_exhaustive.py).
+    Against the oracle's numpy form it agrees everywhere (NaN bits included) except where
+    expf and numpy's exp round differently and the fp32 quotient sits next to an fp16 rounding
+    midpoint: three inputs, one fp16 ulp each. The GPU suite holds every SiLU in the library
+    to this table."""
+    table = np.load(os.path.join(GOLDEN, "silu_fp16_exhaustive.npy"))
+    assert table.dtype == np.uint16 and table.shape == (65536,)
+    g = np.arange(65536, dtype=np.uint32).astype(np.uint16).view(np.float16)
+    with np.errstate(over="ignore", invalid="ignore"):
+        ref = O.silu_and_mul(g, np.ones_like(g)).view(np.uint16)
+    diff = np.nonzero(table != ref)[0]
+    assert len(diff) <= 3
+    assert np.all(np.abs(table[diff].astype(np.int32) - ref[diff].astype(np.int32)) == 1)
+    # SiLU(+0) = +0, SiLU(-0) = -0, SiLU(+inf) = +inf, SiLU(-inf) = NaN
+    assert table[0x0000] == 0x0000 and table[0x8000] == 0x8000
+    assert table[0x7C00] == 0x7C00 and np.isnan(table[0xFC00:0xFC01].view(np.float16))[0]
 
 
 def test_topk_softmax_bruteforce_and_ties():
