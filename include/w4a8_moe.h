@@ -319,6 +319,15 @@ W4A8_API int w4a8_moe_apply_set_stage_events(void* const* events, int count);
  * Process-wide. No reference counterpart (the reference runs separate launches). */
 W4A8_API int w4a8_set_decode_fused(int on);
 
+/* Prefill pair switch: on != 0 (the default; W4A8_PREFILL_PAIR=0 in the environment, read
+ * once, turns it off) lets the many-token schedule run gemm1+SiLU and gemm2 of the
+ * activation-resident tiles as one launch where both apply (hidden size <= 2048,
+ * intermediate size <= 1024): each work-group takes a 64-row tile through gemm1, then through
+ * gemm2 on the h rows it has just written. Results are the same bits as the two launches.
+ * Returns the previous setting. Process-wide. No reference counterpart (the reference runs
+ * separate launches). */
+W4A8_API int w4a8_set_prefill_pair(int on);
+
 /* Test hook of the fused decode layer: while on != 0 (a device-side word of the current
  * device, so captured graphs see it between replays), its in-kernel waits wait for a flag
  * value no work-group publishes, with a short spin limit, so they give up and the call's

@@ -261,6 +261,22 @@ bool decode_fused_enabled() {
     return v == 1;
 }
 
+// gemm1+SiLU and gemm2 of the activation-resident prefill tiles as one launch
+// (prefill_ares_pair_kernel) where both tiles apply; W4A8_PREFILL_PAIR=0 in the environment
+// (read once per process) or w4a8_set_prefill_pair(0) keeps two launches.
+std::atomic<int> g_prefill_pair{-1};   // -1: not read yet
+bool prefill_pair_enabled() {
+    int v = g_prefill_pair.load(std::memory_order_relaxed);
+    if (v < 0) {
+        const char* e = std::getenv("W4A8_PREFILL_PAIR");
+        int want = (e != nullptr && e[0] == '0') ? 0 : 1;
+        int expected = -1;
+        g_prefill_pair.compare_exchange_strong(expected, want, std::memory_order_relaxed);
+        v = g_prefill_pair.load(std::memory_order_relaxed);
+    }
+    return v == 1;
+}
+
 constexpr int kStageEvents = 8;
 constexpr int kStampEvents = 4;   // optional: kernel-exact start / stop of gemm1 and gemm2
 thread_local hipEvent_t g_stage_events[kStageEvents + kStampEvents];
@@ -458,18 +474,8 @@ int moe_apply_impl(const void* x, int x_dtype, int64_t T, int64_t H, int64_t int
     g1.epi = Epi::kSiluHalf; g1.out = h; g1.out_top_k = top_k; g1.x_fp8 = xq; g1.act_scales = s1;
     g1.act_group_sums = pf1 ? gs1 : nullptr;
     g1.w_frag = frag;
-    int rc;
-    stamp_gemm(0);
-    if (!mfma) rc = launch_grouped_scalar(g1, s);
-    else if (pl.decode && !e2m1 && gemv_supported(H, group_size)) rc = launch_grouped_gemv(g1, s);
-    else if (pf1 && prefill_ares_supported(H, 2 * inter, group_size, e2m1, pl.block_m, Epi::kSiluHalf) &&
-             T * H < kAresMaxElems)
-        rc = launch_grouped_prefill_ares(g1, s);
-    else if (pf1) rc = launch_grouped_prefill(g1, s);
-    else rc = launch_grouped_mfma(g1, s);
-    stamp_gemm(-1);
-    if (rc) return rc;
-    stage_mark(4, s);
+    const bool ares1 = pf1 && prefill_ares_supported(H, 2 * inter, group_size, e2m1, pl.block_m,
+                                                     Epi::kSiluHalf) && T * H < kAresMaxElems;
     // act-quant of h over real rows only, once per row (quantising inside the decode GEMV
     // would repeat it for every work-group that reads the row); the activation-resident
     // prefill tiles quantise their own rows instead (a tile is the only reader of its rows)
@@ -477,10 +483,6 @@ int moe_apply_impl(const void* x, int x_dtype, int64_t T, int64_t H, int64_t int
     const bool ares2 = pf2 && prefill_ares_supported(inter, H, group_size, e2m1, pl.block_m, Epi::kHalf) &&
                        pl.P * inter < kAresMaxElems;
     const bool ares2_quant = ares2 && prefill_ares_quantises_rows(inter, Epi::kHalf);
-    if (!ares2_quant && (rc = launch_act_quant(h, false, pl.P, inter, hq, s2, k8, s, sti, ntp,
-                                               numel, pf2 ? gs2 : nullptr)))
-        return rc;
-    stage_mark(5, s);
     // gemm2 (identity gather) -> per-slot rows (decode) or scatter (prefill)
     GroupedArgs g2{};
     g2.x_rows = pl.P; g2.K = inter; g2.w = w2; g2.scales = static_cast<const uint16_t*>(w2_scales_f16);
@@ -494,6 +496,33 @@ int moe_apply_impl(const void* x, int x_dtype, int64_t T, int64_t H, int64_t int
     g2.act_scales = ares2_quant ? nullptr : s2;
     g2.act_group_sums = pf2 && !ares2_quant ? gs2 : nullptr;
     g2.w_frag = frag;
+    int rc;
+    if (ares1 && ares2_quant && prefill_pair_enabled() && prefill_ares_pair_supported(g1, g2)) {
+        // both GEMMs in one launch, each work-group taking a tile through gemm1 and gemm2
+        stamp_gemm(0);
+        rc = launch_grouped_prefill_ares_pair(g1, g2, s);
+        stamp_gemm(-1);
+        if (rc) return rc;
+        stage_mark(4, s);
+        stage_mark(5, s);
+        stage_mark(6, s);
+        rc = launch_row_reduce(y, s2r, topk_weights, T, H, top_k, out, bf16, s);
+        stage_mark(7, s);
+        return rc;
+    }
+    stamp_gemm(0);
+    if (!mfma) rc = launch_grouped_scalar(g1, s);
+    else if (pl.decode && !e2m1 && gemv_supported(H, group_size)) rc = launch_grouped_gemv(g1, s);
+    else if (ares1) rc = launch_grouped_prefill_ares(g1, s);
+    else if (pf1) rc = launch_grouped_prefill(g1, s);
+    else rc = launch_grouped_mfma(g1, s);
+    stamp_gemm(-1);
+    if (rc) return rc;
+    stage_mark(4, s);
+    if (!ares2_quant && (rc = launch_act_quant(h, false, pl.P, inter, hq, s2, k8, s, sti, ntp,
+                                               numel, pf2 ? gs2 : nullptr)))
+        return rc;
+    stage_mark(5, s);
     stamp_gemm(1);
     if (!mfma) rc = launch_grouped_scalar(g2, s);
     else if (gemv2) rc = launch_grouped_gemv(g2, s);
@@ -883,6 +912,13 @@ int w4a8_set_decode_fused(int on) {
     clear_error();
     const int prev = decode_fused_enabled() ? 1 : 0;
     g_decode_fused.store(on != 0 ? 1 : 0, std::memory_order_relaxed);
+    return prev;
+}
+
+int w4a8_set_prefill_pair(int on) {
+    clear_error();
+    const int prev = prefill_pair_enabled() ? 1 : 0;
+    g_prefill_pair.store(on != 0 ? 1 : 0, std::memory_order_relaxed);
     return prev;
 }
 

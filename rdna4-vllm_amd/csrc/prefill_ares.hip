@@ -131,11 +131,13 @@ __device__ __forceinline__ uint32_t pack_bf16x2(__bf16 a, __bf16 b) {
     return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
 }
 
-// SQ: the tile quantises fp16 rows itself (fp16 output, K <= kArMaxKAq); otherwise it loads
-// prequantised rows. A compile-time choice: with both prologues in one kernel the compiler
-// kept the 16-chunk row staging array in scratch, each store waiting for its load.
+// One tile (BM sorted rows of one expert) over weight ranges [r_begin, r_end) by the whole
+// work-group; ntp: the live padded rows. SQ: the tile quantises fp16 rows itself (fp16
+// output, K <= kArMaxKAq); otherwise it loads prequantised rows. A compile-time choice: with
+// both prologues in one kernel the compiler kept the 16-chunk row staging array in scratch,
+// each store waiting for its load.
 template <Epi EPI, bool FRAG, int BM, bool SQ>
-__global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
+__device__ __forceinline__ void ar_tile(const Params& p, int ntp, int tile, int r_begin, int r_end) {
     constexpr bool kSilu = EPI == Epi::kSiluHalf;
     static_assert(!(SQ && kSilu), "gemm1 tiles take prequantised rows");
     constexpr int GPR = ar_gpr<BM>();
@@ -159,36 +161,7 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
     float* s_asc = reinterpret_cast<float*>(lds + L.total);           // [BM]
 
     const int ncols = kSilu ? p.N / 2 : p.N;
-    const int nranges = ncols / ar_range_cols<kSilu>();
 
-    // ---- piece of this work-group: XCD-aware order over the live tiles. XCD x (work-groups
-    //      b with b % 8 == x) owns a contiguous run of tiles and takes its work-groups in the
-    //      order b / 8. Whole tiles fill the XCD's slots in rounds; when the last round would
-    //      hold at most half the slots, its tiles are split into pieces of consecutive
-    //      ranges instead (each piece reloads the tile's rows), so that round ends after a
-    //      fraction of a tile. The results do not depend on the split. ----
-    const int ntp = p.ntp ? p.ntp[0] : (int)p.P;
-    const int64_t live_rows = std::min<int64_t>((int64_t)ntp, p.P);
-    const int ntiles = (int)((live_rows + BM - 1) / BM);
-    const int per_xcd = (ntiles + kArXcds - 1) / kArXcds;
-    const int b = blockIdx.x;
-    const int t0 = (b % kArXcds) * per_xcd;
-    const int jx = b / kArXcds;
-    const int nx = std::max(0, std::min(per_xcd, ntiles - t0));
-    const int slots = std::max(p.xcd_slots, 1);
-    const int tail = nx % slots;
-    const int split = tail > 0 && 2 * tail <= slots ? std::min(slots / tail, nranges) : 1;
-    const int whole = split > 1 ? nx - tail : nx;
-    int tile, r_begin = 0, r_end = nranges;
-    if (jx < whole) {
-        tile = t0 + jx;
-    } else {
-        const int i = jx - whole;
-        if (split == 1 || i >= tail * split) return;
-        tile = t0 + whole + i / split;
-        r_begin = (i % split) * nranges / split;
-        r_end = (i % split + 1) * nranges / split;
-    }
     const int64_t row0 = (int64_t)tile * BM;
     const int e = p.expert_ids ? p.expert_ids[row0 / p.block_m] : 0;
     if (e < 0 || e >= p.E) return;
@@ -701,6 +674,71 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
     }
 }
 
+// Live tiles of a launch, and the XCD-aware order over them: XCD x (work-groups b with
+// b % 8 == x) owns a contiguous run of per_xcd tiles and takes its work-groups in the order
+// b / 8.
+struct ArOrder {
+    int ntp, ntiles, per_xcd;
+    template <int BM>
+    __device__ static ArOrder of(const Params& p) {
+        ArOrder o;
+        o.ntp = p.ntp ? p.ntp[0] : (int)p.P;
+        const int64_t live_rows = std::min<int64_t>((int64_t)o.ntp, p.P);
+        o.ntiles = (int)((live_rows + BM - 1) / BM);
+        o.per_xcd = (o.ntiles + kArXcds - 1) / kArXcds;
+        return o;
+    }
+};
+
+// One GEMM. Whole tiles fill an XCD's slots in rounds; when the last round would hold at most
+// half the slots, its tiles are split into pieces of consecutive ranges instead (each piece
+// reloads the tile's rows), so that round ends after a fraction of a tile. The results do not
+// depend on the split.
+template <Epi EPI, bool FRAG, int BM, bool SQ>
+__global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
+    constexpr bool kSilu = EPI == Epi::kSiluHalf;
+    const int nranges = (kSilu ? p.N / 2 : p.N) / ar_range_cols<kSilu>();
+    const ArOrder o = ArOrder::of<BM>(p);
+    const int b = blockIdx.x;
+    const int t0 = (b % kArXcds) * o.per_xcd;
+    const int jx = b / kArXcds;
+    const int nx = std::max(0, std::min(o.per_xcd, o.ntiles - t0));
+    const int slots = std::max(p.xcd_slots, 1);
+    const int tail = nx % slots;
+    const int split = tail > 0 && 2 * tail <= slots ? std::min(slots / tail, nranges) : 1;
+    const int whole = split > 1 ? nx - tail : nx;
+    int tile, r_begin = 0, r_end = nranges;
+    if (jx < whole) {
+        tile = t0 + jx;
+    } else {
+        const int i = jx - whole;
+        if (split == 1 || i >= tail * split) return;
+        tile = t0 + whole + i / split;
+        r_begin = (i % split) * nranges / split;
+        r_end = (i % split + 1) * nranges / split;
+    }
+    ar_tile<EPI, FRAG, BM, SQ>(p, o.ntp, tile, r_begin, r_end);
+}
+
+// gemm1+SiLU and gemm2 of the same 64 sorted rows in one work-group, one tile after the
+// other: the tile's h rows (all its intermediate columns) are written by gemm1's epilogues
+// and read back, still in this XCD's L2, by gemm2's self-quantising prologue. Whole tiles
+// only (a gemm1 piece would leave its h rows to several work-groups).
+template <bool FRAG>
+__global__ void __launch_bounds__(kArThreads, 1) prefill_ares_pair_kernel(Params p1, Params p2) {
+    const ArOrder o = ArOrder::of<kArBM>(p1);
+    const int b = blockIdx.x;
+    const int jx = b / kArXcds;
+    const int tile = (b % kArXcds) * o.per_xcd + jx;
+    if (jx >= o.per_xcd || tile >= o.ntiles) return;
+    ar_tile<Epi::kSiluHalf, FRAG, kArBM, false>(p1, o.ntp, tile, 0, (p1.N / 2) / ar_range_cols<true>());
+    // every wave's h stores complete (and so visible to the work-group's loads, which share
+    // the CU's L1) before any wave reads h rows; also the LDS hand-over between the tiles
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    ar_tile<Epi::kHalf, FRAG, kArBM, true>(p2, o.ntp, tile, 0, p2.N / ar_range_cols<false>());
+}
+
 template <Epi EPI, bool FRAG, int BM, bool SQ>
 int launch_ares_bm(const Params& p, hipStream_t s) {
     const size_t lds = ar_lds_bytes<BM>(p.K);
@@ -732,7 +770,45 @@ int launch_ares_t(const Params& p, hipStream_t s) {
                           : launch_ares_bm<EPI, FRAG, kArBMWide, false>(p, s);  // two (K <= 4096)
 }
 
+template <bool FRAG>
+int launch_ares_pair_t(const Params& p1, const Params& p2, hipStream_t s) {
+    const size_t lds = std::max(ar_lds_bytes<kArBM>(p1.K), ar_lds_bytes<kArBM>(p2.K));
+    const void* fn = reinterpret_cast<const void*>(&prefill_ares_pair_kernel<FRAG>);
+    if (int rc = reserve_dyn_lds(fn, (int)ar_lds_bytes<kArBM>(kArMaxK), "prefill_ares_pair_kernel"))
+        return rc;
+    const int64_t tiles = (p1.P + kArBM - 1) / kArBM;
+    const unsigned grid = (unsigned)((tiles + kArXcds - 1) / kArXcds * kArXcds);
+    launch_kernel(&prefill_ares_pair_kernel<FRAG>, dim3(grid), dim3(kArThreads), lds, s, p1, p2);
+    return check_launch("prefill_ares_pair_kernel");
+}
+
 }  // namespace
+
+bool prefill_ares_pair_supported(const GroupedArgs& a1, const GroupedArgs& a2) {
+    return a1.epi == Epi::kSiluHalf && a2.epi == Epi::kHalf && a1.w_frag == a2.w_frag &&
+           a1.K <= kArMaxK && a2.K <= kArMaxKAq && a2.K == a1.N / 2 &&
+           prefill_ares_supported(a1.K, a1.N, a1.group_size, a1.e2m1, a1.block_m, a1.epi) &&
+           prefill_ares_supported(a2.K, a2.N, a2.group_size, a2.e2m1, a2.block_m, a2.epi) &&
+           a1.x_fp8 != nullptr && a1.act_scales != nullptr && a1.act_group_sums != nullptr &&
+           a2.x_fp8 == nullptr && a2.x == a1.out && !a2.x_bf16 && a2.identity_gather &&
+           a1.P == a2.P && a1.block_m == a2.block_m && a1.sorted_ids == a2.sorted_ids &&
+           a1.expert_ids == a2.expert_ids && a1.ntp == a2.ntp && a1.E == a2.E &&
+           a1.x_rows * a1.K < ((int64_t)1 << 31) && a2.x_rows * a2.K < ((int64_t)1 << 31) &&
+           (!a1.w_frag || ((a1.N / 2) % 16 == 0 && a2.N % 16 == 0));
+}
+
+int launch_grouped_prefill_ares_pair(const GroupedArgs& a1, const GroupedArgs& a2, hipStream_t s) {
+    if (!prefill_ares_pair_supported(a1, a2)) {
+        set_error("prefill (activation-resident pair): needs the gemm1+SiLU tile (K <= 2048, "
+                  "prequantised rows) and a self-quantising gemm2 tile (K <= 1024) on h, over the "
+                  "same sorted rows");
+        return W4A8_ERR_INVALID;
+    }
+    const Params p1 = make_params(a1);
+    if (p1.P == 0) return W4A8_OK;
+    const Params p2 = make_params(a2);
+    return a1.w_frag ? launch_ares_pair_t<true>(p1, p2, s) : launch_ares_pair_t<false>(p1, p2, s);
+}
 
 bool prefill_ares_supported(int64_t K, int64_t N, int64_t group_size, bool e2m1, int64_t block_m,
                             Epi epi) {

@@ -182,6 +182,11 @@ int launch_grouped_prefill_ares(const GroupedArgs& a, hipStream_t stream);
 // The activation-resident tiles can take fp16 rows (x, no x_fp8) and quantise them in their
 // prologue, bit-identical to act_quant_kernel with group sums (each tile owns its rows).
 bool prefill_ares_quantises_rows(int64_t K, Epi epi);
+// gemm1+SiLU and the self-quantising gemm2 of the same 64-row tiles in one launch (each
+// work-group runs a tile's gemm1, then its gemm2 on the h rows it just wrote).
+bool prefill_ares_pair_supported(const GroupedArgs& a1, const GroupedArgs& a2);
+int launch_grouped_prefill_ares_pair(const GroupedArgs& a1, const GroupedArgs& a2,
+                                     hipStream_t stream);
 // (E, N, K/8) int32 op layout -> fragment layout: per expert, 16-row tile t and 128-wide
 // group g, a 1 KB block whose 16-byte lane l holds row 16t + l % 16, k in
 // [128g + 32 (l / 16), +32) (the MFMA B operand of lane l). N % 16 == 0, K % 128 == 0.

@@ -23,6 +23,7 @@ from ._ops import (  # noqa: F401
     moe_forward,
     repack_fragments,
     set_decode_fused,
+    set_prefill_pair,
     silu_and_mul,
 )
 
@@ -124,5 +125,5 @@ __all__ = [
     "mmq_fp8_moe_gather_reduce", "act_quant_fp8", "dequant_fp8", "fragments_supported",
     "fused_topk",
     "moe_align_block_size", "moe_apply", "moe_forward", "repack_fragments", "set_decode_fused",
-    "silu_and_mul",
+    "set_prefill_pair", "silu_and_mul",
 ]

@@ -74,6 +74,7 @@ SIGNATURES = {
                                         _c_void_p, _c_void_p, _c_void_p, _int, _c_void_p, _i64,
                                         _c_void_p, _c_void_p, _c_void_p, _c_void_p]),
     "w4a8_set_decode_fused": (_int, [_int]),
+    "w4a8_set_prefill_pair": (_int, [_int]),
     "w4a8_decode_fused_test_fault": (_int, [_int]),
 }
 

@@ -551,6 +551,13 @@ def set_decode_fused(on: bool) -> bool:
     return bool(lib.w4a8_set_decode_fused(1 if on else 0))
 
 
+def set_prefill_pair(on: bool) -> bool:
+    """Runs gemm1+SiLU and gemm2 of the many-token schedule's activation-resident tiles as one
+    launch where both apply (on, the default unless W4A8_PREFILL_PAIR=0) or as two launches
+    (off); the results are the same bits. Returns the previous setting. Process-wide."""
+    return bool(lib.w4a8_set_prefill_pair(1 if on else 0))
+
+
 def _decode_fused_test_fault(on: bool) -> None:
     """Test hook: makes the fused decode layer's in-kernel waits give up (its output is then
     NaN), on the current device, until switched off."""

@@ -224,6 +224,35 @@ def test_prefill_layer_equals_op_composition(T, frag):
     assert torch.equal(fused, unfused)
 
 
+@pytest.mark.parametrize("T,frag,emap", [(160, False, False), (300, True, False),
+                                         (1024, True, True), (4096, True, False)])
+def test_prefill_pair_equals_two_launches(T, frag, emap):
+    """gemm1+SiLU and gemm2 of each 64-row tile in one work-group (prefill_ares_pair_kernel,
+    the default where both tiles apply) give the two launches' output bit for bit, with
+    partial tiles, an expert map that drops experts, and at the c4 size."""
+    cfg = dict(bench.CONFIGS["c4"])
+    cfg["T"] = T
+    ws = bench.make_weights(cfg, 470 + T, DEV)
+    x, logits = bench.make_inputs(cfg, 471 + T, DEV)
+    tw, ids = W.fused_topk(None, logits, cfg["k"], True)
+    w13, w2 = ws["w13"], ws["w2"]
+    if frag:
+        w13, w2 = W.repack_fragments(w13, ws["s13"], ws["z13"]), W.repack_fragments(w2, ws["s2"], ws["z2"])
+    em = None
+    if emap:   # the first 200 global experts map onto local experts 0..199, the rest dropped
+        em = torch.full((cfg["E"],), -1, dtype=torch.int32, device=DEV)
+        em[:200] = torch.arange(200, dtype=torch.int32, device=DEV)
+    prev = W.set_prefill_pair(True)
+    try:
+        a = W.moe_apply(x, w13, w2, ws["s13"], ws["s2"], ws["z13"], ws["z2"], tw, ids, expert_map=em)
+        W.set_prefill_pair(False)
+        b = W.moe_apply(x, w13, w2, ws["s13"], ws["s2"], ws["z13"], ws["z2"], tw, ids, expert_map=em)
+    finally:
+        W.set_prefill_pair(prev)
+    assert torch.isfinite(a.float()).all()
+    assert torch.equal(a, b)
+
+
 @pytest.mark.parametrize("H,T,frag", [(4096, 200, True), (3072, 130, False)])
 def test_prefill_wide_k_tiles(H, T, frag):
     """Hidden sizes above 2048 run gemm1 on the 32-row activation tiles, whose per-range
