@@ -253,6 +253,38 @@ def test_prefill_pair_equals_two_launches(T, frag, emap):
     assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("H,T,frag", [(2048, 300, True), (2048, 170, False), (4096, 260, True)])
+def test_prefill_intermediate_1536(H, T, frag):
+    """Intermediate size 1536 (as c5): gemm2 tiles take the rows act_quant_kernel quantised
+    (above the self-quantising tiles' K <= 1024), so the layer runs gemm1 and gemm2 as two
+    launches whatever the pair switch says; it equals the op-by-op composition bit for bit,
+    and the oracle agrees."""
+    cfg = dict(T=T, H=H, E=32, k=4, I=1536, g=128, routing="uniform")
+    ws = bench.make_weights(cfg, 650 + T, DEV)
+    x, logits = bench.make_inputs(cfg, 651 + T, DEV)
+    tw, ids = W.fused_topk(None, logits, cfg["k"], True)
+    w13, w2 = ws["w13"], ws["w2"]
+    if frag:
+        w13, w2 = W.repack_fragments(w13, ws["s13"], ws["z13"]), W.repack_fragments(w2, ws["s2"], ws["z2"])
+    prev = W.set_prefill_pair(True)
+    try:
+        out = W.moe_apply(x, w13, w2, ws["s13"], ws["s2"], ws["z13"], ws["z2"], tw, ids)
+        W.set_prefill_pair(False)
+        two = W.moe_apply(x, w13, w2, ws["s13"], ws["s2"], ws["z13"], ws["z2"], tw, ids)
+    finally:
+        W.set_prefill_pair(prev)
+    assert torch.equal(out, two)
+    unfused = moe_experts._run_unfused(
+        x.to(torch.float16), ws["w13"], ws["w2"], ws["s13"], ws["s2"], ws["z13"], ws["z2"],
+        tw.reshape(-1).contiguous(), ids, cfg["k"], cfg["E"], None, "wmma", False, None, None,
+        64).to(x.dtype)
+    assert torch.equal(out, unfused)
+    ref = oracle_layer(cfg, ws, x, tw, ids)
+    err = maxrel(out.float().cpu().numpy(), ref)
+    print(f"  H={H} T={T} frag={frag} max rel err {err:.2e}")
+    assert err <= REL_TOL
+
+
 @pytest.mark.parametrize("H,T,frag", [(4096, 200, True), (3072, 130, False)])
 def test_prefill_wide_k_tiles(H, T, frag):
     """Hidden sizes above 2048 run gemm1 on the 32-row activation tiles, whose per-range
