@@ -102,13 +102,35 @@ __device__ __forceinline__ void quantize_row_regs(const RowRegs& rr, int64_t row
     constexpr int kMaxPass = RowRegs::kMaxPass;
     const int npass = (K + 511) / 512;
     const uint4* v = rr.v;
-    float amax = 0.0f;
+    // absmax on the magnitude bits, two values per instruction (packed 16-bit max): the
+    // conversions to the fp16-rounded fp32 value are monotone in them. NaNs, which the fmaxf
+    // form below skips, lie above the infinity pattern; only a lane that holds one takes that
+    // exact form.
+    constexpr uint32_t nan_above = BF16 ? 0x7F80u : 0x7C00u;
+    using u16x2 = unsigned short __attribute__((ext_vector_type(2)));
+    u16x2 m2 = {0, 0};
 #pragma unroll
     for (int ps = 0; ps < kMaxPass; ++ps) {
         if (ps >= npass) break;
         if (ps * 512 + lane * 8 >= K) continue;
+        const uint32_t wd[4] = {v[ps].x, v[ps].y, v[ps].z, v[ps].w};
 #pragma unroll
-        for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(act_from_u4<BF16>(v[ps], j)));
+        for (int j = 0; j < 4; ++j)
+            m2 = __builtin_elementwise_max(m2, __builtin_bit_cast(u16x2, wd[j] & 0x7FFF7FFFu));
+    }
+    const uint32_t mbits = max((uint32_t)m2.x, (uint32_t)m2.y);
+    float amax;
+    if (__builtin_expect(mbits <= nan_above, 1)) {
+        amax = act_from_u4<BF16>(make_uint4(mbits, 0u, 0u, 0u), 0);
+    } else {
+        amax = 0.0f;
+#pragma unroll
+        for (int ps = 0; ps < kMaxPass; ++ps) {
+            if (ps >= npass) break;
+            if (ps * 512 + lane * 8 >= K) continue;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(act_from_u4<BF16>(v[ps], j)));
+        }
     }
     amax = wave_max(amax);
     const float s = act_scale_from_absmax(amax);

@@ -52,6 +52,36 @@ def test_act_quant_bit_exact(k8, K):
     assert np.array_equal(q.cpu().numpy(), qo)
 
 
+@pytest.mark.parametrize("K", [512, 2048, 4096])
+def test_act_quant_nan_and_inf_rows(K):
+    """The absmax skips NaNs (fmaxf, as the reference kernel) and takes infinities: rows with
+    NaNs get the scale of their finite values and the same bytes as the oracle at every
+    non-NaN position; a row holding an infinity gets an infinite scale. (The kernels find
+    the maximum on the magnitude bits and take an exact pass only for a row with a NaN.)"""
+    r = rng(K + 7)
+    x = (r.standard_normal((6, K)) * 5).astype(np.float16)
+    x[0, 3] = np.nan
+    x[1, K - 1] = np.nan
+    x[1, :K // 2] *= 40
+    x[2, ::5] = np.nan
+    x[3, 9] = np.inf
+    x[4, K // 3] = -np.inf
+    q, s = W.act_quant_fp8(torch.from_numpy(x).to(DEV), k8_interleave=False)
+    q, s = q.cpu().numpy(), s.cpu().numpy()
+    xf = x.astype(np.float32)
+    amax = np.nanmax(np.abs(xf), axis=1)
+    s_ref = np.maximum(amax / np.float32(448.0), np.float32(1e-8)).astype(np.float32)
+    assert np.array_equal(s, s_ref)
+    for row in range(3):   # NaN rows: finite scale, oracle bytes where the input is a number
+        finite = ~np.isnan(xf[row])
+        inv = np.float32(1.0) / s_ref[row]
+        ref = O.e4m3_encode((xf[row] * inv).astype(np.float32))
+        assert np.array_equal(q[row][finite], ref[finite])
+    assert np.isinf(s[3]) and np.isinf(s[4]) and np.isfinite(s[5])
+    qo, so = O.act_quant(x[5:6])
+    assert np.array_equal(q[5:6], qo) and np.array_equal(s[5:6], so)
+
+
 @pytest.mark.parametrize("K", [512, 2048])
 def test_act_quant_misaligned_rows_bit_exact(K):
     """Rows whose start is not 16-byte aligned take the element-wise loads: same bytes."""
