@@ -383,12 +383,17 @@ int moe_apply_impl(const void* x, int x_dtype, int64_t T, int64_t H, int64_t int
     // few tokens: the decode gemm1 launch routes them itself (no router launch)
     const bool route_in_gemm1 = logits != nullptr && frag_decode &&
                                 decode_routes_in_kernel(T, n_global, top_k);
+    // decode on fragment weights after a router launch: the routing waves quantise x as well,
+    // and the separate gemm1 launch reads those rows instead of quantising in registers at
+    // every pass start (the fused layer keeps its in-register quantisation)
+    const bool decode_preq = logits != nullptr && frag_decode && !route_in_gemm1 && k8 &&
+                             !(decode_fused_enabled() && decode_layer_fused_supported(H, inter));
     if (logits != nullptr && !route_in_gemm1)
         if (int rc = launch_topk_softmax(logits, T, n_global, top_k, renormalize,
                                          const_cast<float*>(topk_weights),
                                          const_cast<int32_t*>(topk_ids), s,
-                                         route_quant ? x : nullptr, bf16, H, xq, s1,
-                                         pf1 ? gs1 : nullptr))
+                                         route_quant || decode_preq ? x : nullptr, bf16, H, xq,
+                                         s1, pf1 ? gs1 : nullptr))
             return rc;
     stage_mark(0, s);
     if (frag_decode) {
@@ -411,6 +416,10 @@ int moe_apply_impl(const void* x, int x_dtype, int64_t T, int64_t H, int64_t int
             d.topk_ids_out = const_cast<int32_t*>(topk_ids);
         }
         d2.a = h; d2.a_bf16 = false; d2.silu = false;
+        if (decode_preq) {
+            d.aq = xq;
+            d.asc = s1;
+        }
         d2.w = w2; d2.scales = w2_scales_f16; d2.zeros = w2_zeros; d2.out = acc;
         d2.K = inter; d2.N = H;
         SlotReduceSync sync;

@@ -54,6 +54,10 @@ struct DecodeParams {
     const void* a;           // activation rows, fp16 / bf16
     int a_bf16;
     int a_per_token;         // 1: slot s reads row s / top_k (x); 0: row s (h)
+    // gemm1 only: the rows already quantised (k8-interleaved e4m3 (rows, K) and their scales,
+    // act_quant_kernel's bytes, written by the router launch); null: quantise a in registers
+    const uint8_t* aq;
+    const float* asc;
     const int32_t* w;        // fragment layout (E, N/16, 272 G): blocks, then scales/zeros
     void* out;               // kSiluHalf: (numel, N/2) fp16; kSlotF32: (numel, N) fp32
     int K, N, G;
@@ -318,9 +322,10 @@ __device__ __forceinline__ uint4 dec_row16(const uint16_t* base, int64_t elem) {
 // are on the critical path. The value is only kept alive (dec_keep), never used.
 __device__ __forceinline__ uint32_t dec_warm(const DecodeParams& p) {
     const int nrows = p.a_per_token ? p.numel / p.top_k : p.numel;
-    const int lines = (int)(((int64_t)nrows * p.K * 2 + 127) / 128);
+    const int lines = (int)(((int64_t)nrows * p.K * (p.aq ? 1 : 2) + 127) / 128);
     const int idx = ((int)(blockIdx.x / 8) * 4 + (int)(threadIdx.x >> 6)) * 64 + (int)(threadIdx.x & 63);
-    return lines > 0 ? reinterpret_cast<const uint32_t*>(p.a)[(int64_t)min(idx, lines - 1) * 32] : 0u;
+    const uint32_t* rows = p.aq ? reinterpret_cast<const uint32_t*>(p.aq) : reinterpret_cast<const uint32_t*>(p.a);
+    return lines > 0 ? rows[(int64_t)min(idx, lines - 1) * 32] : 0u;
 }
 // keeps the warm-up load (its value never matches: a NaN pattern in a block that does not exist)
 __device__ __forceinline__ void dec_keep(uint32_t warm, void* out) {
@@ -329,7 +334,9 @@ __device__ __forceinline__ void dec_keep(uint32_t warm, void* out) {
 
 // One GEMM of the layer over the lists L by the whole grid (the body of decode_gemv_kernel).
 // DEP: the activation rows are h written by the first GEMM of the same kernel (DecDep).
-template <Epi EPI, int GPW, int KSPLIT, bool ABF16, bool DEP>
+// PREQ: the rows come quantised (p.aq, p.asc); a pass start loads their e4m3 bytes straight
+// into the MFMA operand registers.
+template <Epi EPI, int GPW, int KSPLIT, bool ABF16, bool DEP, bool PREQ = false>
 __device__ __forceinline__ void dec_run(const DecodeParams& p, const DecodeLists& L,
                                         float (&s_amax)[4][16], v4f* s_part, const DecDep& dep) {
     using C = DecCfg<EPI, GPW, KSPLIT>;
@@ -376,7 +383,8 @@ __device__ __forceinline__ void dec_run(const DecodeParams& p, const DecodeLists
 
     uint4 wv[C::D][C::GC * C::FR];
     uint32_t mw[C::D][C::FR][C::GC];   // metadata words: fp16 scale | zero-point << 16
-    uint4 raw[GPW][4];
+    uint4 raw[PREQ ? 1 : GPW][4];
+    float rasc = 0.f;   // PREQ: the scale of this lane's row c16
     v8i af[GPW];
     v4f sa[GPW];   // 2^-9 * group sums of rows 4q .. 4q + 3 (zero-point term)
     v4f run[C::FR];
@@ -424,12 +432,25 @@ __device__ __forceinline__ void dec_run(const DecodeParams& p, const DecodeLists
         const int my_slot = L.slot[s0 + min(c16, mreal - 1)];
         const int arow = p.a_per_token ? my_slot / p.top_k : my_slot;
         const int64_t xr = (int64_t)arow * p.K + q * 32;
+        if constexpr (PREQ) {
+            // the 32 bytes of k in [128 g + 32 q, +32): the operand register order (k8
+            // interleave inside each 8-byte block, as the in-register quantisation packs it)
 #pragma unroll
-        for (int g = 0; g < GPW; ++g)
+            for (int g = 0; g < GPW; ++g) {
+                const uint4* src = reinterpret_cast<const uint4*>(p.aq + xr + (g0 + g) * kGroup);
+                const uint4 lo = src[0], hi = src[1];
+                af[g] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w,
+                            (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+            }
+            rasc = p.asc[arow];
+        } else {
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                raw[g][i] = dec_row16<DEP>(reinterpret_cast<const uint16_t*>(p.a),
-                                           xr + (g0 + g) * kGroup + i * 8);
+            for (int g = 0; g < GPW; ++g)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    raw[g][i] = dec_row16<DEP>(reinterpret_cast<const uint16_t*>(p.a),
+                                               xr + (g0 + g) * kGroup + i * 8);
+        }
     };
     // DEP: wait until every work-group of the first GEMM that wrote a unit of the touched
     // experts in this team's range has published its rows. Lane i polls work-group
@@ -461,68 +482,72 @@ __device__ __forceinline__ void dec_run(const DecodeParams& p, const DecodeLists
             if (__ballot(!ok) != 0 && lane == 0) dep.timeout[blockIdx.x] = dep.nonce;
         }
     };
-    // quantise the pass's rows, bit-identical to act_quant_kernel: absmax on the magnitude
+    // quantise the pass's rows (PREQ: they are quantised already; only the group sums and
+    // the output rows remain), bit-identical to act_quant_kernel: absmax on the magnitude
     // bits (both conversions are monotone in them; NaNs, which fmaxf skips, count as 0), then
     // over the row's four quarter-lanes and the team's K-split waves. Two values per
     // instruction (packed 16-bit max); a maximum above the infinity pattern means a NaN is
     // present, and only then the exact NaN-skipping pass runs.
     auto quantize = [&](const DecCursor& c) __attribute__((always_inline)) {
-        constexpr uint32_t nan_above = ABF16 ? 0x7F80u : 0x7C00u;
-        u16x2 m2 = {0, 0};
-#pragma unroll
-        for (int g = 0; g < GPW; ++g)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t wd[4] = {raw[g][i].x, raw[g][i].y, raw[g][i].z, raw[g][i].w};
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    m2 = __builtin_elementwise_max(m2, __builtin_bit_cast(u16x2, wd[j] & 0x7FFF7FFFu));
-            }
-        uint32_t mbits = max((uint32_t)m2.x, (uint32_t)m2.y);
-        if (mbits > nan_above) {
-            mbits = 0;
+        float my_asc = rasc;
+        if constexpr (!PREQ) {
+            constexpr uint32_t nan_above = ABF16 ? 0x7F80u : 0x7C00u;
+            u16x2 m2 = {0, 0};
 #pragma unroll
             for (int g = 0; g < GPW; ++g)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const uint32_t wd[4] = {raw[g][i].x, raw[g][i].y, raw[g][i].z, raw[g][i].w};
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const uint32_t lo = wd[j] & 0x7FFFu, hi = (wd[j] >> 16) & 0x7FFFu;
-                        mbits = max(mbits, lo > nan_above ? 0u : lo);
-                        mbits = max(mbits, hi > nan_above ? 0u : hi);
+                    for (int j = 0; j < 4; ++j)
+                        m2 = __builtin_elementwise_max(m2, __builtin_bit_cast(u16x2, wd[j] & 0x7FFF7FFFu));
+                }
+            uint32_t mbits = max((uint32_t)m2.x, (uint32_t)m2.y);
+            if (mbits > nan_above) {
+                mbits = 0;
+#pragma unroll
+                for (int g = 0; g < GPW; ++g)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const uint32_t wd[4] = {raw[g][i].x, raw[g][i].y, raw[g][i].z, raw[g][i].w};
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            const uint32_t lo = wd[j] & 0x7FFFu, hi = (wd[j] >> 16) & 0x7FFFu;
+                            mbits = max(mbits, lo > nan_above ? 0u : lo);
+                            mbits = max(mbits, hi > nan_above ? 0u : hi);
+                        }
                     }
-                }
-        }
-        float amax = dec_act_f32<ABF16>(mbits);
-        {
-            const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(amax), __float_as_uint(amax), false, false);
-            amax = fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
-            const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(amax), __float_as_uint(amax), false, false);
-            amax = fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
-        }
-        if constexpr (KSPLIT > 1) {
-            if (q == 0) s_amax[wave][c16] = amax;
-            lds_barrier();
-#pragma unroll
-            for (int j = 0; j < KSPLIT; ++j) amax = fmaxf(amax, s_amax[team * KSPLIT + j][c16]);
-        }
-        const float my_asc = act_scale_from_absmax(amax);
-        const float inv = 1.0f / my_asc;
-#pragma unroll
-        for (int g = 0; g < GPW; ++g)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {   // k8-interleaved bytes, as act_quant_kernel
-                const uint32_t wd[4] = {raw[g][i].x, raw[g][i].y, raw[g][i].z, raw[g][i].w};
-                float f[8];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    f[2 * j] = dec_act_f32<ABF16>(wd[j] & 0xFFFFu) * inv;
-                    f[2 * j + 1] = dec_act_f32<ABF16>(wd[j] >> 16) * inv;
-                }
-                af[g][2 * i] = (int)pack4_e4m3(f[0], f[2], f[4], f[6]);
-                af[g][2 * i + 1] = (int)pack4_e4m3(f[1], f[3], f[5], f[7]);
             }
+            float amax = dec_act_f32<ABF16>(mbits);
+            {
+                const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(amax), __float_as_uint(amax), false, false);
+                amax = fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+                const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(amax), __float_as_uint(amax), false, false);
+                amax = fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+            }
+            if constexpr (KSPLIT > 1) {
+                if (q == 0) s_amax[wave][c16] = amax;
+                lds_barrier();
+#pragma unroll
+                for (int j = 0; j < KSPLIT; ++j) amax = fmaxf(amax, s_amax[team * KSPLIT + j][c16]);
+            }
+            my_asc = act_scale_from_absmax(amax);
+            const float inv = 1.0f / my_asc;
+#pragma unroll
+            for (int g = 0; g < GPW; ++g)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {   // k8-interleaved bytes, as act_quant_kernel
+                    const uint32_t wd[4] = {raw[g][i].x, raw[g][i].y, raw[g][i].z, raw[g][i].w};
+                    float f[8];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        f[2 * j] = dec_act_f32<ABF16>(wd[j] & 0xFFFFu) * inv;
+                        f[2 * j + 1] = dec_act_f32<ABF16>(wd[j] >> 16) * inv;
+                    }
+                    af[g][2 * i] = (int)pack4_e4m3(f[0], f[2], f[4], f[6]);
+                    af[g][2 * i + 1] = (int)pack4_e4m3(f[1], f[3], f[5], f[7]);
+                }
+        }
 #pragma unroll
         for (int g = 0; g < GPW; ++g) {
             const int one = (int)kDecOnes;
@@ -711,7 +736,7 @@ __device__ __forceinline__ void dec_run(const DecodeParams& p, const DecodeLists
     }
 }
 
-template <Epi EPI, int GPW, int KSPLIT, bool ABF16>
+template <Epi EPI, int GPW, int KSPLIT, bool ABF16, bool PREQ>
 __global__ void __launch_bounds__(kDecThreads, 1) decode_gemv_kernel(DecodeParams p) {
     __shared__ DecodeLists L;
     __shared__ float s_amax[4][16];
@@ -724,7 +749,7 @@ __global__ void __launch_bounds__(kDecThreads, 1) decode_gemv_kernel(DecodeParam
         ids = s_ids;
     }
     build_lists(p, ids, L);
-    dec_run<EPI, GPW, KSPLIT, ABF16, false>(p, L, s_amax, reinterpret_cast<v4f*>(s_dyn), DecDep{});
+    dec_run<EPI, GPW, KSPLIT, ABF16, false, PREQ>(p, L, s_amax, reinterpret_cast<v4f*>(s_dyn), DecDep{});
     dec_keep(warm, p.out);
 }
 
@@ -786,22 +811,24 @@ DecSplit dec_split(int G) {
 // one four-wave work-group per CU (one wave per SIMD, up to 512 registers)
 int persistent_grid() { return device_cu_count(); }
 
-template <Epi EPI, int GPW, int KSPLIT, bool ABF16>
+template <Epi EPI, int GPW, int KSPLIT, bool ABF16, bool PREQ = false>
 int launch_dec_a(const DecodeParams& p, hipStream_t s) {
     using C = DecCfg<EPI, GPW, KSPLIT>;
     const size_t lds = C::LDS_BYTES;
-    auto* kern = &decode_gemv_kernel<EPI, GPW, KSPLIT, ABF16>;
+    auto* kern = &decode_gemv_kernel<EPI, GPW, KSPLIT, ABF16, PREQ>;
     if (int rc = reserve_dyn_lds(reinterpret_cast<const void*>(kern), (int)lds, "decode_gemv_kernel"))
         return rc;
     launch_kernel(kern, dim3(persistent_grid()), dim3(kDecThreads), lds, s, p);
     return check_launch("decode_gemv_kernel");
 }
 
-// gemm1 reads x (fp16 or bf16); gemm2 reads the fp16 h rows
+// gemm1 reads x (fp16 or bf16, or the router's quantised rows); gemm2 reads the fp16 h rows
 template <Epi EPI, int GPW, int KSPLIT>
 int launch_dec_t(const DecodeParams& p, hipStream_t s) {
-    if constexpr (EPI == Epi::kSiluHalf)
+    if constexpr (EPI == Epi::kSiluHalf) {
+        if (p.aq != nullptr) return launch_dec_a<EPI, GPW, KSPLIT, false, true>(p, s);
         if (p.a_bf16) return launch_dec_a<EPI, GPW, KSPLIT, true>(p, s);
+    }
     return launch_dec_a<EPI, GPW, KSPLIT, false>(p, s);
 }
 
@@ -902,6 +929,8 @@ DecodeParams dec_params(const DecodeLaunch& d) {
     p.E = (int)d.E;
     p.a = d.a;
     p.a_bf16 = d.a_bf16 ? 1 : 0;
+    p.aq = d.silu ? d.aq : nullptr;
+    p.asc = d.silu ? d.asc : nullptr;
     p.a_per_token = d.silu ? 1 : 0;
     p.w = d.w;
     p.out = d.out;

@@ -305,8 +305,9 @@ __device__ __forceinline__ void topk_one_token(const float* __restrict__ l, int 
     topk_select<NV>(v, E, top_k, renorm, tw, ids, ids_lds, lane);
 }
 
-// RowQuant: optional act-quant of the token's activation row by the same wave, after its
-// routing (act_quant_kernel's arithmetic; saves a launch for the many-token schedule).
+// RowQuant: optional act-quant of the tokens' activation rows in the same launch
+// (act_quant_kernel's arithmetic; saves a launch), by work-groups of their own beside the
+// selecting ones, so a few-token launch ends after the longer of the two chains, not their sum.
 struct RowQuant {
     const void* x = nullptr;   // (T, K) fp16 / bf16, or null: no quantisation
     bool bf16 = false;
@@ -321,26 +322,19 @@ __global__ void __launch_bounds__(256) topk_softmax_kernel(
     const float* __restrict__ logits, int64_t T, int E, int top_k, bool renorm,
     float* __restrict__ tw, int32_t* __restrict__ tids, RowQuant rq) {
     const int lane = threadIdx.x & 63;
+    const int64_t nsel = (T + 3) / 4;   // work-groups [0, nsel) select, the rest quantise
+    if ((int64_t)blockIdx.x >= nsel) {
+        const int64_t t = ((int64_t)blockIdx.x - nsel) * 4 + (threadIdx.x >> 6);
+        if (t >= T || rq.x == nullptr) return;
+        if (rq.bf16) quantize_row<true>(rq.x, t, rq.K, rq.xq, rq.xs, true, rq.gsum, lane);
+        else quantize_row<false>(rq.x, t, rq.K, rq.xq, rq.xs, true, rq.gsum, lane);
+        return;
+    }
     const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (t >= T) return;
     float v[NV];
     topk_load<NV>(logits + t * E, E, lane, v);
-    if (rq.x == nullptr) {
-        topk_select<NV>(v, E, top_k, renorm, tw + t * top_k, tids + t * top_k, nullptr, lane);
-        return;
-    }
-    // the row's loads go out behind the logits, so the selection runs while they arrive
-    RowRegs rr;
-    const bool in_regs = row_load(rq.x, t, rq.K, lane, rr);
     topk_select<NV>(v, E, top_k, renorm, tw + t * top_k, tids + t * top_k, nullptr, lane);
-    if (!in_regs) {
-        if (rq.bf16) quantize_row<true>(rq.x, t, rq.K, rq.xq, rq.xs, true, rq.gsum, lane);
-        else quantize_row<false>(rq.x, t, rq.K, rq.xq, rq.xs, true, rq.gsum, lane);
-    } else if (rq.bf16) {
-        quantize_row_regs<true>(rr, t, rq.K, rq.xq, rq.xs, true, rq.gsum, lane);
-    } else {
-        quantize_row_regs<false>(rr, t, rq.K, rq.xq, rq.xs, true, rq.gsum, lane);
-    }
 }
 
 // Decode prologue in one launch: work-group 0 builds the align layout (numel <= kChunk),
@@ -433,7 +427,7 @@ int launch_topk_softmax(const float* logits, int64_t T, int64_t E, int64_t top_k
         }
         rq.x = x; rq.bf16 = x_bf16; rq.K = (int)K; rq.xq = xq; rq.xs = xs; rq.gsum = gsum;
     }
-    const dim3 grid((unsigned)((T + 3) / 4));
+    const dim3 grid((unsigned)((T + 3) / 4 * (x != nullptr ? 2 : 1)));
     if (E <= 64) topk_softmax_kernel<1><<<grid, 256, 0, stream>>>(logits, T, (int)E, (int)top_k, renorm, w, ids, rq);
     else if (E <= 128) topk_softmax_kernel<2><<<grid, 256, 0, stream>>>(logits, T, (int)E, (int)top_k, renorm, w, ids, rq);
     else if (E <= 256) topk_softmax_kernel<4><<<grid, 256, 0, stream>>>(logits, T, (int)E, (int)top_k, renorm, w, ids, rq);

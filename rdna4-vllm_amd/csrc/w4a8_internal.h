@@ -221,6 +221,10 @@ struct DecodeLaunch {
     int64_t emap_len, numel, top_k, E;
     const void* a;
     bool a_bf16;
+    // gemm1 (silu) only: a's rows quantised already by the router launch (k8-interleaved
+    // e4m3 (T, K) and their scales, act_quant_kernel's bytes), or null
+    const uint8_t* aq = nullptr;
+    const float* asc = nullptr;
     bool silu;
     const int32_t* w;
     const void* scales;
