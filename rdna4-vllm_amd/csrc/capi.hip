@@ -214,7 +214,7 @@ void carve_apply(WS& w, const ApplyPlan& pl, int64_t T, int64_t H, int64_t inter
                  int64_t top_k, int32_t** sti, int32_t** eid, int32_t** ntp, void** align_ws,
                  size_t* align_bytes, uint8_t** xq, float** s1, __half** h, uint8_t** hq,
                  float** s2, float** acc, float** gs1, float** gs2, __half** y,
-                 int32_t** s2r, uint64_t** dflags) {
+                 int32_t** s2r, uint64_t** dflags, DecHandover** dhand) {
     *sti = w.template take<int32_t>((size_t)pl.P);
     *eid = w.template take<int32_t>((size_t)pl.nblk);
     *ntp = w.template take<int32_t>(1);
@@ -235,6 +235,8 @@ void carve_apply(WS& w, const ApplyPlan& pl, int64_t T, int64_t H, int64_t inter
     *gs2 = pl.decode ? nullptr : w.template take<float>((size_t)(pl.P * ((inter + 127) / 128)));
     // decode: completion flags of the fused layer's work-groups and their timeout words
     *dflags = pl.decode ? w.template take<uint64_t>((size_t)(2 * kDecodeFlagSlots)) : nullptr;
+    // decode: the lists the gemm1 launch hands to the gemm2 launch
+    *dhand = pl.decode ? w.template take<DecHandover>(1) : nullptr;
 }
 
 // Per-call value of the fused decode layer's completion flags (never 0).
@@ -358,8 +360,9 @@ int moe_apply_impl(const void* x, int x_dtype, int64_t T, int64_t H, int64_t int
     int32_t *sti, *eid, *ntp; void* aws; size_t abytes; uint8_t* xq; float* s1; __half* h;
     uint8_t* hq; float* s2; float* acc; float* gs1; float* gs2; __half* y; int32_t* s2r;
     uint64_t* dflags;
+    DecHandover* dhand;
     carve_apply(w, pl, T, H, inter, E, top_k, &sti, &eid, &ntp, &aws, &abytes, &xq, &s1, &h, &hq,
-                &s2, &acc, &gs1, &gs2, &y, &s2r, &dflags);
+                &s2, &acc, &gs1, &gs2, &y, &s2r, &dflags, &dhand);
     if (workspace == nullptr || !w.ok()) {
         set_error("moe_apply: workspace smaller than w4a8_moe_apply_workspace_size()");
         return W4A8_ERR_WORKSPACE;
@@ -438,6 +441,9 @@ int moe_apply_impl(const void* x, int x_dtype, int64_t T, int64_t H, int64_t int
             stage_mark(4, s);
             stage_mark(5, s);
         } else {
+            // gemm1 hands its expert lists to the gemm2 launch
+            d.hand_out = dhand;
+            d2.hand_in = dhand;
             stamp_gemm(0);
             rc = launch_decode_gemv(d, s);
             stamp_gemm(-1);
@@ -836,9 +842,9 @@ size_t w4a8_moe_apply_workspace_size(int64_t T, int64_t H, int64_t inter, int64_
     const ApplyPlan pl = plan_apply(T, E, top_k);
     SizeProbe sp;
     int32_t *a, *b, *c; void* d; size_t db; uint8_t* e; float* f; __half* g; uint8_t* h;
-    float *i, *j, *k, *l; __half* m; int32_t* n; uint64_t* o;
+    float *i, *j, *k, *l; __half* m; int32_t* n; uint64_t* o; DecHandover* q;
     carve_apply(sp, pl, T, H, inter, E, top_k, &a, &b, &c, &d, &db, &e, &f, &g, &h, &i, &j, &k,
-                &l, &m, &n, &o);
+                &l, &m, &n, &o, &q);
     return sp.s.used;
 }
 

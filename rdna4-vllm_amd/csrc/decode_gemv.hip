@@ -8,9 +8,10 @@
 // zero-point term, scale fold order and split-K sum order). The schedule is this file's own:
 //
 //   * one four-wave work-group per CU (one wave per SIMD, so a wave holds four weight chunks
-//     in registers); every work-group builds, in LDS, the list of touched experts and each
-//     one's slots from topk_ids (the order of slots inside an expert does not matter: every
-//     output row depends on its own activation row only);
+//     in registers); every work-group of gemm1 builds, in LDS, the list of touched experts
+//     and each one's slots from topk_ids (the order of slots inside an expert does not
+//     matter: every output row depends on its own activation row only), and work-group 0
+//     writes the lists to the workspace, where gemm2's work-groups read them;
 //   * the layer's work is a list of units (touched expert, column unit: 16 gate + 16 up
 //     columns for gemm1+SiLU, 32 columns for gemm2), streamed once per 16-row pass over the
 //     expert's slots; it is split over teams (a team is one wave, or the whole work-group
@@ -58,10 +59,17 @@ struct DecodeParams {
     // act_quant_kernel's bytes, written by the router launch); null: quantise a in registers
     const uint8_t* aq;
     const float* asc;
+    // list hand-over between the two launches: gemm1 writes its lists (hand_out), gemm2 reads
+    // them (hand_in) instead of loading the ids and building them again
+    DecHandover* hand_out;
+    const DecHandover* hand_in;
     const int32_t* w;        // fragment layout (E, N/16, 272 G): blocks, then scales/zeros
     void* out;               // kSiluHalf: (numel, N/2) fp16; kSlotF32: (numel, N) fp32
     int K, N, G;
 };
+
+static_assert(kDecMaxExperts == kDecHandExperts && kDecMaxSlots == kDecHandSlots,
+              "the hand-over holds the lists whole");
 
 struct DecodeLists {
     int n_touched;
@@ -207,6 +215,34 @@ __device__ int unit_at_cost(const DecodeLists& L, int n_t, int upe, int X) {
     const int d = X - dec_cost(L, r, upe) - np * kDecPassCost;
     const int k = d <= 0 ? 0 : (d + np - 1) / np;
     return r * upe + min(k, upe);
+}
+
+// gemm1's side of the hand-over: work-group 0 writes the lists before its own work.
+__device__ void dec_hand_lists(const DecodeParams& p, const DecodeLists& L) {
+    if (blockIdx.x != 0) return;
+    DecHandover* h = p.hand_out;
+    const int n_t = L.n_touched;
+    for (int i = threadIdx.x; i <= n_t; i += kDecThreads) {
+        h->expert[i] = i < n_t ? L.expert[i] : (int16_t)0;
+        h->first[i] = L.first[i];
+        h->pp[i] = L.pp[i];
+    }
+    for (int i = threadIdx.x; i < p.numel; i += kDecThreads) h->slot[i] = L.slot[i];
+    if (threadIdx.x == 0) h->n_touched = n_t;
+}
+
+// gemm2's side: the lists into LDS (one round of loads)
+__device__ void dec_hand_read(const DecodeParams& p, DecodeLists& L) {
+    const DecHandover* h = p.hand_in;
+    const int nmax = min(p.E, p.numel);      // touched experts <= min(E, slots)
+    for (int i = threadIdx.x; i <= nmax; i += kDecThreads) {
+        L.expert[i] = h->expert[i];
+        L.first[i] = h->first[i];
+        L.pp[i] = h->pp[i];
+    }
+    for (int i = threadIdx.x; i < p.numel; i += kDecThreads) L.slot[i] = h->slot[i];
+    if (threadIdx.x == kDecThreads - 1) L.n_touched = h->n_touched;
+    __syncthreads();
 }
 
 template <Epi EPI, int GPW, int KSPLIT>
@@ -748,7 +784,12 @@ __global__ void __launch_bounds__(kDecThreads, 1) decode_gemv_kernel(DecodeParam
         dec_route(p, s_ids);
         ids = s_ids;
     }
-    build_lists(p, ids, L);
+    if (p.hand_in != nullptr) {
+        dec_hand_read(p, L);
+    } else {
+        build_lists(p, ids, L);
+        if (p.hand_out != nullptr) dec_hand_lists(p, L);
+    }
     dec_run<EPI, GPW, KSPLIT, ABF16, false, PREQ>(p, L, s_amax, reinterpret_cast<v4f*>(s_dyn), DecDep{});
     dec_keep(warm, p.out);
 }
@@ -931,6 +972,8 @@ DecodeParams dec_params(const DecodeLaunch& d) {
     p.a_bf16 = d.a_bf16 ? 1 : 0;
     p.aq = d.silu ? d.aq : nullptr;
     p.asc = d.silu ? d.asc : nullptr;
+    p.hand_out = d.silu ? d.hand_out : nullptr;
+    p.hand_in = d.silu ? nullptr : d.hand_in;
     p.a_per_token = d.silu ? 1 : 0;
     p.w = d.w;
     p.out = d.out;

@@ -208,6 +208,18 @@ bool gemv_supported(int64_t K, int64_t group_size);
 // groups the slots by expert from topk_ids itself and quantises its activation rows in
 // registers. silu: gemm1 (a = x (T, K) by token, out = h (numel, N/2) fp16 after SiLU*mul);
 // else gemm2 (a = h (numel, K) fp16 by slot, out = y (numel, N) fp32).
+// Hand-over of the decode lists from the gemm1 launch to the gemm2 launch (workspace):
+// the touched experts, their slot lists and pass counts.
+constexpr int kDecHandExperts = 1024;
+constexpr int kDecHandSlots = 1024;
+struct DecHandover {
+    int n_touched;
+    int16_t expert[kDecHandExperts + 1];
+    int16_t first[kDecHandExperts + 1];
+    int pp[kDecHandExperts + 1];
+    int16_t slot[kDecHandSlots];
+};
+
 struct DecodeLaunch {
     const int32_t* topk_ids;
     // gemm1 only: route in the kernel from these logits (decode_routes_in_kernel), writing
@@ -225,6 +237,9 @@ struct DecodeLaunch {
     // e4m3 (T, K) and their scales, act_quant_kernel's bytes), or null
     const uint8_t* aq = nullptr;
     const float* asc = nullptr;
+    // list hand-over: gemm1 writes it (hand_out), gemm2 reads it (hand_in)
+    DecHandover* hand_out = nullptr;
+    const DecHandover* hand_in = nullptr;
     bool silu;
     const int32_t* w;
     const void* scales;
