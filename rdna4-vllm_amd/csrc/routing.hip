@@ -111,28 +111,37 @@ __device__ int chunk_rank(const int32_t* __restrict__ ids, int64_t numel, int64_
 }
 
 // Writes expert_ids, the padding sentinels and ntp from per-expert totals `cnt` and
-// padded offsets `eoff` (both in LDS). One thread per expert; with nwg > 1 work-groups
-// sharing the job, work-group wg takes experts wg, wg + nwg, ... and every nwg-th
-// stretch of the tail.
+// padded offsets `eoff` (both in LDS), one padded row and one block per thread: the expert of
+// padded row r is the largest e with eoff[e] <= r (a binary search over the offsets; an
+// expert without slots has the offset of the next one, so it is never the largest), and
+// r is a padding row when r - eoff[e] >= cnt[e]. With nwg > 1 work-groups sharing the job,
+// work-group wg takes every nwg-th stretch of kAlignThreads rows and blocks.
 __device__ void write_layout(const int* cnt, const int* eoff, int E, int64_t block_m,
                              int64_t numel, int total_padded, int32_t* __restrict__ sorted_ids,
                              int64_t sorted_len, int32_t* __restrict__ expert_ids,
                              int32_t* __restrict__ ntp, int wg = 0, int nwg = 1) {
     const int tid = threadIdx.x;
-    for (int e = wg + nwg * tid; e < E; e += nwg * kAlignThreads) {
-        const int c = cnt[e];
-        if (c == 0) continue;
-        const int o = eoff[e];
-        const int padded = (int)((c + block_m - 1) / block_m * block_m);
-        for (int r = o + c; r < o + padded; ++r) sorted_ids[r] = (int32_t)numel;
-        for (int b = (int)(o / block_m); b < (int)((o + padded) / block_m); ++b)
-            expert_ids[b] = e;
-    }
+    auto expert_of = [&](int r) {
+        int lo = 0, hi = E - 1;             // eoff[0] = 0 <= r
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (eoff[mid] <= r) lo = mid;
+            else hi = mid - 1;
+        }
+        return lo;
+    };
     const int64_t step = (int64_t)nwg * kAlignThreads;
-    for (int64_t r = total_padded + (int64_t)wg * kAlignThreads + tid; r < sorted_len; r += step)
-        sorted_ids[r] = (int32_t)numel;
-    for (int64_t b = total_padded / block_m + (int64_t)wg * kAlignThreads + tid; b < sorted_len / block_m; b += step)
-        expert_ids[b] = -1;
+    for (int64_t r = (int64_t)wg * kAlignThreads + tid; r < sorted_len; r += step) {
+        if (r >= total_padded) {
+            sorted_ids[r] = (int32_t)numel;
+            continue;
+        }
+        const int e = expert_of((int)r);
+        if (r - eoff[e] >= cnt[e]) sorted_ids[r] = (int32_t)numel;
+    }
+    const int64_t nblocks = sorted_len / block_m;
+    for (int64_t b = (int64_t)wg * kAlignThreads + tid; b < nblocks; b += step)
+        expert_ids[b] = b * block_m < total_padded ? expert_of((int)(b * block_m)) : -1;
     if (wg == 0 && tid == 0) ntp[0] = total_padded;
 }
 
