@@ -214,8 +214,12 @@ def gemm1_kernel_name(cfg, decode, layout, fused=False):
         # persistent decode kernel (decode_gemv.hip dec_split): groups per wave, split-K
         split = {1: "1, 1", 2: "2, 1", 3: "3, 1", 4: "4, 1", 8: "2, 4", 12: "3, 4", 16: "4, 4",
                  32: "8, 4"}[H // 128]
-        # the bench's activations are bf16: the kernel's bf16 instantiation runs
-        return f"decode_gemv_kernel<(w4a8::Epi)1, {split}, true>"
+        # the bench's activations are bf16. After a router launch (T > 4) gemm1 reads the
+        # rows the router quantised (ABF16 false, PREQ true); with T <= 4 tokens it routes
+        # them itself and quantises the bf16 rows in registers (ABF16 true, PREQ false)
+        if cfg["T"] > 4:
+            return f"decode_gemv_kernel<(w4a8::Epi)1, {split}, false, true>"
+        return f"decode_gemv_kernel<(w4a8::Epi)1, {split}, true, false>"
     if decode:
         split = {1: "1, 1", 2: "2, 1", 3: "3, 1", 4: "4, 1", 8: "4, 2", 12: "3, 4", 16: "4, 4",
                  32: "8, 4"}[H // 128]
