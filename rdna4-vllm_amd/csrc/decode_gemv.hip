@@ -234,9 +234,9 @@ __device__ void dec_hand_lists(const DecodeParams& p, const DecodeLists& L) {
 // gemm2's side: the lists into LDS (one round of loads)
 __device__ void dec_hand_read(const DecodeParams& p, DecodeLists& L) {
     const DecHandover* h = p.hand_in;
-    const int nmax = min(p.E, p.numel);      // touched experts <= min(E, slots)
+    const int nmax = min(p.E, p.numel);      // touched experts <= min(E, slots) <= 1024
     for (int i = threadIdx.x; i <= nmax; i += kDecThreads) {
-        L.expert[i] = h->expert[i];
+        if (i < nmax) L.expert[i] = h->expert[i];
         L.first[i] = h->first[i];
         L.pp[i] = h->pp[i];
     }

@@ -224,6 +224,25 @@ def test_prefill_layer_equals_op_composition(T, frag):
     assert torch.equal(fused, unfused)
 
 
+def test_decode_1024_experts_1024_slots():
+    """The decode schedule at its list limits (1024 experts, 64 tokens x top-16 = 1024 slots):
+    gemm2 reads the lists gemm1 hands over whole. moe_forward (router launch, prequantised
+    rows) equals fused_topk + moe_apply bit for bit, and the oracle agrees."""
+    cfg = dict(T=64, H=256, E=1024, k=16, I=128, g=128, routing="uniform")
+    ws = bench.make_weights(cfg, 990, DEV)
+    x, logits = bench.make_inputs(cfg, 991, DEV)
+    f13 = W.repack_fragments(ws["w13"], ws["s13"], ws["z13"])
+    f2 = W.repack_fragments(ws["w2"], ws["s2"], ws["z2"])
+    tw, ids = W.fused_topk(None, logits, cfg["k"], True)
+    a = W.moe_apply(x, f13, f2, ws["s13"], ws["s2"], ws["z13"], ws["z2"], tw, ids)
+    b, tw2, ids2 = W.moe_forward(x, logits, cfg["k"], f13, f2, ws["s13"], ws["s2"], ws["z13"],
+                                 ws["z2"])
+    assert torch.equal(ids, ids2) and torch.equal(tw, tw2)
+    assert torch.equal(a, b)
+    ref = oracle_layer(cfg, ws, x, tw, ids)
+    assert maxrel(a.float().cpu().numpy(), ref) <= REL_TOL
+
+
 @pytest.mark.parametrize("T,frag,emap", [(160, False, False), (300, True, False),
                                          (1024, True, True), (4096, True, False)])
 def test_prefill_pair_equals_two_launches(T, frag, emap):
