@@ -180,7 +180,9 @@ template <int S>
 __device__ __forceinline__ uint32_t dpp_step(uint32_t v) {
     static_assert(S >= 0 && S < 4, "DPP steps stay inside a row of 16 lanes");
     constexpr int ctrl = S == 0 ? 0xB1 : S == 1 ? 0x4E : S == 2 ? 0x141 : 0x140;
-    return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, ctrl, 0xF, 0xF, false);
+    // every lane receives a value (full permutations inside rows), so the old value is never
+    // kept; with it left undefined the compiler folds the move into the consuming VALU op
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, ctrl, 0xF, 0xF, true);
 }
 
 // v combined over aligned groups of 2^LOG2 lanes (op commutative and associative).
