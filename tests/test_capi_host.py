@@ -42,7 +42,7 @@ def test_abi_version_and_sizes():
     assert L.w4a8_abi_version() == 3
     assert L.w4a8_fragments_words(2, 32, 256) == 2 * 2 * 272 * 2     # 16-row tiles of 272 G words
     assert L.w4a8_moe_align_sorted_len(256, 256, 16) == O.align_alloc_len(256, 256, 16)
-    assert L.w4a8_moe_align_sorted_len(32768, 256, 64) == 48896      # SURVEY C4 P_alloc
+    assert L.w4a8_moe_align_sorted_len(32768, 256, 64) == 48896      # c4: T k + E (64 - 1)
     assert L.w4a8_moe_align_sorted_len(8, 256, 8) == 1800            # C2 with block_m 8
     assert L.w4a8_moe_align_workspace_size(256, 256) == 0            # one-chunk path
     assert L.w4a8_moe_align_workspace_size(32768, 256) > 0
