@@ -16,7 +16,8 @@
 //     columns for gemm1+SiLU, 32 columns for gemm2), streamed once per 16-row pass over the
 //     expert's slots; it is split over teams (a team is one wave, or the whole work-group
 //     when the K groups are split over its 4 waves) in contiguous ranges of equal work, a
-//     pass start (row load and quantisation) counting kDecPassCost units;
+//     pass start (row load, and quantisation where the rows are not quantised already)
+//     counting a GEMM's pass cost in units;
 //   * a team walks its range expert by expert and pass by pass; at a pass start it loads the
 //     activation rows (gemm1: x rows of the slots' tokens, fp16 or bf16; gemm2: the slots'
 //     h rows) and quantises them in registers, bit-identical to act_quant_kernel; the weight
@@ -38,7 +39,10 @@ constexpr int kDecThreads = 256;
 constexpr int kDecMaxSlots = 1024;      // T * top_k
 constexpr int kDecMaxExperts = 1024;
 constexpr int kDecRing = 3;             // weight chunks in flight per wave (a ring slot each)
-constexpr int kDecPassCost = 2;         // partition cost of a pass start (row load), in units
+// partition cost of a pass start, in units: gemm1 loads quantised rows (or one row of x per
+// token), gemm2 loads and quantises its h rows (measured best at c3: 1 and 3)
+constexpr int kDecPassCost1 = 1;
+constexpr int kDecPassCost2 = 3;
 constexpr uint32_t kDecOnes = 0x38383838u;   // four e4m3 bytes of 1.0
 using u16x2 = unsigned short __attribute__((ext_vector_type(2)));
 
@@ -83,9 +87,9 @@ struct DecodeLists {
 
 // Partition cost of the work before touched expert r for a GEMM with upe column units per
 // expert: every 16-row pass streams the upe units once and starts with a row load charged
-// as kDecPassCost units.
-__device__ __forceinline__ int dec_cost(const DecodeLists& L, int r, int upe) {
-    return L.pp[r] * (upe + kDecPassCost);
+// as pc units.
+__device__ __forceinline__ int dec_cost(const DecodeLists& L, int r, int upe, int pc) {
+    return L.pp[r] * (upe + pc);
 }
 
 // Touched experts and their slot lists (the align's grouping, without padding) in LDS, and
@@ -200,19 +204,19 @@ __device__ void dec_route(const DecodeParams& p, int32_t* s_ids) {
 }
 
 // First unit whose work start is at or past X: the work start of unit u of touched expert r
-// is cost[r] + np (kDecPassCost + u - r upe), np = its passes. Wave-wide 64-ary search.
-__device__ int unit_at_cost(const DecodeLists& L, int n_t, int upe, int X) {
+// is cost[r] + np (pc + u - r upe), np = its passes. Wave-wide 64-ary search.
+__device__ int unit_at_cost(const DecodeLists& L, int n_t, int upe, int pc, int X) {
     const int lane = threadIdx.x & 63;
     const int step = (n_t + 64) / 64;       // candidates cost[0], cost[step], ... cover [0, n_t]
     int cand = lane * step;
-    uint64_t m = __ballot(cand <= n_t && dec_cost(L, cand, upe) <= X);   // bit 0: cost 0 <= X
+    uint64_t m = __ballot(cand <= n_t && dec_cost(L, cand, upe, pc) <= X);   // bit 0: cost 0 <= X
     const int base = (63 - __clzll(m)) * step;
     cand = base + lane;
-    m = __ballot(lane < step && cand <= n_t && dec_cost(L, cand, upe) <= X);
+    m = __ballot(lane < step && cand <= n_t && dec_cost(L, cand, upe, pc) <= X);
     const int r = base + 63 - __clzll(m);    // largest r with cost[r] <= X
     if (r >= n_t) return n_t * upe;
     const int np = ((int)L.first[r + 1] - (int)L.first[r] + 15) >> 4;
-    const int d = X - dec_cost(L, r, upe) - np * kDecPassCost;
+    const int d = X - dec_cost(L, r, upe, pc) - np * pc;
     const int k = d <= 0 ? 0 : (d + np - 1) / np;
     return r * upe + min(k, upe);
 }
@@ -257,6 +261,7 @@ struct DecCfg {
     static constexpr int GC = GPW < 4 ? GPW : (GPW == 8 ? 2 : 4);
     static constexpr int NB = GPW / GC;           // chunks per unit
     static constexpr int TEAMS = 4 / KSPLIT;      // teams per work-group
+    static constexpr int PC = kSilu ? kDecPassCost1 : kDecPassCost2;   // pass-start cost
     static_assert(KSPLIT == 1 || KSPLIT == 4, "a team is one wave or the whole work-group");
     static_assert(GPW % GC == 0 && (NB == 1 || NB == 2 || NB == 4), "unsupported groups per wave");
     // ring slots: a multiple of NB, so a slot's group batch is fixed
@@ -390,11 +395,11 @@ __device__ __forceinline__ void dec_run(const DecodeParams& p, const DecodeLists
     const int nteams = (int)gridDim.x * C::TEAMS;
     const int tm = (int)blockIdx.x * C::TEAMS + team;
     // team tm starts at work floor(W tm / nteams), in 32-bit arithmetic (W < 2^25)
-    const int work = dec_cost(L, n_t, upe);
+    const int work = dec_cost(L, n_t, upe, C::PC);
     const int wq = work / nteams, wr = work % nteams;
     auto work_at = [&](int t) { return wq * t + wr * t / nteams; };
-    const int ua = __builtin_amdgcn_readfirstlane(unit_at_cost(L, n_t, upe, work_at(tm)));
-    const int ub = __builtin_amdgcn_readfirstlane(unit_at_cost(L, n_t, upe, work_at(tm + 1)));
+    const int ua = __builtin_amdgcn_readfirstlane(unit_at_cost(L, n_t, upe, C::PC, work_at(tm)));
+    const int ub = __builtin_amdgcn_readfirstlane(unit_at_cost(L, n_t, upe, C::PC, work_at(tm + 1)));
     if (ua >= ub) return;      // team-uniform; a K-split team is the whole work-group
 
     // the team's work in order: touched experts r, 16-row passes over each expert's slots,
@@ -496,12 +501,12 @@ __device__ __forceinline__ void dec_run(const DecodeParams& p, const DecodeLists
     auto producers = [&](int& w_lo, int& w_hi) __attribute__((always_inline)) {
         const int r_a = ua / upe, r_b = (ub - 1) / upe;
         const int n1 = (int)gridDim.x * dep.teams1;
-        const int w1 = dec_cost(L, n_t, dep.upe1);
+        const int w1 = dec_cost(L, n_t, dep.upe1, kDecPassCost1);
         // start costs of the first unit of r_a and the last unit of r_b in the first GEMM
         const int np_a = ((int)L.first[r_a + 1] - (int)L.first[r_a] + 15) >> 4;
         const int np_b = ((int)L.first[r_b + 1] - (int)L.first[r_b] + 15) >> 4;
-        const int s_lo = dec_cost(L, r_a, dep.upe1) + np_a * kDecPassCost;
-        const int s_hi = dec_cost(L, r_b, dep.upe1) + np_b * (kDecPassCost + dep.upe1 - 1);
+        const int s_lo = dec_cost(L, r_a, dep.upe1, kDecPassCost1) + np_a * kDecPassCost1;
+        const int s_hi = dec_cost(L, r_b, dep.upe1, kDecPassCost1) + np_b * (kDecPassCost1 + dep.upe1 - 1);
         w_lo = dec_owner(s_lo, w1, n1) / dep.teams1;
         w_hi = dec_owner(s_hi, w1, n1) / dep.teams1;
     };
