@@ -489,10 +489,15 @@ __device__ __forceinline__ void ar_tile(const Params& p, int ntp, int tile, int 
         using M0 = std::integral_constant<int, 0>;
         using M1 = std::integral_constant<int, 1>;
         using M2 = std::integral_constant<int, 2>;
+        // The scales of group g are read from the table one step ahead of their fold (in step
+        // g, folded in step g + 1 or by fold_last): read right before the fold, the LDS
+        // round trip stood between the step's MFMAs and its fold every step.
+        uint4 scn = make_uint4(0u, 0u, 0u, 0u);
         auto consume = [&](int g, auto slotc, auto modec) __attribute__((always_inline)) {
             constexpr int sl = decltype(slotc)::value;
             constexpr int mode = decltype(modec)::value;
-            const uint4 sc = mode ? scales_of(g - 1) : make_uint4(0u, 0u, 0u, 0u);
+            const uint4 sc = scn;                  // group g - 1 (not read when mode == 0)
+            scn = scales_of(g);
             v8i bf[kArNT];
 #pragma unroll
             for (int j = 0; j < kArNT; ++j) bf[j] = spread_nibbles(bw[sl][j]);
@@ -541,7 +546,8 @@ __device__ __forceinline__ void ar_tile(const Params& p, int ntp, int tile, int 
         };
         // fold of the last step's MFMA results (group g) into the accumulators
         auto fold_last = [&](int g) __attribute__((always_inline)) {
-            const uint4 sc = scales_of(g);
+            (void)g;
+            const uint4 sc = scn;                  // read by the step of group g
 #pragma unroll
             for (int i = 0; i < NF; ++i)
 #pragma unroll
