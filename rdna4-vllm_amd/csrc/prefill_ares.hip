@@ -131,13 +131,32 @@ __device__ __forceinline__ uint32_t pack_bf16x2(__bf16 a, __bf16 b) {
     return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
 }
 
-// One tile (BM sorted rows of one expert) over weight ranges [r_begin, r_end) by the whole
-// work-group; ntp: the live padded rows. SQ: the tile quantises fp16 rows itself (fp16
-// output, K <= kArMaxKAq); otherwise it loads prequantised rows. A compile-time choice: with
-// both prologues in one kernel the compiler kept the 16-chunk row staging array in scratch,
-// each store waiting for its load.
+// A tile's expert and, in lane l < BM, the slot of tile row l (-1: padding or past the ntp
+// live padded rows). The two GEMMs of a pair kernel's tile share it: both walk the same
+// sorted rows.
+struct ArRoute {
+    int e;
+    int slot;
+};
+template <int BM>
+__device__ __forceinline__ ArRoute ar_route(const Params& p, int ntp, int tile) {
+    const int64_t row0 = (int64_t)tile * BM;
+    ArRoute rt;
+    rt.e = p.expert_ids ? p.expert_ids[row0 / p.block_m] : 0;
+    rt.slot = -1;
+    if (rt.e >= 0 && rt.e < p.E && (threadIdx.x & 63) < BM)
+        resolve_row(p, row0 + (threadIdx.x & 63), ntp, rt.slot);
+    return rt;
+}
+
+// One tile (BM sorted rows of one expert, routed by rt) over weight ranges [r_begin, r_end)
+// by the whole work-group. SQ: the tile quantises fp16 rows itself (fp16 output,
+// K <= kArMaxKAq); otherwise it loads prequantised rows. A compile-time choice: with both
+// prologues in one kernel the compiler kept the 16-chunk row staging array in scratch, each
+// store waiting for its load.
 template <Epi EPI, bool FRAG, int BM, bool SQ>
-__device__ __forceinline__ void ar_tile(const Params& p, int ntp, int tile, int r_begin, int r_end) {
+__device__ __forceinline__ void ar_tile(const Params& p, const ArRoute& rt, int tile, int r_begin,
+                                        int r_end) {
     constexpr bool kSilu = EPI == Epi::kSiluHalf;
     static_assert(!(SQ && kSilu), "gemm1 tiles take prequantised rows");
     constexpr int GPR = ar_gpr<BM>();
@@ -163,11 +182,10 @@ __device__ __forceinline__ void ar_tile(const Params& p, int ntp, int tile, int 
     const int ncols = kSilu ? p.N / 2 : p.N;
 
     const int64_t row0 = (int64_t)tile * BM;
-    const int e = p.expert_ids ? p.expert_ids[row0 / p.block_m] : 0;
+    const int e = rt.e;
     if (e < 0 || e >= p.E) return;
-    // lane l < BM of every wave resolves row l; a real row's source is its activation row
-    int slot = -1;
-    const int src = lane < BM ? resolve_row(p, row0 + lane, ntp, slot) : -1;
+    // lane l < BM of every wave holds row l's slot; a real row's source is its activation row
+    const int src = rt.slot < 0 ? -1 : p.identity ? (int)(row0 + lane) : rt.slot / p.top_k;
     const uint64_t vmask = __ballot(src >= 0);
     if (vmask == 0) return;
     const int maxrow = 63 - __clzll(vmask);
@@ -337,7 +355,11 @@ __device__ __forceinline__ void ar_tile(const Params& p, int ntp, int tile, int 
     constexpr int kRowsPerWave = BM / kArWaves;
     constexpr int kAqPass = kArMaxKAq / 512;
     constexpr bool self_quant = SQ;
-    uint4 raw[SQ ? kRowsPerWave : 1][SQ ? kAqPass : 1]; // fp16 rows (self-quantising tiles)
+    // fp16 rows (self-quantising tiles): wave w takes rows 8 w .. 8 w + 7 in two passes of four
+    // rows, sixteen lanes a row; lane c of a row holds its 32 values c * 32 .. c * 32 + 31 of
+    // each 512-wide part of K, four 8-value pieces (one 16-byte load each)
+    static_assert(!SQ || kRowsPerWave == 8, "self-quantising tiles take 64 rows");
+    uint4 raw[SQ ? 2 : 1][SQ ? kAqPass : 1][SQ ? 4 : 1];
     float asv[BM * GPR / kArThreads];                   // row group sums
     // Prequantised rows go straight into the LDS tile (global_load_lds, 16 bytes per lane; no
     // registers, no LDS writes): a wave instruction fills one contiguous KB, rows
@@ -361,12 +383,14 @@ __device__ __forceinline__ void ar_tile(const Params& p, int ntp, int tile, int 
         const int npass = K / 512;                      // 1 or 2 (K <= kArMaxKAq)
         const __half* xh = reinterpret_cast<const __half*>(p.xh);
 #pragma unroll
-        for (int u = 0; u < kRowsPerWave; ++u) {
-            const int sr = src_of(kRowsPerWave * wave + u);
+        for (int pp = 0; pp < 2; ++pp) {
+            const int sr = src_of(8 * wave + 4 * pp + (lane >> 4));
 #pragma unroll
             for (int ps = 0; ps < kAqPass; ++ps)
-                raw[u][ps] = *reinterpret_cast<const uint4*>(
-                    xh + (int64_t)sr * K + std::min(ps, npass - 1) * 512 + lane * 8);
+#pragma unroll
+                for (int pc = 0; pc < 4; ++pc)
+                    raw[pp][ps][pc] = *reinterpret_cast<const uint4*>(
+                        xh + (int64_t)sr * K + std::min(ps, npass - 1) * 512 + c16 * 32 + pc * 8);
         }
     } else {
 #pragma unroll
@@ -389,44 +413,82 @@ __device__ __forceinline__ void ar_tile(const Params& p, int ntp, int tile, int 
     issue(S3{});
     if constexpr (self_quant) {
         // as act_quant_kernel: s = max(absmax / 448, 1e-8), e4m3 RNE of x / s in k8-interleaved
-        // order, per-group sums of the e4m3 values by the same lane tree; straight into LDS
+        // order, per-group sums of the e4m3 values; straight into LDS. A row's sixteen lanes
+        // reduce its absmax. A group's sixteen 8-value pieces lie in four lanes, four each
+        // (piece 4 (c & 3) + pc), so the sum tree of act_quant_kernel (pieces i and i ^ 1,
+        // then i ^ 2, i ^ 4, i ^ 8) runs as two adds in the lane and two steps over the four
+        // lanes: the same sums in the same order, so the same bits.
         const int npass = K / 512;
+        using u16x2 = unsigned short __attribute__((ext_vector_type(2)));
+        auto hval = [&](const uint4& w4, int j) __attribute__((always_inline)) {
+            const uint32_t wd = j < 2 ? w4.x : j < 4 ? w4.y : j < 6 ? w4.z : w4.w;
+            return __half2float(__ushort_as_half((uint16_t)((j & 1) ? wd >> 16 : wd & 0xFFFF)));
+        };
 #pragma unroll
-        for (int u = 0; u < kRowsPerWave; ++u) {
-            const int m = kRowsPerWave * wave + u;
-            auto val = [&](int ps, int j) __attribute__((always_inline)) {
-                const uint4 w4 = raw[u][ps];
-                const uint32_t wd = j < 2 ? w4.x : j < 4 ? w4.y : j < 6 ? w4.z : w4.w;
-                return __half2float(__ushort_as_half((uint16_t)((j & 1) ? wd >> 16 : wd & 0xFFFF)));
-            };
-            float amax = 0.0f;
+        for (int pp = 0; pp < 2; ++pp) {
+            const int m = 8 * wave + 4 * pp + (lane >> 4);
+            // absmax on the magnitude bits, two values per instruction: the conversion to fp32
+            // is monotone in them; a NaN (above the infinity pattern), which fmaxf skips,
+            // sends the lane to the element-wise form
+            u16x2 m2 = {0, 0};
 #pragma unroll
             for (int ps = 0; ps < kAqPass; ++ps) {
                 if (ps >= npass) break;
 #pragma unroll
-                for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(val(ps, j)));
+                for (int pc = 0; pc < 4; ++pc) {
+                    const uint4 w4 = raw[pp][ps][pc];
+                    const uint32_t wd[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        m2 = __builtin_elementwise_max(m2, __builtin_bit_cast(u16x2, wd[j] & 0x7FFF7FFFu));
+                }
             }
-            amax = wave_max(amax);
+            const uint32_t mbits = max((uint32_t)m2.x, (uint32_t)m2.y);
+            float amax;
+            if (__builtin_expect(mbits <= 0x7C00u, 1)) {
+                amax = __half2float(__ushort_as_half((uint16_t)mbits));
+            } else {
+                amax = 0.0f;
+#pragma unroll
+                for (int ps = 0; ps < kAqPass; ++ps) {
+                    if (ps >= npass) break;
+#pragma unroll
+                    for (int pc = 0; pc < 4; ++pc)
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(hval(raw[pp][ps][pc], j)));
+                }
+            }
+            amax = lane_allreduce<4>(amax, MaxOp{});
             const float sc = act_scale_from_absmax(amax);
-            if (lane == 0) s_asc[m] = sc;
+            if (c16 == 0) s_asc[m] = sc;
             const float inv = 1.0f / sc;
 #pragma unroll
             for (int ps = 0; ps < kAqPass; ++ps) {
                 if (ps >= npass) break;
-                float v[8];
+                uint32_t lo[4], hi[4];
+                float t[4];
 #pragma unroll
-                for (int j = 0; j < 8; ++j) v[j] = val(ps, j) * inv;
-                const uint32_t lo = pack4_e4m3(v[0], v[2], v[4], v[6]);
-                const uint32_t hi = pack4_e4m3(v[1], v[3], v[5], v[7]);
-                const int k = ps * 512 + lane * 8;
-                *reinterpret_cast<uint2*>(s_a + ar_a_off<BM>(m, k / kGroup, (k % kGroup) / 16) + 8 * (lane & 1)) =
-                    make_uint2(lo, hi);
-                float t = e4m3_pair_sum(0.f, lo, hi);
-                t = lane_allreduce<4>(t, SumOp{});
-                if ((lane & 15) == 0) {
-                    const __bf16 h = (__bf16)t;
-                    s_sah[m * GPR + k / kGroup] = h;
-                    s_sal[m * GPR + k / kGroup] = (__bf16)(t - (float)h);
+                for (int pc = 0; pc < 4; ++pc) {
+                    float v[8];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) v[j] = hval(raw[pp][ps][pc], j) * inv;
+                    lo[pc] = pack4_e4m3(v[0], v[2], v[4], v[6]);
+                    hi[pc] = pack4_e4m3(v[1], v[3], v[5], v[7]);
+                    t[pc] = e4m3_pair_sum(0.f, lo[pc], hi[pc]);
+                }
+                const int k = ps * 512 + c16 * 32;          // the lane's first value
+                const int g = k / kGroup;
+                // pieces 0, 1 fill one 16-byte chunk (8 bytes each), pieces 2, 3 the next
+#pragma unroll
+                for (int h2 = 0; h2 < 2; ++h2)
+                    *reinterpret_cast<uint4*>(s_a + ar_a_off<BM>(m, g, (k % kGroup) / 16 + h2)) =
+                        make_uint4(lo[2 * h2], hi[2 * h2], lo[2 * h2 + 1], hi[2 * h2 + 1]);
+                float gs = (t[0] + t[1]) + (t[2] + t[3]);
+                gs = lane_allreduce<2>(gs, SumOp{});
+                if ((c16 & 3) == 0) {
+                    const __bf16 h = (__bf16)gs;
+                    s_sah[m * GPR + g] = h;
+                    s_sal[m * GPR + g] = (__bf16)(gs - (float)h);
                 }
             }
         }
@@ -723,7 +785,7 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_kernel(Params p) {
         r_begin = (i % split) * nranges / split;
         r_end = (i % split + 1) * nranges / split;
     }
-    ar_tile<EPI, FRAG, BM, SQ>(p, o.ntp, tile, r_begin, r_end);
+    ar_tile<EPI, FRAG, BM, SQ>(p, ar_route<BM>(p, o.ntp, tile), tile, r_begin, r_end);
 }
 
 // gemm1+SiLU and gemm2 of the same 64 sorted rows in one work-group, one tile after the
@@ -737,12 +799,13 @@ __global__ void __launch_bounds__(kArThreads, 1) prefill_ares_pair_kernel(Params
     const int jx = b / kArXcds;
     const int tile = (b % kArXcds) * o.per_xcd + jx;
     if (jx >= o.per_xcd || tile >= o.ntiles) return;
-    ar_tile<Epi::kSiluHalf, FRAG, kArBM, false>(p1, o.ntp, tile, 0, (p1.N / 2) / ar_range_cols<true>());
+    const ArRoute rt = ar_route<kArBM>(p1, o.ntp, tile);
+    ar_tile<Epi::kSiluHalf, FRAG, kArBM, false>(p1, rt, tile, 0, (p1.N / 2) / ar_range_cols<true>());
     // every wave's h stores complete (and so visible to the work-group's loads, which share
     // the CU's L1) before any wave reads h rows; also the LDS hand-over between the tiles
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    ar_tile<Epi::kHalf, FRAG, kArBM, true>(p2, o.ntp, tile, 0, p2.N / ar_range_cols<false>());
+    ar_tile<Epi::kHalf, FRAG, kArBM, true>(p2, rt, tile, 0, p2.N / ar_range_cols<false>());
 }
 
 template <Epi EPI, bool FRAG, int BM, bool SQ>
@@ -799,6 +862,7 @@ bool prefill_ares_pair_supported(const GroupedArgs& a1, const GroupedArgs& a2) {
            a2.x_fp8 == nullptr && a2.x == a1.out && !a2.x_bf16 && a2.identity_gather &&
            a1.P == a2.P && a1.block_m == a2.block_m && a1.sorted_ids == a2.sorted_ids &&
            a1.expert_ids == a2.expert_ids && a1.ntp == a2.ntp && a1.E == a2.E &&
+           a1.num_valid == a2.num_valid &&
            a1.x_rows * a1.K < ((int64_t)1 << 31) && a2.x_rows * a2.K < ((int64_t)1 << 31) &&
            (!a1.w_frag || ((a1.N / 2) % 16 == 0 && a2.N % 16 == 0));
 }
