@@ -394,6 +394,36 @@ def test_moe_forward_equals_router_then_apply(T, frag, E):
     assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("T,E,k,frag,emap", [(129, 256, 8, True, False), (1000, 256, 8, True, False),
+                                              (513, 128, 4, False, False), (700, 64, 6, True, False),
+                                              (600, 4, 4, True, True), (2048, 128, 8, True, False)])
+def test_router_many_tokens_equals_router_then_apply(T, E, k, frag, emap):
+    """Many tokens (T * k > 1024, the multi-chunk align): moe_forward (router launch that
+    also quantises x, then the align from the ids in memory) equals fused_topk + moe_apply bit
+    for bit: partial last chunks (129 * 8 = 1032 slots), top-k that does not divide a chunk
+    (k = 6), both layouts, and an expert map (8 routed ids, 4 local experts)."""
+    cfg = dict(T=T, H=256, E=E, k=k, I=128, g=128, routing="uniform")
+    ws = bench.make_weights(cfg, 900 + T, DEV)
+    emap_t = None
+    if emap:
+        x, logits = bench.make_inputs(dict(cfg, E=2 * E), 901 + T, DEV)
+        emap_t = torch.tensor([-1] * E + list(range(E)), dtype=torch.int32, device=DEV)
+    else:
+        x, logits = bench.make_inputs(cfg, 901 + T, DEV)
+    x = x.to(torch.bfloat16)
+    w13, w2 = ws["w13"], ws["w2"]
+    if frag:
+        w13, w2 = W.repack_fragments(w13, ws["s13"], ws["z13"]), W.repack_fragments(w2, ws["s2"], ws["z2"])
+    tw, ids = W.fused_topk(None, logits, k, True)
+    a = W.moe_apply(x, w13, w2, ws["s13"], ws["s2"], ws["z13"], ws["z2"], tw, ids, expert_map=emap_t)
+    b, tw2, ids2 = W.moe_forward(x, logits, k, w13, w2, ws["s13"], ws["s2"], ws["z13"], ws["z2"],
+                                 expert_map=emap_t)
+    assert torch.equal(ids2, ids.to(torch.int32)) and torch.equal(tw2, tw)
+    assert torch.equal(a, b)
+    if emap:
+        assert int(ids.max()) >= E and int(ids.min()) < E
+
+
 def test_decode_is_deterministic_and_token_local():
     """Decode schedule: bit-identical reruns; permuting tokens permutes outputs exactly."""
     cfg = dict(bench.CONFIGS["c3"])
