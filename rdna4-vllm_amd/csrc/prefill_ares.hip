@@ -143,9 +143,11 @@ __device__ __forceinline__ ArRoute ar_route(const Params& p, int ntp, int tile) 
     const int64_t row0 = (int64_t)tile * BM;
     ArRoute rt;
     rt.e = p.expert_ids ? p.expert_ids[row0 / p.block_m] : 0;
-    rt.slot = -1;
-    if (rt.e >= 0 && rt.e < p.E && (threadIdx.x & 63) < BM)
-        resolve_row(p, row0 + (threadIdx.x & 63), ntp, rt.slot);
+    // the slot loads do not wait for the expert id (both are in flight together); rows past
+    // the live ones load nothing
+    int slot = -1;
+    if ((threadIdx.x & 63) < BM) resolve_row(p, row0 + (threadIdx.x & 63), ntp, slot);
+    rt.slot = rt.e >= 0 && rt.e < p.E ? slot : -1;
     return rt;
 }
 
