@@ -243,12 +243,13 @@ def test_decode_1024_experts_1024_slots():
     assert maxrel(a.float().cpu().numpy(), ref) <= REL_TOL
 
 
-@pytest.mark.parametrize("T,frag,emap", [(160, False, False), (300, True, False),
-                                         (1024, True, True), (4096, True, False)])
+@pytest.mark.parametrize("T,frag,emap", [(100, True, False), (129, True, False), (160, False, False),
+                                         (300, True, False), (1024, True, True), (4096, True, False)])
 def test_prefill_pair_equals_two_launches(T, frag, emap):
     """gemm1+SiLU and gemm2 of each 64-row tile in one work-group (prefill_ares_pair_kernel,
     the default where both tiles apply) give the two launches' output bit for bit, with
-    partial tiles, an expert map that drops experts, and at the c4 size."""
+    partial tiles (T = 100 and 129: a few tiles, 800 and 1032 slots), an expert map that
+    drops experts, and at the c4 size."""
     cfg = dict(bench.CONFIGS["c4"])
     cfg["T"] = T
     ws = bench.make_weights(cfg, 470 + T, DEV)
