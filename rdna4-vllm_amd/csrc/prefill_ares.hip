@@ -21,7 +21,8 @@
 //   * per step and live 16-row fragment: v_mfma_f32_16x16x128_f8f6f4 on the raw-nibble B
 //     (n * 2^-9, two ANDs and a shift) with the operands swapped, so lane (q, c16) holds
 //     tile row c16, columns 4q..4q+3; then the fp32 scale fold run += acc * scale[n, g]
-//     (moe_gemm_tiled.h:144-151) with the lane's four scales read from a per-wave LDS table;
+//     (moe_gemm_tiled.h:144-151) with the lane's four scales read from a per-wave LDS table
+//     one step ahead of the fold that uses them;
 //   * the range's scales and zero-points are fetched one range ahead into registers (on
 //     fragment weights: the rows' metadata words stored after each 16-row tile's blocks); at
 //     a range boundary each wave writes the scale table and s*z (bf16 hi/lo) for its own 32
@@ -35,7 +36,11 @@
 //   * the two waves of a SIMD take turns at the higher issue priority, one range each, so
 //     neither ends a tile far behind the other;
 //   * the main loop is instantiated per live 16-row fragment count (1..4), so partial tiles
-//     run straight-line code without per-fragment branches.
+//     run straight-line code without per-fragment branches;
+//   * fp16 rows (gemm2 on h) are quantised by the tile itself in its prologue, four rows per
+//     wave at a time, bit-identical to act_quant_kernel; prefill_ares_pair_kernel takes
+//     each tile through gemm1+SiLU and then this gemm2 on the h rows it just wrote, both
+//     halves routed once.
 #include <algorithm>
 #include <type_traits>
 
