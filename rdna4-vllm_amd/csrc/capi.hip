@@ -816,6 +816,10 @@ int w4a8_mmq_fp8_gemm(const void* x_f16, int64_t M, int64_t K, const int32_t* w_
     a.block_m = 64;
     if (kernel == 0) { mk = W4A8_MOE_KERNEL_SCALAR; a.block_m = 1; }
     if (kernel == 11) { mk = W4A8_MOE_KERNEL_GEMV; a.block_m = 16; }
+    // a few rows: the dense GEMV (rows quantised in the kernel, no act-quant launch)
+    if (kernel == 11 && dense_gemv_supported(M, N, K, group_size, weight_is_e2m1 != 0))
+        return launch_dense_gemv(x_f16, M, K, w_packed, scales_f16, w_zeros, N, out_f16,
+                                 as_stream(stream));
     return run_grouped(a, mk, workspace, workspace_bytes, as_stream(stream));
 }
 

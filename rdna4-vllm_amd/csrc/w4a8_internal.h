@@ -172,6 +172,11 @@ struct GroupedArgs {
     float* act_group_sums;  // (x_rows, K/128) per-group sums of the e4m3 values, or null
 };
 
+// Dense GEMV for 1 <= M <= 16 rows of fp16 x on op-layout weights (dense_gemv.hip): group
+// 128, K a multiple of 1024 up to 4096, N % 16 == 0; quantises the rows itself.
+bool dense_gemv_supported(int64_t M, int64_t N, int64_t K, int64_t group_size, bool e2m1);
+int launch_dense_gemv(const void* x_f16, int64_t M, int64_t K, const int32_t* w, const void* scales_f16,
+                      const int32_t* zeros, int64_t N, void* out_f16, hipStream_t s);
 int launch_grouped_scalar(const GroupedArgs& a, hipStream_t stream);
 int launch_grouped_mfma(const GroupedArgs& a, hipStream_t stream);   // prefill tiles
 int launch_grouped_gemv(const GroupedArgs& a, hipStream_t stream);   // decode GEMV

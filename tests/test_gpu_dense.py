@@ -82,6 +82,29 @@ def test_dense_gemv_equals_tiles(M):
     assert float((a - b).abs().max() / b.abs().max()) <= 2e-3
 
 
+@pytest.mark.parametrize("M,N,K,asym", [(1, 16, 1024, True), (3, 384, 3072, True), (16, 1024, 1024, False),
+                                         (1, 4096, 4096, False), (7, 2048, 4096, True)])
+def test_dense_few_rows_vs_oracle(M, N, K, asym):
+    """1 <= M <= 16 rows take the dense GEMV (rows quantised in the kernel, K split over eight
+    waves): every split (one to four groups a wave), one column tile, symmetric and AWQ
+    weights, against the oracle and the MFMA tiles."""
+    r = np.random.default_rng(7200 + M + N + K)
+    g = 128
+    nib, zp, sc = make_weights(r, N, K, g, asym)
+    w = O.pack_nibbles(nib)
+    z = O.pack_zeros(zp) if asym else None
+    x = torch.randn(M, K, generator=torch.Generator().manual_seed(M + K)).to(torch.float16)
+    wd, sd = torch.from_numpy(w).to(DEV), torch.from_numpy(sc).to(DEV)
+    zd = torch.from_numpy(z).to(DEV) if asym else None
+    out = linear.w4a8_dense_apply(x.to(DEV), wd, sd, zd, None, None, None, N, K, g, asym,
+                                  0 if asym else 8, 0)
+    assert tuple(out.shape) == (M, N) and torch.isfinite(out.float()).all()
+    assert maxrel(out.cpu().numpy(), O.dense_gemm(x.numpy(), w, sc, z)) <= REL_TOL
+    from w4a8_fp8_wmma import mmq_fp8_gemm
+    b = mmq_fp8_gemm(x.to(DEV), wd, sd, kernel="prefill_wmma_ashuffle", w_zeros=zd).float()
+    assert float((out.float() - b).abs().max() / b.abs().max()) <= 2e-3
+
+
 def gptq_pack(nib):
     """(N, K) nibbles -> AutoGPTQ qweight (K/8, N): word [k8, n] holds k = 8 k8 + j of column
     n in nibble j (packed along K)."""
