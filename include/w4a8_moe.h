@@ -322,7 +322,7 @@ W4A8_API int w4a8_set_decode_fused(int on);
 /* Prefill pair switch: on != 0 (the default; W4A8_PREFILL_PAIR=0 in the environment, read
  * once, turns it off) lets the many-token schedule run gemm1+SiLU and gemm2 of the
  * activation-resident tiles as one launch where both apply (hidden size <= 2048,
- * intermediate size <= 1024): each work-group takes a 64-row tile through gemm1, then through
+ * intermediate size <= 1536): each work-group takes a 64-row tile through gemm1, then through
  * gemm2 on the h rows it has just written. Results are the same bits as the two launches.
  * Returns the previous setting. Process-wide. No reference counterpart (the reference runs
  * separate launches). */

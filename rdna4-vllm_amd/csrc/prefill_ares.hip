@@ -58,7 +58,7 @@ constexpr int kArBN = kArWaves * kArNT * 16;    // 256 weight rows per range
 constexpr int kArD = 4;                         // B steps in flight per wave
 constexpr int kArMaxK = 2048;                   // 64-row activation tile must fit LDS
 constexpr int kArMaxKWide = 4096;               // 32-row activation tile must fit LDS
-constexpr int kArMaxKAq = 1024;                 // fp16 rows quantised in the prologue
+constexpr int kArMaxKAq = 1536;                 // fp16 rows quantised in the prologue
 constexpr int kArGp = 16;                       // group slots of the per-range weight tables
 constexpr int kArXcds = 8;                      // work-groups go round-robin to 8 XCDs
 
@@ -387,7 +387,7 @@ __device__ __forceinline__ void ar_tile(const Params& p, const ArRoute& rt, int 
     if constexpr (self_quant) {
         // fp16 rows in (the tile owns its rows: each is read by this work-group only);
         // wave w quantises tile rows 8w .. 8w + 7 below
-        const int npass = K / 512;                      // 1 or 2 (K <= kArMaxKAq)
+        const int npass = K / 512;                      // 1 to 3 (K <= kArMaxKAq)
         const __half* xh = reinterpret_cast<const __half*>(p.xh);
 #pragma unroll
         for (int pp = 0; pp < 2; ++pp) {
@@ -877,7 +877,7 @@ bool prefill_ares_pair_supported(const GroupedArgs& a1, const GroupedArgs& a2) {
 int launch_grouped_prefill_ares_pair(const GroupedArgs& a1, const GroupedArgs& a2, hipStream_t s) {
     if (!prefill_ares_pair_supported(a1, a2)) {
         set_error("prefill (activation-resident pair): needs the gemm1+SiLU tile (K <= 2048, "
-                  "prequantised rows) and a self-quantising gemm2 tile (K <= 1024) on h, over the "
+                  "prequantised rows) and a self-quantising gemm2 tile (K <= 1536) on h, over the "
                   "same sorted rows");
         return W4A8_ERR_INVALID;
     }
@@ -905,7 +905,7 @@ int launch_grouped_prefill_ares(const GroupedArgs& a, hipStream_t s) {
     const Params p = make_params(a);
     if (p.P == 0) return W4A8_OK;
     // rows come prequantised (x_fp8 with scales and group sums), or, for fp16 output and
-    // K <= 1024, as fp16 rows the tile quantises itself
+    // K <= 1536, as fp16 rows the tile quantises itself
     const bool prequant = p.xq != nullptr && p.asum != nullptr && p.asc != nullptr;
     const bool self_quant = p.xq == nullptr && p.xh != nullptr && !a.x_bf16 &&
                             a.epi == Epi::kHalf && a.K <= kArMaxKAq;
@@ -914,7 +914,7 @@ int launch_grouped_prefill_ares(const GroupedArgs& a, hipStream_t s) {
         set_error("prefill (activation-resident): needs g128 int4 weights, K % 512 == 0 and "
                   "K <= 4096, output columns in whole 256-row ranges, block_m % 64 == 0 (32 for "
                   "K > 2048), fp16 out, and prequantised rows with group sums (or fp16 rows, fp16 "
-                  "out, K <= 1024)");
+                  "out, K <= 1536)");
         return W4A8_ERR_INVALID;
     }
     if (a.w_frag && (a.N % 16 != 0 || (a.epi == Epi::kSiluHalf && (a.N / 2) % 16 != 0))) {
