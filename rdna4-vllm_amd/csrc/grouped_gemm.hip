@@ -634,7 +634,7 @@ __global__ void __launch_bounds__(256, 2) grouped_gemv_kernel(Params p, int tpt)
             // the first weight chunks go out with the raw rows; the wait for the rows then
             // also covers those chunks, which were issued just before them
             issue(0, B0{});
-            issue(1, B1{});
+            if constexpr (GPW <= 4) issue(1, B1{});
             const uint16_t* xr = reinterpret_cast<const uint16_t*>(p.xh) + (int64_t)asrc * p.K + q * 32;
             const bool bf16 = p.xbf16;
             uint4 raw[GPW][4];   // 32 values of group g0 + u: k = 8i .. 8i+7 in raw[u][i]
@@ -675,20 +675,31 @@ __global__ void __launch_bounds__(256, 2) grouped_gemv_kernel(Params p, int tpt)
             }
             my_asc = act_scale_from_absmax(amax);
             const float inv = 1.0f / my_asc;
+            // one branch on the dtype around the whole conversion: a select per value
+            // becomes a uniform branch per value, and at eight groups a wave the values
+            // live across those joins spill
+            auto convert = [&](auto bfc) {
+                constexpr bool BF = decltype(bfc)::value;
 #pragma unroll
-            for (int u = 0; u < GPW; ++u)
+                for (int u = 0; u < GPW; ++u)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {   // k8-interleaved bytes, as act_quant_kernel
-                    const uint32_t w[4] = {raw[u][i].x, raw[u][i].y, raw[u][i].z, raw[u][i].w};
-                    float f[8];
+                    for (int i = 0; i < 4; ++i) {   // k8-interleaved bytes, as act_quant_kernel
+                        const uint32_t w[4] = {raw[u][i].x, raw[u][i].y, raw[u][i].z, raw[u][i].w};
+                        float f[8];
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        f[2 * j] = act_bits_to_f32(w[j] & 0xFFFFu, bf16) * inv;
-                        f[2 * j + 1] = act_bits_to_f32(w[j] >> 16, bf16) * inv;
+                        for (int j = 0; j < 4; ++j) {
+                            f[2 * j] = half_bits_to_f32<BF>(w[j] & 0xFFFFu) * inv;
+                            f[2 * j + 1] = half_bits_to_f32<BF>(w[j] >> 16) * inv;
+                        }
+                        af[u][2 * i] = (int)pack4_e4m3(f[0], f[2], f[4], f[6]);
+                        af[u][2 * i + 1] = (int)pack4_e4m3(f[1], f[3], f[5], f[7]);
                     }
-                    af[u][2 * i] = (int)pack4_e4m3(f[0], f[2], f[4], f[6]);
-                    af[u][2 * i + 1] = (int)pack4_e4m3(f[1], f[3], f[5], f[7]);
-                }
+            };
+            if (bf16) convert(std::true_type{});
+            else convert(std::false_type{});
+            // eight groups a wave: 128 VGPRs of rows leave no room for the second chunk
+            // until they are converted
+            if constexpr (GPW > 4) issue(1, B1{});
         }
         v4f sa[GPW];   // 2^-9 * group sums of rows 4q..4q+3
 #pragma unroll

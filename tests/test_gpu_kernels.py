@@ -344,10 +344,12 @@ def test_e2m1_fp4_tiles_equal_scalar(case):
 
 
 @pytest.mark.parametrize("case", [(32, 8, 512, 2048, 8, 16, 128), (24, 16, 256, 512, 4, 16, 128),
-                                  (9, 8, 384, 1024, 2, 32, 128), (40, 8, 256, 1536, 2, 64, 128)])
+                                  (9, 8, 384, 1024, 2, 32, 128), (40, 8, 256, 1536, 2, 64, 128),
+                                  (8, 8, 256, 4096, 2, 16, 128), (33, 16, 512, 4096, 8, 64, 128)])
 def test_gemv_in_kernel_quant_matches_prequant(case):
     """With no workspace the decode GEMV quantises its rows in registers; that path must give
-    the bytes act_quant gives, so both calls agree bit for bit."""
+    the bytes act_quant gives, so both calls agree bit for bit (K = 4096: eight groups a
+    wave, the second weight chunk issued after the conversion)."""
     from w4a8_fp8_wmma._lib import lib as L
     from w4a8_fp8_wmma._ops import _ptr, _stream, _workspace
     T, E, N, K, k, bm, g = case
