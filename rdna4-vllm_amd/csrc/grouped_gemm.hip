@@ -453,8 +453,8 @@ __device__ __forceinline__ float half_bits_to_f32(uint32_t bits) {
     }
 }
 
-// fp16 or bf16 bits -> f32 with the input dtype chosen at run time (no divergent callees,
-// so the raw row words stay in registers)
+// fp16 or bf16 bits -> f32 with the input dtype chosen at run time (a single value; loops
+// over many values branch on the dtype once and call half_bits_to_f32 instead)
 __device__ __forceinline__ float act_bits_to_f32(uint32_t bits, bool bf16) {
     return bf16 ? half_bits_to_f32<true>(bits) : half_bits_to_f32<false>(bits);
 }
@@ -631,8 +631,9 @@ __global__ void __launch_bounds__(256, 2) grouped_gemv_kernel(Params p, int tpt)
             issue(0, B0{});
             issue(1, B1{});
         } else {
-            // the first weight chunks go out with the raw rows; the wait for the rows then
-            // also covers those chunks, which were issued just before them
+            // the first weight chunks (at eight groups a wave, the first chunk only) go out
+            // with the raw rows; the wait for the rows then also covers them, as they were
+            // issued just before
             issue(0, B0{});
             if constexpr (GPW <= 4) issue(1, B1{});
             const uint16_t* xr = reinterpret_cast<const uint16_t*>(p.xh) + (int64_t)asrc * p.K + q * 32;
