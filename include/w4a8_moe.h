@@ -108,7 +108,10 @@ W4A8_API int w4a8_moe_align_block_size(const int32_t* topk_ids, int64_t numel, i
  * Grouped GEMM, padded sorted layout: out (P, N) fp16.
  * Replaces mmq_fp8_moe_gemm (bindings.cpp:178-228 -> moe_kernel.hip:1358-1392).
  * Row r with slot s = sorted_token_ids[r] < T*top_k (and r < ntp) gathers x[s/top_k];
- * other rows are not written.
+ * other rows are not written. The workspace (w4a8_moe_gemm_workspace_size) holds the
+ * quantised rows; with the GEMV kernel, int4 weights, group 128 and K / 128 one of
+ * 1, 2, 3, 4, 6, 8, 12, 16, 32 it may be NULL, and each work-group then quantises its block's rows itself (same bytes,
+ * no act-quant launch). Other calls without it return W4A8_ERR_WORKSPACE.
  */
 W4A8_API size_t w4a8_moe_gemm_workspace_size(int64_t x_rows, int64_t K);
 W4A8_API int w4a8_mmq_fp8_moe_gemm(const void* x_f16, int64_t T, int64_t K,
